@@ -1,0 +1,274 @@
+// capi.hip -- C ABI of the fused-MoE operator: argument checks, workspace layout,
+// the launch sequence and a small stage profiler.
+//
+// Replaces the host orchestration of the reference (solution/python/main.cpp:66-266):
+// there ~16 launches and ~20 torch allocations per call; here five launches on the
+// caller's stream over one caller-provided workspace, no host synchronisation and no
+// allocation:
+//   route    (T/4 workgroups)      -> topk ids / weights
+//   dispatch (1 workgroup)         -> expert offsets, row tiles, permutation, inverse map
+//   gemm1    (persistent)          -> bf16 SwiGLU rows   [N_a, 2048]
+//   gemm2    (persistent)          -> fp32 expert rows   [N_a, 7168]
+//   combine  (7 T workgroups)      -> bf16 output        [T, 7168]
+// The GEMM grids are sized from the host-known bound on the tile count; each
+// workgroup reads the real count written by dispatch and exits when it runs out.
+
+#include <stdio.h>
+#include <string.h>
+
+#include "moe_device.h"
+#include "moe_mi355.h"
+
+namespace moe {
+void launch_route(const float*, const uint16_t*, int, float, int*, float*, hipStream_t);
+bool launch_dispatch(const int*, const float*, int, int, int, int*, int*, int4*, int*, float*,
+                     int*, hipStream_t);
+int dispatch_max_tiles(int T, int tm);
+void launch_gemm1(const uint8_t*, const float*, int, const uint8_t*, const float*, const int4*,
+                  const int*, int, const int*, uint16_t*, hipStream_t);
+void launch_gemm2(const uint16_t*, const uint8_t*, const float*, const int4*, const int*, int,
+                  float*, hipStream_t);
+void launch_combine(const float*, const float*, const int*, int, uint16_t*, hipStream_t);
+void launch_e4m3_to_bf16(const uint8_t*, uint16_t*, int, hipStream_t);
+}  // namespace moe
+
+namespace {
+
+constexpr int kTileM = 64;              // rows per GEMM tile (4 MFMA column blocks)
+constexpr int32_t kMaxT = 1 << 20;      // keeps every row index inside int32
+
+thread_local char g_hip_error[256] = "";
+
+size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
+
+bool fill_layout(int32_t T, moe_mi355_workspace_layout* L) {
+    if (T < 0 || T > kMaxT) return false;
+    const size_t R = (size_t)T * moe::kTopK;
+    const int mt = moe::dispatch_max_tiles(T, kTileM);
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = off;
+        off = align_up(off + bytes);
+        return o;
+    };
+    L->topk_ids = take(R * 4);
+    L->topk_weights = take(R * 4);
+    L->inverse_rows = take(R * 4);
+    L->meta = take(64 * 4);
+    L->tiles = take((size_t)mt * 16);
+    L->sorted_tokens = take(R * 4);
+    L->sorted_weights = take(R * 4);
+    L->intermediate = take(R * moe::kI * 2);
+    L->expert_out = take(R * moe::kH * 4);
+    L->total = off;
+    L->tile_m = kTileM;
+    L->max_tiles = mt;
+    return true;
+}
+
+int hip_status(hipError_t e) {
+    if (e == hipSuccess) return MOE_OK;
+    snprintf(g_hip_error, sizeof g_hip_error, "%s (%d)", hipGetErrorString(e), (int)e);
+    return MOE_ERR_HIP;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int clamp_offset(int64_t off) {
+    if (off > (int64_t)(1 << 30)) return 1 << 30;
+    if (off < -(int64_t)(1 << 30)) return -(1 << 30);
+    return (int)off;
+}
+
+// ---- stage profiler ------------------------------------------------------------
+struct Profiler {
+    hipEvent_t* ev = nullptr;   // [slots][kNumStages + 1]
+    int slots = 0;
+    int used = 0;
+};
+Profiler g_prof;
+
+void prof_record(int slot, int stage, hipStream_t s) {
+    (void)hipEventRecord(g_prof.ev[slot * (MOE_MI355_NUM_STAGES + 1) + stage], s);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* moe_mi355_version(void) { return "moe_mi355 0.1 gfx950"; }
+
+const char* moe_mi355_last_hip_error(void) { return g_hip_error; }
+
+const char* moe_mi355_strerror(int status) {
+    switch (status) {
+        case MOE_OK: return "ok";
+        case MOE_ERR_NULL_POINTER: return "a required pointer is NULL";
+        case MOE_ERR_BAD_SIZE: return "token count out of range";
+        case MOE_ERR_WORKSPACE: return "workspace NULL, not 256-byte aligned, or too small";
+        case MOE_ERR_MISALIGNED: return "a tensor pointer is not 16-byte aligned";
+        case MOE_ERR_HIP: return "HIP launch failed";
+        case MOE_ERR_BAD_TILE: return "unsupported tile height";
+        default: return "unknown status";
+    }
+}
+
+int32_t moe_mi355_max_tiles(int32_t T, int32_t tile_m) {
+    if (T < 0 || tile_m <= 0) return 0;
+    return moe::dispatch_max_tiles(T, tile_m);
+}
+
+size_t moe_mi355_workspace_bytes(int32_t T) {
+    moe_mi355_workspace_layout L;
+    if (!fill_layout(T, &L)) return 0;
+    return L.total;
+}
+
+int moe_mi355_get_workspace_layout(int32_t T, moe_mi355_workspace_layout* out) {
+    if (!out) return MOE_ERR_NULL_POINTER;
+    if (!fill_layout(T, out)) return MOE_ERR_BAD_SIZE;
+    return MOE_OK;
+}
+
+int moe_mi355_route(const float* routing_logits, const uint16_t* routing_bias, int32_t T,
+                    double routed_scaling_factor, int32_t* topk_ids, float* topk_weights,
+                    void* stream) {
+    if (T < 0 || T > kMaxT) return MOE_ERR_BAD_SIZE;
+    if (T == 0) return MOE_OK;
+    if (!routing_logits || !routing_bias || !topk_ids || !topk_weights) return MOE_ERR_NULL_POINTER;
+    if (!aligned16(routing_logits) || ((uintptr_t)routing_bias & 7u)) return MOE_ERR_MISALIGNED;
+    hipStream_t s = (hipStream_t)stream;
+    moe::launch_route(routing_logits, routing_bias, T, (float)routed_scaling_factor, topk_ids,
+                      topk_weights, s);
+    return hip_status(hipGetLastError());
+}
+
+int moe_mi355_dispatch(const int32_t* topk_ids, const float* topk_weights, int32_t T,
+                       int64_t local_expert_offset, int32_t tile_m, int32_t* expert_offsets,
+                       int32_t* sorted_tokens, float* sorted_weights, int32_t* inverse_rows,
+                       int32_t* tiles, int32_t* num_tiles, void* stream) {
+    if (T < 0 || T > kMaxT) return MOE_ERR_BAD_SIZE;
+    if (tile_m != 16 && tile_m != 32 && tile_m != 64) return MOE_ERR_BAD_TILE;
+    if (!topk_ids || !topk_weights || !expert_offsets || !sorted_tokens || !sorted_weights ||
+        !inverse_rows || !tiles || !num_tiles)
+        return MOE_ERR_NULL_POINTER;
+    if (!aligned16(tiles)) return MOE_ERR_MISALIGNED;
+    hipStream_t s = (hipStream_t)stream;
+    moe::launch_dispatch(topk_ids, topk_weights, T, clamp_offset(local_expert_offset), tile_m,
+                         expert_offsets, num_tiles, reinterpret_cast<int4*>(tiles), sorted_tokens,
+                         sorted_weights, inverse_rows, s);
+    return hip_status(hipGetLastError());
+}
+
+int moe_mi355_forward(const moe_mi355_args* a, void* stream) {
+    if (!a) return MOE_ERR_NULL_POINTER;
+    const int32_t T = a->T;
+    moe_mi355_workspace_layout L;
+    if (!fill_layout(T, &L)) return MOE_ERR_BAD_SIZE;
+    if (T == 0) return MOE_OK;
+    if (!a->routing_logits || !a->routing_bias || !a->hidden_states || !a->hidden_states_scale ||
+        !a->gemm1_weights || !a->gemm1_weights_scale || !a->gemm2_weights ||
+        !a->gemm2_weights_scale || !a->output)
+        return MOE_ERR_NULL_POINTER;
+    if (!aligned16(a->routing_logits) || ((uintptr_t)a->routing_bias & 7u) ||
+        !aligned16(a->hidden_states) || ((uintptr_t)a->hidden_states_scale & 3u) ||
+        !aligned16(a->gemm1_weights) || ((uintptr_t)a->gemm1_weights_scale & 3u) ||
+        !aligned16(a->gemm2_weights) || ((uintptr_t)a->gemm2_weights_scale & 3u) ||
+        !aligned16(a->output))
+        return MOE_ERR_MISALIGNED;
+    if (!a->workspace || ((uintptr_t)a->workspace & 255u) || a->workspace_bytes < L.total)
+        return MOE_ERR_WORKSPACE;
+
+    hipStream_t s = (hipStream_t)stream;
+    uint8_t* ws = static_cast<uint8_t*>(a->workspace);
+    int* ids = reinterpret_cast<int*>(ws + L.topk_ids);
+    float* wts = reinterpret_cast<float*>(ws + L.topk_weights);
+    int* inv = reinterpret_cast<int*>(ws + L.inverse_rows);
+    int* meta = reinterpret_cast<int*>(ws + L.meta);
+    int4* tiles = reinterpret_cast<int4*>(ws + L.tiles);
+    int* stok = reinterpret_cast<int*>(ws + L.sorted_tokens);
+    float* sw = reinterpret_cast<float*>(ws + L.sorted_weights);
+    uint16_t* inter = reinterpret_cast<uint16_t*>(ws + L.intermediate);
+    float* rows = reinterpret_cast<float*>(ws + L.expert_out);
+    int* num_tiles = meta + moe::kEL + 1;
+
+    const bool prof = (a->flags & MOE_MI355_FLAG_PROFILE) && g_prof.ev && g_prof.used < g_prof.slots;
+    const int slot = prof ? g_prof.used++ : 0;
+
+    if (prof) prof_record(slot, 0, s);
+    moe::launch_route(a->routing_logits, a->routing_bias, T, (float)a->routed_scaling_factor, ids,
+                      wts, s);
+    if (prof) prof_record(slot, 1, s);
+    moe::launch_dispatch(ids, wts, T, clamp_offset(a->local_expert_offset), L.tile_m, meta,
+                         num_tiles, tiles, stok, sw, inv, s);
+    if (prof) prof_record(slot, 2, s);
+    moe::launch_gemm1(a->hidden_states, a->hidden_states_scale, T, a->gemm1_weights,
+                      a->gemm1_weights_scale, tiles, num_tiles, L.max_tiles, stok, inter, s);
+    if (prof) prof_record(slot, 3, s);
+    moe::launch_gemm2(inter, a->gemm2_weights, a->gemm2_weights_scale, tiles, num_tiles,
+                      L.max_tiles, rows, s);
+    if (prof) prof_record(slot, 4, s);
+    moe::launch_combine(rows, sw, inv, T, a->output, s);
+    if (prof) prof_record(slot, 5, s);
+    return hip_status(hipGetLastError());
+}
+
+int moe_mi355_profile_begin(int32_t max_calls) {
+    moe_mi355_profile_end();
+    if (max_calls <= 0) return MOE_ERR_BAD_SIZE;
+    const int n = max_calls * (MOE_MI355_NUM_STAGES + 1);
+    g_prof.ev = new hipEvent_t[n];
+    for (int i = 0; i < n; ++i) {
+        const hipError_t e = hipEventCreate(&g_prof.ev[i]);
+        if (e != hipSuccess) {
+            for (int j = 0; j < i; ++j) (void)hipEventDestroy(g_prof.ev[j]);
+            delete[] g_prof.ev;
+            g_prof.ev = nullptr;
+            return hip_status(e);
+        }
+    }
+    g_prof.slots = max_calls;
+    g_prof.used = 0;
+    return MOE_OK;
+}
+
+int moe_mi355_profile_read(float* stage_ms, int32_t n) {
+    if (!stage_ms) return MOE_ERR_NULL_POINTER;
+    if (!g_prof.ev || g_prof.used == 0) return 0;
+    const int ns = MOE_MI355_NUM_STAGES;
+    double sum[MOE_MI355_NUM_STAGES] = {0};
+    for (int c = 0; c < g_prof.used; ++c) {
+        hipEvent_t* ev = g_prof.ev + c * (ns + 1);
+        const hipError_t e = hipEventSynchronize(ev[ns]);
+        if (e != hipSuccess) return hip_status(e);
+        for (int st = 0; st < ns; ++st) {
+            float ms = 0.f;
+            const hipError_t e2 = hipEventElapsedTime(&ms, ev[st], ev[st + 1]);
+            if (e2 != hipSuccess) return hip_status(e2);
+            sum[st] += ms;
+        }
+    }
+    for (int st = 0; st < ns && st < n; ++st) stage_ms[st] = (float)(sum[st] / g_prof.used);
+    return g_prof.used;
+}
+
+int moe_mi355_profile_end(void) {
+    if (g_prof.ev) {
+        for (int i = 0; i < g_prof.slots * (MOE_MI355_NUM_STAGES + 1); ++i)
+            (void)hipEventDestroy(g_prof.ev[i]);
+        delete[] g_prof.ev;
+    }
+    g_prof.ev = nullptr;
+    g_prof.slots = 0;
+    g_prof.used = 0;
+    return MOE_OK;
+}
+
+int moe_mi355_debug_e4m3_to_bf16(const uint8_t* in, uint16_t* out, int32_t n, void* stream) {
+    if (!in || !out) return MOE_ERR_NULL_POINTER;
+    if (n < 0 || (n & 3)) return MOE_ERR_BAD_SIZE;
+    moe::launch_e4m3_to_bf16(in, out, n, (hipStream_t)stream);
+    return hip_status(hipGetLastError());
+}
+
+}  // extern "C"

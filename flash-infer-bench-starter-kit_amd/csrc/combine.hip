@@ -1,0 +1,83 @@
+// combine.hip -- routing-weighted combine of the expert rows into the bf16 output.
+//
+// Semantics: reference solution/cuda/moe.cu:210, 233-239: acc starts at 0, each local
+// expert in ascending order adds round(O * w) into the fp32 accumulator, then one
+// bf16 round-to-nearest-even.  The reference's live kernels do this with a gather
+// over the inverse slot map (finalize_weighted_bf16_kernel, kernel.cu:809-839) or
+// with bf16 atomics (kernel.cu:431-455); here it is a gather with a fixed order and
+// no atomics, so the output is identical run to run.
+//
+// Rows of one token are visited in ascending row index, which is ascending local
+// expert because the permutation is expert-major.  Tokens with no local expert get
+// +0.0.  One thread produces 8 consecutive outputs (one 16-byte store).
+
+#include "moe_device.h"
+
+namespace moe {
+
+#pragma clang fp contract(off)
+
+__device__ __forceinline__ void cswap(int& a, int& b) {
+    const int x = min(a, b), y = max(a, b);
+    a = x;
+    b = y;
+}
+
+__global__ __launch_bounds__(128) void combine_kernel(const float* __restrict__ rows_out,
+                                                      const float* __restrict__ sorted_w,
+                                                      const int* __restrict__ inv, int T,
+                                                      uint16_t* __restrict__ out) {
+    constexpr int kParts = kH / (128 * 8);  // 7 blocks of 128 threads per token
+    const int t = blockIdx.x / kParts;
+    const int h0 = ((blockIdx.x % kParts) * 128 + threadIdx.x) * 8;
+    if (t >= T) return;
+
+    int r[kTopK];
+#pragma unroll
+    for (int k = 0; k < kTopK; ++k) {
+        const int v = inv[(size_t)t * kTopK + k];
+        r[k] = v < 0 ? 0x7fffffff : v;
+    }
+    // 8-input sorting network (19 compare-exchanges)
+    cswap(r[0], r[1]); cswap(r[2], r[3]); cswap(r[4], r[5]); cswap(r[6], r[7]);
+    cswap(r[0], r[2]); cswap(r[1], r[3]); cswap(r[4], r[6]); cswap(r[5], r[7]);
+    cswap(r[1], r[2]); cswap(r[5], r[6]); cswap(r[0], r[4]); cswap(r[3], r[7]);
+    cswap(r[1], r[5]); cswap(r[2], r[6]);
+    cswap(r[1], r[4]); cswap(r[3], r[6]);
+    cswap(r[2], r[4]); cswap(r[3], r[5]);
+    cswap(r[3], r[4]);
+
+    float acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kTopK; ++k) {
+        if (r[k] != 0x7fffffff) {
+            const float w = sorted_w[r[k]];
+            const float4* p = reinterpret_cast<const float4*>(rows_out + (size_t)r[k] * kH + h0);
+            const float4 a = p[0], b = p[1];
+            const float o[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float prod = o[j] * w;
+                acc[j] = acc[j] + prod;
+            }
+        }
+    }
+    uint4 pk;
+    pk.x = f32_to_bf16_bits(acc[0]) | (f32_to_bf16_bits(acc[1]) << 16);
+    pk.y = f32_to_bf16_bits(acc[2]) | (f32_to_bf16_bits(acc[3]) << 16);
+    pk.z = f32_to_bf16_bits(acc[4]) | (f32_to_bf16_bits(acc[5]) << 16);
+    pk.w = f32_to_bf16_bits(acc[6]) | (f32_to_bf16_bits(acc[7]) << 16);
+    *reinterpret_cast<uint4*>(out + (size_t)t * kH + h0) = pk;
+}
+
+void launch_combine(const float* rows_out, const float* sorted_w, const int* inv, int T,
+                    uint16_t* out, hipStream_t stream) {
+    if (T <= 0) return;
+    constexpr int kParts = kH / (128 * 8);
+    hipLaunchKernelGGL(combine_kernel, dim3((unsigned)T * kParts), dim3(128), 0, stream, rows_out,
+                       sorted_w, inv, T, out);
+}
+
+}  // namespace moe

@@ -1,0 +1,316 @@
+"""MI355X (gfx950) fused-MoE operator -- drop-in for the contest solution entry point.
+
+Definition : moe_fp8_block_scale_ds_routing_topk8_ng8_kg4_e32_h7168_i2048
+Language   : python  (loads the prebuilt HIP library ``libmoe_mi355.so`` via ctypes)
+DPS        : true    (output pre-allocated bfloat16 [T, H], passed as last arg)
+Entry      : kernel.py::kernel
+
+Same signature, argument meaning and destination-passing contract as the
+reference's ``solution/python/kernel.py:95-120``; the work behind it is the C ABI of
+``include/moe_mi355.h`` (route -> dispatch -> FP8 GEMM1 + SwiGLU -> bf16 GEMM2 ->
+ordered combine, all on the caller's current stream, no host synchronisation).
+
+The reference JIT-compiles its extension on first use (kernel.py:57-92); this one
+is compiled ahead of time by ``build.py`` into this directory.  When the library is
+missing, ``kernel`` raises -- there is no CPU or PyTorch fallback.  Set
+``MOE_MI355_JIT=1`` to let the first call compile it with hipcc instead.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+H, I, E_GLOBAL, E_LOCAL, TOP_K, BLK = 7168, 2048, 256, 32, 8, 128
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libmoe_mi355.so")
+
+_lib = None  # cached ctypes handle (the reference caches its module in `_mod`)
+_lock = threading.Lock()
+
+
+class MoeArgs(ctypes.Structure):
+    """``moe_mi355_args`` of include/moe_mi355.h."""
+    _fields_ = [
+        ("routing_logits", ctypes.c_void_p),
+        ("routing_bias", ctypes.c_void_p),
+        ("hidden_states", ctypes.c_void_p),
+        ("hidden_states_scale", ctypes.c_void_p),
+        ("gemm1_weights", ctypes.c_void_p),
+        ("gemm1_weights_scale", ctypes.c_void_p),
+        ("gemm2_weights", ctypes.c_void_p),
+        ("gemm2_weights_scale", ctypes.c_void_p),
+        ("local_expert_offset", ctypes.c_int64),
+        ("routed_scaling_factor", ctypes.c_double),
+        ("output", ctypes.c_void_p),
+        ("T", ctypes.c_int32),
+        ("flags", ctypes.c_int32),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
+class WorkspaceLayout(ctypes.Structure):
+    """``moe_mi355_workspace_layout`` of include/moe_mi355.h."""
+    _fields_ = [(n, ctypes.c_size_t) for n in (
+        "topk_ids", "topk_weights", "inverse_rows", "meta", "tiles", "sorted_tokens",
+        "sorted_weights", "intermediate", "expert_out", "total")] + [
+        ("tile_m", ctypes.c_int32), ("max_tiles", ctypes.c_int32)]
+
+
+FLAG_PROFILE = 1
+NUM_STAGES = 5
+STAGES = ("route", "dispatch", "gemm1", "gemm2", "combine")
+
+
+def _declare(L: ctypes.CDLL) -> ctypes.CDLL:
+    P, I32, I64, SZ, D = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t, ctypes.c_double
+    sig = {
+        "moe_mi355_workspace_bytes": (SZ, [I32]),
+        "moe_mi355_forward": (ctypes.c_int, [ctypes.POINTER(MoeArgs), P]),
+        "moe_mi355_route": (ctypes.c_int, [P, P, I32, D, P, P, P]),
+        "moe_mi355_dispatch": (ctypes.c_int, [P, P, I32, I64, I32, P, P, P, P, P, P, P]),
+        "moe_mi355_max_tiles": (I32, [I32, I32]),
+        "moe_mi355_get_workspace_layout": (ctypes.c_int, [I32, ctypes.POINTER(WorkspaceLayout)]),
+        "moe_mi355_profile_begin": (ctypes.c_int, [I32]),
+        "moe_mi355_profile_read": (ctypes.c_int, [P, I32]),
+        "moe_mi355_profile_end": (ctypes.c_int, []),
+        "moe_mi355_debug_e4m3_to_bf16": (ctypes.c_int, [P, P, I32, P]),
+        "moe_mi355_strerror": (ctypes.c_char_p, [ctypes.c_int]),
+        "moe_mi355_last_hip_error": (ctypes.c_char_p, []),
+        "moe_mi355_version": (ctypes.c_char_p, []),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    return L
+
+
+def _build_extension() -> ctypes.CDLL:
+    """Load (or, with MOE_MI355_JIT=1, first compile) the HIP library."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(_LIB_PATH):
+            if os.environ.get("MOE_MI355_JIT") == "1":
+                import importlib.util
+                spec = importlib.util.spec_from_file_location("_moe_mi355_build", os.path.join(_HERE, "build.py"))
+                mod = importlib.util.module_from_spec(spec)
+                spec.loader.exec_module(mod)
+                mod.build(verbose=False)
+            else:
+                raise RuntimeError(
+                    f"{_LIB_PATH} is not built; run `python {os.path.join(_HERE, 'build.py')}` "
+                    "(or set MOE_MI355_JIT=1). There is no fallback path.")
+        _lib = _declare(ctypes.CDLL(_LIB_PATH))
+    return _lib
+
+
+def library_path() -> str:
+    return _LIB_PATH
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        L = _build_extension()
+        msg = L.moe_mi355_strerror(rc).decode()
+        hip = L.moe_mi355_last_hip_error().decode()
+        raise RuntimeError(f"{what} failed: {msg} ({rc}){': ' + hip if hip and rc == -5 else ''}")
+
+
+def _expect(t, name, dtype, shape):
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must have dtype {dtype}, got {t.dtype}")
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} must have shape {tuple(shape)}, got {tuple(t.shape)}")
+
+
+def _stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def workspace_bytes(T: int) -> int:
+    return int(_build_extension().moe_mi355_workspace_bytes(int(T)))
+
+
+def workspace_layout(T: int) -> WorkspaceLayout:
+    L = _build_extension()
+    lay = WorkspaceLayout()
+    _check(L.moe_mi355_get_workspace_layout(int(T), ctypes.byref(lay)), "moe_mi355_get_workspace_layout")
+    return lay
+
+
+def validate(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+             gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset,
+             routed_scaling_factor, output):
+    """Argument checks (the reference's TORCH_CHECKs, main.cpp:79, and the shapes of
+    kernel.py:96-106).  Returns (T, logits, hs_scale) with logits / hs_scale made
+    contiguous as main.cpp:91,182 does."""
+    if not isinstance(routing_logits, torch.Tensor) or routing_logits.dim() != 2:
+        raise ValueError("routing_logits must be a 2-D tensor [T, 256]")
+    T = int(routing_logits.shape[0])
+    dev = routing_logits.device
+    tensors = (
+        (routing_logits, "routing_logits", torch.float32, (T, E_GLOBAL)),
+        (routing_bias, "routing_bias", torch.bfloat16, (E_GLOBAL,)),
+        (hidden_states, "hidden_states", torch.float8_e4m3fn, (T, H)),
+        (hidden_states_scale, "hidden_states_scale", torch.float32, (H // BLK, T)),
+        (gemm1_weights, "gemm1_weights", torch.float8_e4m3fn, (E_LOCAL, 2 * I, H)),
+        (gemm1_weights_scale, "gemm1_weights_scale", torch.float32, (E_LOCAL, 2 * I // BLK, H // BLK)),
+        (gemm2_weights, "gemm2_weights", torch.float8_e4m3fn, (E_LOCAL, H, I)),
+        (gemm2_weights_scale, "gemm2_weights_scale", torch.float32, (E_LOCAL, H // BLK, I // BLK)),
+        (output, "output", torch.bfloat16, (T, H)),
+    )
+    for t, name, dtype, shape in tensors:
+        _expect(t, name, dtype, shape)
+    for t, name, _, _ in tensors:
+        if not t.is_cuda:
+            raise ValueError(f"{name} must be a GPU tensor")
+        if t.device != dev:
+            raise ValueError(f"{name} is on {t.device}, expected {dev}")
+    try:
+        int(local_expert_offset)
+        float(routed_scaling_factor)
+    except (TypeError, ValueError) as e:
+        raise TypeError("local_expert_offset must be an int and routed_scaling_factor a float") from e
+    for name, t in (("routing_bias", routing_bias), ("hidden_states", hidden_states),
+                    ("gemm1_weights", gemm1_weights), ("gemm1_weights_scale", gemm1_weights_scale),
+                    ("gemm2_weights", gemm2_weights), ("gemm2_weights_scale", gemm2_weights_scale),
+                    ("output", output)):
+        if not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+    return T, routing_logits.contiguous(), hidden_states_scale.contiguous()
+
+
+def kernel(
+    routing_logits,        # [T, 256]          float32
+    routing_bias,          # [256]             bfloat16
+    hidden_states,         # [T, 7168]         fp8_e4m3fn
+    hidden_states_scale,   # [56, T]           float32
+    gemm1_weights,         # [32, 4096, 7168]  fp8_e4m3fn
+    gemm1_weights_scale,   # [32, 32, 56]      float32
+    gemm2_weights,         # [32, 7168, 2048]  fp8_e4m3fn
+    gemm2_weights_scale,   # [32, 56, 16]      float32
+    local_expert_offset,   # int
+    routed_scaling_factor, # float
+    output,                # [T, 7168]         bfloat16 (DPS, pre-allocated)
+    *,
+    workspace: torch.Tensor | None = None,
+    flags: int = 0,
+):
+    """MoE forward pass on gfx950 HIP kernels; writes ``output`` in place, returns None.
+
+    ``workspace`` (keyword-only, optional) lets a caller supply and later inspect
+    the uint8 scratch buffer (>= workspace_bytes(T), 256-byte aligned); by default
+    one is taken from the caching allocator on the current stream."""
+    L = _build_extension()
+    T, logits, hs_scale = validate(routing_logits, routing_bias, hidden_states,
+                                   hidden_states_scale, gemm1_weights, gemm1_weights_scale,
+                                   gemm2_weights, gemm2_weights_scale, local_expert_offset,
+                                   routed_scaling_factor, output)
+    if T == 0:
+        return None
+    dev = routing_logits.device
+    need = int(L.moe_mi355_workspace_bytes(T))
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    elif workspace.numel() * workspace.element_size() < need or workspace.device != dev:
+        raise ValueError(f"workspace must hold >= {need} bytes on {dev}")
+    a = MoeArgs(
+        routing_logits=logits.data_ptr(),
+        routing_bias=routing_bias.data_ptr(),
+        hidden_states=hidden_states.data_ptr(),
+        hidden_states_scale=hs_scale.data_ptr(),
+        gemm1_weights=gemm1_weights.data_ptr(),
+        gemm1_weights_scale=gemm1_weights_scale.data_ptr(),
+        gemm2_weights=gemm2_weights.data_ptr(),
+        gemm2_weights_scale=gemm2_weights_scale.data_ptr(),
+        local_expert_offset=int(local_expert_offset),
+        routed_scaling_factor=float(routed_scaling_factor),
+        output=output.data_ptr(),
+        T=T,
+        flags=int(flags),
+        workspace=workspace.data_ptr(),
+        workspace_bytes=workspace.numel() * workspace.element_size(),
+    )
+    with torch.cuda.device(dev):
+        rc = L.moe_mi355_forward(ctypes.byref(a), ctypes.c_void_p(_stream_ptr(dev)))
+    _check(rc, "moe_mi355_forward")
+    return None
+
+
+# --------------------------------------------------------------------------- #
+# sub-step entry points (routing / dispatch) for callers and parity tests     #
+# --------------------------------------------------------------------------- #
+
+def route(routing_logits: torch.Tensor, routing_bias: torch.Tensor, routed_scaling_factor: float):
+    """Routing only: returns (topk_ids int32 [T,8], topk_weights fp32 [T,8])."""
+    L = _build_extension()
+    if routing_logits.dtype != torch.float32 or routing_logits.dim() != 2 or routing_logits.shape[1] != E_GLOBAL:
+        raise ValueError("routing_logits must be float32 [T, 256]")
+    if routing_bias.dtype != torch.bfloat16 or tuple(routing_bias.shape) != (E_GLOBAL,):
+        raise ValueError("routing_bias must be bfloat16 [256]")
+    dev = routing_logits.device
+    T = routing_logits.shape[0]
+    lg = routing_logits.contiguous()
+    ids = torch.empty(T, TOP_K, dtype=torch.int32, device=dev)
+    w = torch.empty(T, TOP_K, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        rc = L.moe_mi355_route(lg.data_ptr(), routing_bias.contiguous().data_ptr(), T,
+                               float(routed_scaling_factor), ids.data_ptr(), w.data_ptr(),
+                               ctypes.c_void_p(_stream_ptr(dev)))
+    _check(rc, "moe_mi355_route")
+    return ids, w
+
+
+def dispatch(topk_ids: torch.Tensor, topk_weights: torch.Tensor, local_expert_offset: int,
+             tile_m: int = 64) -> dict:
+    """Dispatch only: the canonical permutation (see include/moe_mi355.h)."""
+    L = _build_extension()
+    dev = topk_ids.device
+    T = topk_ids.shape[0]
+    ids = topk_ids.to(torch.int32).contiguous()
+    w = topk_weights.to(torch.float32).contiguous()
+    mt = int(L.moe_mi355_max_tiles(T, tile_m))
+    R = max(1, T * TOP_K)
+    out = dict(
+        exp_off=torch.empty(E_LOCAL + 1, dtype=torch.int32, device=dev),
+        sorted_tok=torch.empty(R, dtype=torch.int32, device=dev),
+        sorted_w=torch.empty(R, dtype=torch.float32, device=dev),
+        inv=torch.empty(T, TOP_K, dtype=torch.int32, device=dev),
+        tiles=torch.empty(max(1, mt), 4, dtype=torch.int32, device=dev),
+        num_tiles=torch.empty(1, dtype=torch.int32, device=dev),
+    )
+    with torch.cuda.device(dev):
+        rc = L.moe_mi355_dispatch(ids.data_ptr(), w.data_ptr(), T, int(local_expert_offset),
+                                  int(tile_m), out["exp_off"].data_ptr(),
+                                  out["sorted_tok"].data_ptr(), out["sorted_w"].data_ptr(),
+                                  out["inv"].data_ptr(), out["tiles"].data_ptr(),
+                                  out["num_tiles"].data_ptr(), ctypes.c_void_p(_stream_ptr(dev)))
+    _check(rc, "moe_mi355_dispatch")
+    return out
+
+
+def profile_begin(max_calls: int) -> None:
+    _check(_build_extension().moe_mi355_profile_begin(int(max_calls)), "moe_mi355_profile_begin")
+
+
+def profile_read() -> tuple[int, list[float]]:
+    """(calls averaged, average ms per stage in STAGES order)."""
+    buf = (ctypes.c_float * NUM_STAGES)()
+    n = _build_extension().moe_mi355_profile_read(buf, NUM_STAGES)
+    if n < 0:
+        _check(n, "moe_mi355_profile_read")
+    return n, [float(x) for x in buf]
+
+
+def profile_end() -> None:
+    _build_extension().moe_mi355_profile_end()

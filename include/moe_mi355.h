@@ -1,0 +1,172 @@
+/*
+ * moe_mi355.h -- C ABI of the MI355X (gfx950) fused-MoE operator
+ *   moe_fp8_block_scale_ds_routing_topk8_ng8_kg4_e32_h7168_i2048
+ *
+ * Plain pointers and sizes only: every tensor argument is a device pointer the
+ * caller owns, laid out exactly like the reference's torch tensors (row-major,
+ * contiguous).  All work is enqueued on `stream` (a hipStream_t, 0 = null stream);
+ * nothing synchronises the host.  Functions return MOE_OK (0) or a negative
+ * moe_mi355_status; moe_mi355_strerror() names it.
+ *
+ * Reference interfaces replaced (paths under the reference repository):
+ *   moe_mi355_forward   <- solution/python/main.cpp:66-266  run(...) (pybind `run`,
+ *                          main.cpp:268-270) behind kernel.py:95-120 kernel(...)
+ *   moe_mi355_route     <- solution/python/kernel.h:39-48 launch_noaux_routing_topk8
+ *                          (kernel.cu:56-200)
+ *   moe_mi355_dispatch  <- solution/python/kernel.h launch_compute_offsets +
+ *                          launch_fill_local_assignments_with_inverse +
+ *                          launch_build_padded_arrays (kernel.cu:503-547, 321-351,
+ *                          676-757), main.cpp:98-161
+ *   moe_mi355_workspace_bytes <- the ~20 per-call torch temporaries of
+ *                          main.cpp:87-231, replaced by one caller-provided buffer
+ */
+#ifndef MOE_MI355_H_
+#define MOE_MI355_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#if defined(__GNUC__)
+#define MOE_MI355_API __attribute__((visibility("default")))
+#else
+#define MOE_MI355_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Fixed geometry (reference solution/python/kernel.h:9-25). */
+#define MOE_MI355_HIDDEN 7168
+#define MOE_MI355_INTERMEDIATE 2048
+#define MOE_MI355_EXPERTS_GLOBAL 256
+#define MOE_MI355_EXPERTS_LOCAL 32
+#define MOE_MI355_TOP_K 8
+#define MOE_MI355_N_GROUP 8
+#define MOE_MI355_TOPK_GROUP 4
+#define MOE_MI355_BLOCK 128
+
+typedef enum moe_mi355_status {
+    MOE_OK = 0,
+    MOE_ERR_NULL_POINTER = -1,     /* a required pointer is NULL */
+    MOE_ERR_BAD_SIZE = -2,         /* T < 0 or T too large for 32-bit row indices */
+    MOE_ERR_WORKSPACE = -3,        /* workspace NULL, misaligned or too small */
+    MOE_ERR_MISALIGNED = -4,       /* a tensor pointer is not 16-byte aligned */
+    MOE_ERR_HIP = -5,              /* a HIP launch failed (see moe_mi355_last_hip_error) */
+    MOE_ERR_BAD_TILE = -6          /* tile_m not supported */
+} moe_mi355_status;
+
+/* Arguments of one forward call.  Mirrors kernel.py:95-107 / main.cpp:66-77:
+ *   routing_logits       fp32   [T, 256]
+ *   routing_bias         bf16   [256]                (raw bf16 bits)
+ *   hidden_states        e4m3fn [T, 7168]            (raw bytes)
+ *   hidden_states_scale  fp32   [56, T]              (note: block-major)
+ *   gemm1_weights        e4m3fn [32, 4096, 7168]
+ *   gemm1_weights_scale  fp32   [32, 32, 56]
+ *   gemm2_weights        e4m3fn [32, 7168, 2048]
+ *   gemm2_weights_scale  fp32   [32, 56, 16]
+ *   local_expert_offset  global id of local expert 0 (experts outside [0,256) are
+ *                        never selected, as in moe.cu:213-214)
+ *   routed_scaling_factor  multiplies the normalised weights (cast to fp32)
+ *   output               bf16   [T, 7168]            fully overwritten (DPS)
+ *   workspace            device buffer of >= moe_mi355_workspace_bytes(T) bytes,
+ *                        256-byte aligned; contents need no initialisation */
+typedef struct moe_mi355_args {
+    const float* routing_logits;
+    const uint16_t* routing_bias;
+    const uint8_t* hidden_states;
+    const float* hidden_states_scale;
+    const uint8_t* gemm1_weights;
+    const float* gemm1_weights_scale;
+    const uint8_t* gemm2_weights;
+    const float* gemm2_weights_scale;
+    int64_t local_expert_offset;
+    double routed_scaling_factor;
+    uint16_t* output;
+    int32_t T;
+    int32_t flags;      /* MOE_MI355_FLAG_* */
+    void* workspace;
+    size_t workspace_bytes;
+} moe_mi355_args;
+
+/* Record per-stage HIP events for the profiler (moe_mi355_profile_*). */
+#define MOE_MI355_FLAG_PROFILE 1
+
+/* Bytes of workspace a forward call over T tokens needs. */
+MOE_MI355_API size_t moe_mi355_workspace_bytes(int32_t T);
+
+/* The whole operator: routing -> dispatch -> GEMM1+SwiGLU -> GEMM2 -> combine.
+ * Replaces main.cpp:66-266 run(). */
+MOE_MI355_API int moe_mi355_forward(const moe_mi355_args* args, void* stream);
+
+/* Routing only (kernel.cu:56-200): topk_ids int32 [T,8], topk_weights fp32 [T,8],
+ * ids in selection order (score desc, index asc).  routing_bias is bf16 bits. */
+MOE_MI355_API int moe_mi355_route(const float* routing_logits, const uint16_t* routing_bias, int32_t T,
+                    double routed_scaling_factor, int32_t* topk_ids, float* topk_weights,
+                    void* stream);
+
+/* Dispatch only (kernel.cu:503-547, 321-351): from topk ids/weights build the
+ * canonical (local expert asc, token asc) permutation.
+ *   expert_offsets int32 [33]   exclusive scan of per-expert counts ([32] = N_a)
+ *   sorted_tokens  int32 [8T]   token of row r (rows >= N_a untouched)
+ *   sorted_weights fp32  [8T]   routing weight of row r
+ *   inverse_rows   int32 [T,8]  row of assignment (t,k) or -1 if not local
+ *   tiles          int32 [moe_mi355_max_tiles(T,tile_m), 4]  (expert, first row,
+ *                               rows, 0) per tile of <= tile_m rows
+ *   num_tiles      int32 [1]
+ * tile_m must be 16, 32 or 64. */
+MOE_MI355_API int moe_mi355_dispatch(const int32_t* topk_ids, const float* topk_weights, int32_t T,
+                       int64_t local_expert_offset, int32_t tile_m,
+                       int32_t* expert_offsets, int32_t* sorted_tokens,
+                       float* sorted_weights, int32_t* inverse_rows, int32_t* tiles,
+                       int32_t* num_tiles, void* stream);
+
+/* Upper bound on the number of row tiles for T tokens and tile height tile_m. */
+MOE_MI355_API int32_t moe_mi355_max_tiles(int32_t T, int32_t tile_m);
+
+/* Where a forward call keeps its intermediate arrays inside the workspace (byte
+ * offsets), so a caller can inspect routing and dispatch results after the call. */
+typedef struct moe_mi355_workspace_layout {
+    size_t topk_ids;        /* int32 [T,8] */
+    size_t topk_weights;    /* fp32  [T,8] */
+    size_t inverse_rows;    /* int32 [T,8] */
+    size_t meta;            /* int32 [64]: [0..32] expert offsets, [33] num tiles */
+    size_t tiles;           /* int32 [max_tiles,4] */
+    size_t sorted_tokens;   /* int32 [8T] */
+    size_t sorted_weights;  /* fp32  [8T] */
+    size_t intermediate;    /* bf16  [8T, 2048]  SwiGLU output rows */
+    size_t expert_out;      /* fp32  [8T, 7168]  GEMM2 output rows */
+    size_t total;
+    int32_t tile_m;
+    int32_t max_tiles;
+} moe_mi355_workspace_layout;
+
+MOE_MI355_API int moe_mi355_get_workspace_layout(int32_t T, moe_mi355_workspace_layout* out);
+
+/* Stage profiler: with MOE_MI355_FLAG_PROFILE set, each forward call records HIP
+ * events around each of its kernels into a ring of `max_calls` slots.
+ * moe_mi355_profile_read synchronises those events and writes the average
+ * duration in milliseconds of each stage over the recorded calls into
+ * stage_ms[0..n) (stage order: route, dispatch, gemm1, gemm2, combine) and
+ * returns the number of calls averaged. */
+MOE_MI355_API int moe_mi355_profile_begin(int32_t max_calls);
+MOE_MI355_API int moe_mi355_profile_read(float* stage_ms, int32_t n);
+MOE_MI355_API int moe_mi355_profile_end(void);
+#define MOE_MI355_NUM_STAGES 5
+
+/* Debug: widen n e4m3 bytes (n % 4 == 0) to bf16 bits with the conversion the GEMM2
+ * kernel uses.  No reference counterpart (the reference never widens e4m3 to bf16);
+ * it lets a test pin that conversion against the OCP e4m3 table. */
+MOE_MI355_API int moe_mi355_debug_e4m3_to_bf16(const uint8_t* in, uint16_t* out, int32_t n, void* stream);
+
+MOE_MI355_API const char* moe_mi355_strerror(int status);
+/* Text of the last HIP error seen by this library in the calling thread. */
+MOE_MI355_API const char* moe_mi355_last_hip_error(void);
+/* Library version string. */
+MOE_MI355_API const char* moe_mi355_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOE_MI355_H_ */

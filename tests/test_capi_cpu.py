@@ -1,0 +1,156 @@
+"""C-ABI library checks that need no GPU: it loads, exports every symbol the header
+declares, sizes its workspace sensibly and rejects bad arguments before touching
+the device.  The Python entry point's argument checks run on CPU tensors too."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from conftest import REPO, pkg
+
+HEADER = os.path.join(REPO, "include", "moe_mi355.h")
+
+
+def header_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"MOE_MI355_API\s+[\w\s\*]+?\b(moe_mi355_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return pkg("kernel")._build_extension()
+
+
+def test_header_declares_entry_points():
+    syms = header_symbols()
+    for s in ("moe_mi355_forward", "moe_mi355_route", "moe_mi355_dispatch",
+              "moe_mi355_workspace_bytes", "moe_mi355_strerror"):
+        assert s in syms
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for s in header_symbols():
+        assert hasattr(lib, s), s
+
+
+def test_exported_symbols_are_only_the_c_abi():
+    path = pkg("kernel").library_path()
+    import subprocess
+    out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True).stdout
+    exported = {l.split()[-1] for l in out.splitlines() if " T " in l}
+    assert exported == set(header_symbols())
+
+
+def test_workspace_bytes(lib):
+    k = pkg("kernel")
+    sizes = [k.workspace_bytes(t) for t in (0, 1, 8, 64, 1024, 8192)]
+    assert all(s % 256 == 0 for s in sizes)
+    assert sizes == sorted(sizes)
+    lay = k.workspace_layout(64)
+    assert lay.total == sizes[3]
+    offs = [lay.topk_ids, lay.topk_weights, lay.inverse_rows, lay.meta, lay.tiles,
+            lay.sorted_tokens, lay.sorted_weights, lay.intermediate, lay.expert_out]
+    assert offs == sorted(offs) and all(o % 256 == 0 for o in offs)
+    assert lay.expert_out + 64 * 8 * 7168 * 4 <= lay.total
+    assert lay.max_tiles == (64 * 8 + lay.tile_m - 1) // lay.tile_m + 32
+    assert lib.moe_mi355_workspace_bytes(-1) == 0
+    assert lib.moe_mi355_workspace_bytes(1 << 21) == 0
+
+
+def test_forward_rejects_bad_arguments_without_a_gpu(lib):
+    k = pkg("kernel")
+    a = k.MoeArgs()
+    assert lib.moe_mi355_forward(None, None) == -1
+    a.T = -3
+    assert lib.moe_mi355_forward(ctypes.byref(a), None) == -2
+    a.T = 0
+    assert lib.moe_mi355_forward(ctypes.byref(a), None) == 0   # nothing to do
+    a.T = 4
+    assert lib.moe_mi355_forward(ctypes.byref(a), None) == -1  # NULL tensors
+    fake = 1 << 20
+    for f in ("routing_logits", "routing_bias", "hidden_states", "hidden_states_scale",
+              "gemm1_weights", "gemm1_weights_scale", "gemm2_weights", "gemm2_weights_scale",
+              "output"):
+        setattr(a, f, fake)
+    a.hidden_states = fake + 8
+    assert lib.moe_mi355_forward(ctypes.byref(a), None) == -4  # misaligned
+    a.hidden_states = fake
+    assert lib.moe_mi355_forward(ctypes.byref(a), None) == -3  # no workspace
+    a.workspace = fake
+    a.workspace_bytes = 100
+    assert lib.moe_mi355_forward(ctypes.byref(a), None) == -3  # too small
+    assert lib.moe_mi355_dispatch(None, None, 4, 0, 48, None, None, None, None, None, None, None) == -6
+    assert lib.moe_mi355_route(None, None, -1, 1.0, None, None, None) == -2
+    assert lib.moe_mi355_strerror(-3).decode().startswith("workspace")
+    assert lib.moe_mi355_debug_e4m3_to_bf16(None, None, 4, None) == -1
+
+
+def _cpu_args(T=4):
+    return [torch.zeros(T, 256), torch.zeros(256, dtype=torch.bfloat16),
+            torch.zeros(T, 7168, dtype=torch.float8_e4m3fn), torch.ones(56, T),
+            torch.zeros(32, 4096, 7168, dtype=torch.float8_e4m3fn), torch.ones(32, 32, 56),
+            torch.zeros(32, 7168, 2048, dtype=torch.float8_e4m3fn), torch.ones(32, 56, 16),
+            0, 2.5, torch.zeros(T, 7168, dtype=torch.bfloat16)]
+
+
+@pytest.fixture(scope="module")
+def cpu_args():
+    return _cpu_args()
+
+
+@pytest.mark.parametrize("idx,bad,msg", [
+    (0, torch.zeros(4, 256, dtype=torch.float16), "routing_logits must have dtype"),
+    (1, torch.zeros(256), "routing_bias must have dtype"),
+    (1, torch.zeros(128, dtype=torch.bfloat16), "routing_bias must have shape"),
+    (2, torch.zeros(4, 7168, dtype=torch.bfloat16), "hidden_states must have dtype"),
+    (3, torch.ones(4, 56), "hidden_states_scale must have shape"),
+    (5, torch.ones(32, 56, 32), "gemm1_weights_scale must have shape"),
+    (7, torch.ones(32, 16, 56), "gemm2_weights_scale must have shape"),
+    (10, torch.zeros(4, 7168), "output must have dtype"),
+    (10, torch.zeros(3, 7168, dtype=torch.bfloat16), "output must have shape"),
+])
+def test_kernel_validates_like_the_reference(cpu_args, idx, bad, msg):
+    k = pkg("kernel")
+    args = list(cpu_args)
+    args[idx] = bad
+    with pytest.raises(ValueError, match=msg):
+        k.kernel(*args)
+
+
+def test_kernel_rejects_host_tensors(cpu_args):
+    k = pkg("kernel")
+    with pytest.raises(ValueError, match="GPU tensor"):
+        k.kernel(*cpu_args)
+
+
+def test_kernel_signature_matches_reference():
+    """Same 11 positional parameters, same names and order as the reference's
+    solution/python/kernel.py:95-107 (the harness checks the DPS parameter count)."""
+    import inspect
+    k = pkg("kernel")
+    params = [p for p in inspect.signature(k.kernel).parameters.values()
+              if p.kind == p.POSITIONAL_OR_KEYWORD]
+    assert [p.name for p in params] == [
+        "routing_logits", "routing_bias", "hidden_states", "hidden_states_scale",
+        "gemm1_weights", "gemm1_weights_scale", "gemm2_weights", "gemm2_weights_scale",
+        "local_expert_offset", "routed_scaling_factor", "output"]
+
+
+def test_config_toml_names_the_entry_point():
+    import tomli
+    with open(os.path.join(REPO, "flash-infer-bench-starter-kit_amd", "config.toml"), "rb") as f:
+        cfg = tomli.load(f)
+    assert cfg["solution"]["definition"] == "moe_fp8_block_scale_ds_routing_topk8_ng8_kg4_e32_h7168_i2048"
+    assert cfg["build"]["entry_point"] == "kernel.py::kernel"
+    assert cfg["build"]["destination_passing_style"] is True
+
+
+def test_no_oracle_import_in_product():
+    pkg_dir = os.path.join(REPO, "flash-infer-bench-starter-kit_amd")
+    for root, _, files in os.walk(pkg_dir):
+        for f in files:
+            if f.endswith((".py", ".hip", ".h", ".cpp")):
+                text = open(os.path.join(root, f)).read()
+                assert "moe_oracle" not in text and "oracle/" not in text, f

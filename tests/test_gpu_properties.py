@@ -1,0 +1,107 @@
+"""Size-independent exact properties of the HIP path at the full benchmark sizes
+(runs on the MI355X box).  None of these needs the oracle:
+
+* determinism: two calls give bit-identical outputs (no order-dependent atomics);
+* linearity in routed_scaling_factor: doubling it doubles every output exactly
+  (power-of-two scaling commutes with every rounding on the path);
+* token permutation: permuting the tokens permutes the output rows exactly;
+* tokens with no local expert get exactly +0, and an offset with no local experts
+  zeroes the whole (pre-poisoned) output;
+* T = 0 is a no-op; T = 1 and odd T work.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import oracle, pkg
+from gpu_common import compare_to_oracle, config_inputs, note, run_forward
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("idx", [1, 3, 4])
+def test_deterministic(idx):
+    d = config_inputs(idx)
+    note(f"[gpu] determinism config {idx}")
+    a = run_forward(d)
+    b = run_forward(d)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+@pytest.mark.parametrize("idx", [1, 2])
+def test_factor_doubling_is_exact(idx):
+    d = config_inputs(idx)
+    note(f"[gpu] factor doubling config {idx}")
+    a = run_forward(d)
+    b = run_forward(d, routed_scaling_factor=2 * d["routed_scaling_factor"])
+    assert torch.equal((a.float() * 2).to(torch.bfloat16).view(torch.int16), b.view(torch.int16))
+
+
+def test_token_permutation():
+    d = config_inputs(2)
+    note("[gpu] token permutation config 2")
+    T = d["routing_logits"].shape[0]
+    perm = torch.randperm(T, generator=torch.Generator().manual_seed(3)).cuda()
+    p = dict(d)
+    p["routing_logits"] = d["routing_logits"][perm].contiguous()
+    p["hidden_states"] = d["hidden_states"][perm].contiguous()
+    p["hidden_states_scale"] = d["hidden_states_scale"][:, perm].contiguous()
+    a = run_forward(d)
+    b = run_forward(p)
+    assert torch.equal(a[perm].view(torch.int16), b.view(torch.int16))
+
+
+def test_nonlocal_tokens_are_zero():
+    d = config_inputs(1)
+    out = run_forward(d)
+    ids, _ = oracle().route(d["routing_logits"], d["routing_bias"], d["routed_scaling_factor"])
+    off = d["local_expert_offset"]
+    nonlocal_t = [t for t in range(ids.shape[0]) if not ((ids[t] >= off) & (ids[t] < off + 32)).any()]
+    for t in nonlocal_t:
+        assert (out[t].view(torch.int16) == 0).all()
+
+
+@pytest.mark.parametrize("offset", [1000, -100])
+def test_offset_without_local_experts_zeroes_output(offset):
+    d = config_inputs(0)
+    out = run_forward(d, local_expert_offset=offset)
+    assert (out.view(torch.int16) == 0).all()
+
+
+def test_partially_local_offset_matches_oracle():
+    """offset 240: local experts 240..271, only 240..255 exist (moe.cu:213-214)."""
+    d = dict(config_inputs(1))
+    d["local_expert_offset"] = 240
+    out = run_forward(d)
+    st = compare_to_oracle(d, out, list(range(d["routing_logits"].shape[0])))
+    note(f"[gpu] offset 240 stats {st}")
+    assert st["frac_within"] == 1.0, st
+
+
+def test_empty_batch_is_noop():
+    k = pkg("kernel")
+    wl = pkg("workloads")
+    d = dict(config_inputs(0))
+    d["routing_logits"] = d["routing_logits"][:0]
+    d["hidden_states"] = d["hidden_states"][:0]
+    d["hidden_states_scale"] = d["hidden_states_scale"][:, :0].contiguous()
+    d["output"] = d["output"][:0]
+    k.kernel(*wl.as_args(d))
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("T", [1, 5, 67])
+def test_small_odd_batches(T):
+    d0 = config_inputs(1)
+    d = dict(d0)
+    d["routing_logits"] = d0["routing_logits"][:T].contiguous() if T <= 64 else torch.cat(
+        [d0["routing_logits"], d0["routing_logits"][:T - 64]]).contiguous()
+    d["hidden_states"] = d0["hidden_states"][:T].contiguous() if T <= 64 else torch.cat(
+        [d0["hidden_states"].view(torch.uint8), d0["hidden_states"][:T - 64].view(torch.uint8)]).view(torch.float8_e4m3fn)
+    d["hidden_states_scale"] = d0["hidden_states_scale"][:, :T].contiguous() if T <= 64 else torch.cat(
+        [d0["hidden_states_scale"], d0["hidden_states_scale"][:, :T - 64]], dim=1).contiguous()
+    d["output"] = torch.empty(T, 7168, dtype=torch.bfloat16, device="cuda")
+    out = run_forward(d)
+    st = compare_to_oracle(d, out, list(range(T)))
+    note(f"[gpu] T={T} stats {st}")
+    assert st["frac_within"] == 1.0, st
