@@ -54,7 +54,23 @@ def parse():
     ap.add_argument("--rotate", type=int, default=4, help="input copies cycled over steps")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget-s", type=float, default=20.0)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run K device-to-device copies of MIB MiB (calibrates "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE against known bytes)")
     return ap.parse_args()
+
+
+def copy_calibration(mib: int, steps: int) -> int:
+    import torch
+    n = mib * (1 << 20)
+    src = torch.randint(0, 255, (n,), dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": n, "steps": steps}))
+    return 0
 
 
 def traffic_from_profiles(workload: str, kernel: str):
@@ -75,6 +91,8 @@ def main() -> int:
         print(f"bench.py measures one GPU only (one expert-parallel rank's share); "
               f"--gpus {a.gpus} is not supported in this build.", file=sys.stderr)
         return 2
+    if a.copy_calibration:
+        return copy_calibration(a.copy_calibration, a.steps)
 
     import numpy as np
     import torch

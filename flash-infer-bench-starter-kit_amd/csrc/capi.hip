@@ -14,6 +14,7 @@
 // workgroup reads the real count written by dispatch and exits when it runs out.
 
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "moe_device.h"
@@ -24,18 +25,43 @@ void launch_route(const float*, const uint16_t*, int, float, int*, float*, hipSt
 bool launch_dispatch(const int*, const float*, int, int, int, int*, int*, int4*, int*, float*,
                      int*, hipStream_t);
 int dispatch_max_tiles(int T, int tm);
-void launch_gemm1(const uint8_t*, const float*, int, const uint8_t*, const float*, const int4*,
-                  const int*, int, const int*, uint16_t*, hipStream_t);
-void launch_gemm2(const uint16_t*, const uint8_t*, const float*, const int4*, const int*, int,
-                  float*, hipStream_t);
+bool launch_gemm1(int, const uint8_t*, const float*, int, const uint8_t*, const float*,
+                  const int4*, const int*, int, const int*, uint16_t*, hipStream_t);
+bool launch_gemm2(int, const uint16_t*, const uint8_t*, const float*, const int4*, const int*,
+                  int, float*, hipStream_t);
 void launch_combine(const float*, const float*, const int*, int, uint16_t*, hipStream_t);
 void launch_e4m3_to_bf16(const uint8_t*, uint16_t*, int, hipStream_t);
 }  // namespace moe
 
 namespace {
 
-constexpr int kTileM = 64;              // rows per GEMM tile (4 MFMA column blocks)
 constexpr int32_t kMaxT = 1 << 20;      // keeps every row index inside int32
+constexpr int kMinTileM = 16;           // smallest row tile; sizes the tile list
+
+// Kernel plan per token count.  Small T streams weights through LDS with the
+// DMA kernels (row tiles of 16 or 32 rows); large T uses the 64-row tile kernels.
+// Variant ids are those of launch_gemm1 / launch_gemm2; MOE_MI355_G1 / MOE_MI355_G2
+// override them for tuning sweeps (ignored unless both imply the same tile height).
+struct Plan {
+    int tm, g1, g2;
+};
+
+int variant_tile_m(int v) { return v < 0 ? 64 : ((v % 6) < 3 ? 16 : 32); }
+
+Plan choose_plan(int32_t T) {
+    Plan p;
+    if (T <= 96) p = {16, 8, 8};
+    else if (T <= 256) p = {32, 11, 10};
+    else p = {64, -1, -1};
+    const char* e1 = getenv("MOE_MI355_G1");
+    const char* e2 = getenv("MOE_MI355_G2");
+    const int env_g1 = e1 ? atoi(e1) : -99;
+    const int env_g2 = e2 ? atoi(e2) : -99;
+    if (env_g1 >= -1 && env_g1 <= 11 && env_g2 >= -1 && env_g2 <= 11 &&
+        variant_tile_m(env_g1) == variant_tile_m(env_g2))
+        p = {variant_tile_m(env_g1), env_g1, env_g2};
+    return p;
+}
 
 thread_local char g_hip_error[256] = "";
 
@@ -44,7 +70,7 @@ size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
 bool fill_layout(int32_t T, moe_mi355_workspace_layout* L) {
     if (T < 0 || T > kMaxT) return false;
     const size_t R = (size_t)T * moe::kTopK;
-    const int mt = moe::dispatch_max_tiles(T, kTileM);
+    const int mt = moe::dispatch_max_tiles(T, kMinTileM);
     size_t off = 0;
     auto take = [&](size_t bytes) {
         const size_t o = off;
@@ -61,7 +87,7 @@ bool fill_layout(int32_t T, moe_mi355_workspace_layout* L) {
     L->intermediate = take(R * moe::kI * 2);
     L->expert_out = take(R * moe::kH * 4);
     L->total = off;
-    L->tile_m = kTileM;
+    L->tile_m = choose_plan(T).tm;
     L->max_tiles = mt;
     return true;
 }
@@ -152,7 +178,8 @@ int moe_mi355_dispatch(const int32_t* topk_ids, const float* topk_weights, int32
     if (!topk_ids || !topk_weights || !expert_offsets || !sorted_tokens || !sorted_weights ||
         !inverse_rows || !tiles || !num_tiles)
         return MOE_ERR_NULL_POINTER;
-    if (!aligned16(tiles)) return MOE_ERR_MISALIGNED;
+    if (!aligned16(tiles) || !aligned16(topk_ids) || !aligned16(topk_weights))
+        return MOE_ERR_MISALIGNED;
     hipStream_t s = (hipStream_t)stream;
     moe::launch_dispatch(topk_ids, topk_weights, T, clamp_offset(local_expert_offset), tile_m,
                          expert_offsets, num_tiles, reinterpret_cast<int4*>(tiles), sorted_tokens,
@@ -199,14 +226,16 @@ int moe_mi355_forward(const moe_mi355_args* a, void* stream) {
     moe::launch_route(a->routing_logits, a->routing_bias, T, (float)a->routed_scaling_factor, ids,
                       wts, s);
     if (prof) prof_record(slot, 1, s);
-    moe::launch_dispatch(ids, wts, T, clamp_offset(a->local_expert_offset), L.tile_m, meta,
+    const Plan plan = choose_plan(T);
+    const int max_tiles = moe::dispatch_max_tiles(T, plan.tm);
+    moe::launch_dispatch(ids, wts, T, clamp_offset(a->local_expert_offset), plan.tm, meta,
                          num_tiles, tiles, stok, sw, inv, s);
     if (prof) prof_record(slot, 2, s);
-    moe::launch_gemm1(a->hidden_states, a->hidden_states_scale, T, a->gemm1_weights,
-                      a->gemm1_weights_scale, tiles, num_tiles, L.max_tiles, stok, inter, s);
+    moe::launch_gemm1(plan.g1, a->hidden_states, a->hidden_states_scale, T, a->gemm1_weights,
+                      a->gemm1_weights_scale, tiles, num_tiles, max_tiles, stok, inter, s);
     if (prof) prof_record(slot, 3, s);
-    moe::launch_gemm2(inter, a->gemm2_weights, a->gemm2_weights_scale, tiles, num_tiles,
-                      L.max_tiles, rows, s);
+    moe::launch_gemm2(plan.g2, inter, a->gemm2_weights, a->gemm2_weights_scale, tiles, num_tiles,
+                      max_tiles, rows, s);
     if (prof) prof_record(slot, 4, s);
     moe::launch_combine(rows, sw, inv, T, a->output, s);
     if (prof) prof_record(slot, 5, s);

@@ -21,6 +21,16 @@
 
 namespace moe {
 
+// inclusive prefix sum over lanes 0..31 of a wave (lanes >= 32 unused)
+__device__ __forceinline__ int scan32(int v, int lane) {
+#pragma unroll
+    for (int off = 1; off < 32; off <<= 1) {
+        const int o = __shfl_up(v, off, 64);
+        if (lane >= off) v += o;
+    }
+    return v;
+}
+
 template <int TM>
 __global__ __launch_bounds__(1024) void dispatch_kernel(
     const int* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int offset,
@@ -28,7 +38,6 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(
     int* __restrict__ sorted_tok, float* __restrict__ sorted_w, int* __restrict__ inv) {
     __shared__ int cnt[kEL];
     __shared__ int off[kEL + 1];
-    __shared__ int toff[kEL + 1];
     __shared__ int cursor[kEL];
     __shared__ int wcnt[16][kEL];
     __shared__ int wbase[16][kEL];
@@ -39,6 +48,7 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(
     if (tid < kEL) cnt[tid] = 0;
     __syncthreads();
 
+    // pass 1: per-expert counts (LDS atomics; the totals do not depend on order)
     const long long nassign = (long long)T * kTopK;
     for (long long i = tid; i < nassign; i += 1024) {
         const int le = topk_ids[i] - offset;
@@ -46,53 +56,69 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(
     }
     __syncthreads();
 
-    if (tid == 0) {
-        int a = 0, b = 0;
-        for (int e = 0; e < kEL; ++e) {
-            off[e] = a;
-            toff[e] = b;
-            a += cnt[e];
-            b += (cnt[e] + TM - 1) / TM;
+    // exclusive scans of the counts and of the tile counts (wave 0, lane = expert)
+    if (wave == 0) {
+        const int c = lane < kEL ? cnt[lane] : 0;
+        const int nt = (c + TM - 1) / TM;
+        const int ci = scan32(c, lane);
+        const int ti = scan32(nt, lane);
+        if (lane < kEL) {
+            const int o = ci - c, to = ti - nt;
+            off[lane] = o;
+            cursor[lane] = o;
+            exp_off[lane] = o;
+            for (int j = 0; j < nt; ++j)
+                tiles[to + j] = make_int4(lane, o + j * TM, min(TM, c - j * TM), 0);
         }
-        off[kEL] = a;
-        toff[kEL] = b;
+        if (lane == kEL - 1) {
+            off[kEL] = ci;
+            exp_off[kEL] = ci;
+            *num_tiles = ti;
+        }
     }
     __syncthreads();
 
-    if (tid <= kEL) exp_off[tid] = off[tid];
-    if (tid == 0) *num_tiles = toff[kEL];
-    for (int e = 0; e < kEL; ++e) {
-        const int nt = toff[e + 1] - toff[e];
-        for (int j = tid; j < nt; j += 1024) {
-            const int rows = min(TM, cnt[e] - j * TM);
-            tiles[toff[e] + j] = make_int4(e, off[e] + j * TM, rows, 0);
-        }
-    }
-    if (tid < kEL) cursor[tid] = off[tid];
-    __syncthreads();
-
+    // pass 2: placement, 1024 tokens per chunk, one per thread
     for (int base = 0; base < T; base += 1024) {
         const int t = base + tid;
         int lek[kTopK];
+        float wk[kTopK];
         uint32_t mask = 0;
+        if (t < T) {
+            const int4* ip = reinterpret_cast<const int4*>(topk_ids + (size_t)t * kTopK);
+            const float4* wp = reinterpret_cast<const float4*>(topk_w + (size_t)t * kTopK);
+            const int4 i0 = ip[0], i1 = ip[1];
+            const float4 w0 = wp[0], w1 = wp[1];
+            const int ids[kTopK] = {i0.x, i0.y, i0.z, i0.w, i1.x, i1.y, i1.z, i1.w};
+            const float ws[kTopK] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
-        for (int k = 0; k < kTopK; ++k) {
-            lek[k] = -1;
-            if (t < T) {
-                const int le = topk_ids[(size_t)t * kTopK + k] - offset;
-                if ((unsigned)le < (unsigned)kEL) {
-                    lek[k] = le;
-                    mask |= 1u << le;
-                }
+            for (int k = 0; k < kTopK; ++k) {
+                const int le = ids[k] - offset;
+                const bool loc = (unsigned)le < (unsigned)kEL;
+                lek[k] = loc ? le : -1;
+                wk[k] = ws[k];
+                if (loc) mask |= 1u << le;
             }
+        } else {
+#pragma unroll
+            for (int k = 0; k < kTopK; ++k) { lek[k] = -1; wk[k] = 0.f; }
         }
+        // rank of this token among the chunk's tokens of each of its experts
+        int rank[kTopK];
+#pragma unroll
+        for (int k = 0; k < kTopK; ++k) rank[k] = 0;
         for (int e = 0; e < kEL; ++e) {
             const uint64_t b = __ballot((mask >> e) & 1u);
             if (lane == 0) wcnt[wave][e] = __popcll(b);
+            const int below = __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32),
+                                                        __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+#pragma unroll
+            for (int k = 0; k < kTopK; ++k) rank[k] = (lek[k] == e) ? below : rank[k];
         }
         __syncthreads();
         if (tid < kEL) {
             int run = cursor[tid];
+#pragma unroll
             for (int w = 0; w < 16; ++w) {
                 wbase[w][tid] = run;
                 run += wcnt[w][tid];
@@ -100,26 +126,17 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(
             cursor[tid] = run;
         }
         __syncthreads();
-        for (int e = 0; e < kEL; ++e) {
-            const uint64_t b = __ballot((mask >> e) & 1u);
-            if ((mask >> e) & 1u) {
-                const int below = __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32),
-                                                            __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
-                const int r = wbase[wave][e] + below;
-#pragma unroll
-                for (int k = 0; k < kTopK; ++k) {
-                    if (lek[k] == e) {
-                        sorted_tok[r] = t;
-                        sorted_w[r] = topk_w[(size_t)t * kTopK + k];
-                        inv[(size_t)t * kTopK + k] = r;
-                    }
-                }
-            }
-        }
         if (t < T) {
 #pragma unroll
-            for (int k = 0; k < kTopK; ++k)
-                if (lek[k] < 0) inv[(size_t)t * kTopK + k] = -1;
+            for (int k = 0; k < kTopK; ++k) {
+                int r = -1;
+                if (lek[k] >= 0) {
+                    r = wbase[wave][lek[k]] + rank[k];
+                    sorted_tok[r] = t;
+                    sorted_w[r] = wk[k];
+                }
+                inv[(size_t)t * kTopK + k] = r;
+            }
         }
         __syncthreads();
     }

@@ -145,14 +145,359 @@ __global__ __launch_bounds__(256) void gemm1_swiglu_kernel(
     }
 }
 
-void launch_gemm1(const uint8_t* hidden, const float* hs_scale, int T, const uint8_t* w1,
-                  const float* s1, const int4* tiles, const int* num_tiles, int max_tiles,
-                  const int* sorted_tok, uint16_t* inter, hipStream_t stream) {
-    constexpr int kGroups = kI / 16;
-    long long work = (long long)max_tiles * kGroups;
-    const int grid = (int)(work < 4096 ? work : 4096);
-    hipLaunchKernelGGL(gemm1_swiglu_kernel<4>, dim3(grid), dim3(256), 0, stream, hidden,
-                       hs_scale, T, w1, s1, tiles, num_tiles, sorted_tok, inter);
+__device__ __forceinline__ void store_swiglu4(uint16_t* __restrict__ inter, int row, int n0,
+                                              const v4f& g, const v4f& u) {
+    uint32_t h[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) h[v] = f32_to_bf16_bits(silu_f32(u[v]) * g[v]);
+    uint2 pk;
+    pk.x = h[0] | (h[1] << 16);
+    pk.y = h[2] | (h[3] << 16);
+    *reinterpret_cast<uint2*>(inter + (size_t)row * kI + n0) = pk;
+}
+
+// Weight-streaming GEMM1 for small token counts (decode).  Same arithmetic as
+// gemm1_swiglu_kernel; the difference is how the weight bytes move:
+//   - a work item is (row tile of <= 16*CB rows, 16 gate + 16 up rows); a workgroup
+//     runs 4/KSPLIT items side by side and KSPLIT waves split each item's 56 K blocks;
+//   - every wave keeps a ring of D K blocks of weights, token rows and token scales
+//     in registers, refilled as soon as a stage is consumed, so each wave always has
+//     D blocks (D * 4 KB of weights) in flight; weights use non-temporal loads.
+template <int CB, int KSPLIT, int D>
+__global__ __launch_bounds__(256) void gemm1_stream_kernel(
+    const uint8_t* __restrict__ hidden, const float* __restrict__ hs_scale, int T,
+    const uint8_t* __restrict__ w1, const float* __restrict__ s1,
+    const int4* __restrict__ tiles, const int* __restrict__ num_tiles,
+    const int* __restrict__ sorted_tok, uint16_t* __restrict__ inter) {
+    constexpr int NGW = 4 / KSPLIT;           // items per workgroup
+    constexpr int KB = kHB / KSPLIT;          // K blocks per wave
+    constexpr int kItems = (kI / 16) / NGW;   // workgroup work units per tile
+    __shared__ v4f red[KSPLIT > 1 ? 4 : 1][2][CB][64];
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r16 = lane & 15, kq = lane >> 4;
+    const int ngl = wave / KSPLIT, ks = wave % KSPLIT;
+    const int nwork = (*num_tiles) * kItems;
+    const v4f zero = {0.f, 0.f, 0.f, 0.f};
+
+    for (int work = blockIdx.x; work < nwork; work += gridDim.x) {
+        const int4 tile = tiles[work / kItems];
+        const int ng = (work % kItems) * NGW + ngl;
+        const int le = tile.x, row0 = tile.y, nrows = tile.z;
+        const int ncb = (nrows + 15) >> 4;
+
+        const uint8_t* ap[CB];
+        const float* sp[CB];
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) {
+            const int tok = sorted_tok[row0 + min(cb * 16 + r16, nrows - 1)];
+            ap[cb] = hidden + (size_t)tok * kH + kq * 32;
+            sp[cb] = hs_scale + tok;
+        }
+        const uint8_t* wg = w1 + (size_t)(le * kN1 + ng * 16 + r16) * kH + kq * 32;
+        const uint8_t* wu = wg + (size_t)kI * kH;
+        const float* sg = s1 + (size_t)(le * kN1B + (ng >> 3)) * kHB;
+        const float* su = sg + (size_t)kIB * kHB;
+        const int kb0 = ks * KB;
+
+        v8i bg[D], bu[D], ba[D][CB];
+        float bs[D][CB];
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            const int kb = kb0 + d;
+            bg[d] = load_v8i_stream(wg + kb * kBlk);
+            bu[d] = load_v8i_stream(wu + kb * kBlk);
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) {
+                ba[d][cb] = load_v8i(ap[cb] + kb * kBlk);
+                bs[d][cb] = sp[cb][(size_t)kb * T];
+            }
+        }
+        v4f ag[CB], au[CB];
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) { ag[cb] = zero; au[cb] = zero; }
+
+#pragma unroll
+        for (int k = 0; k < KB; ++k) {
+            const int d = k % D;
+            const int kb = kb0 + k;
+            const float fsg = sg[kb], fsu = su[kb];
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) {
+                if (cb < ncb) {
+                    const v4f tg = mfma_fp8(bg[d], ba[d][cb], zero);
+                    const v4f tu = mfma_fp8(bu[d], ba[d][cb], zero);
+                    const float fg = bs[d][cb] * fsg, fu = bs[d][cb] * fsu;
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        ag[cb][v] = __builtin_fmaf(tg[v], fg, ag[cb][v]);
+                        au[cb][v] = __builtin_fmaf(tu[v], fu, au[cb][v]);
+                    }
+                }
+            }
+            if (k + D < KB) {
+                const int nkb = kb + D;
+                bg[d] = load_v8i_stream(wg + nkb * kBlk);
+                bu[d] = load_v8i_stream(wu + nkb * kBlk);
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb) {
+                    ba[d][cb] = load_v8i(ap[cb] + nkb * kBlk);
+                    bs[d][cb] = sp[cb][(size_t)nkb * T];
+                }
+            }
+        }
+
+        if constexpr (KSPLIT == 1) {
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) {
+                const int r = cb * 16 + r16;
+                if (cb < ncb && r < nrows) store_swiglu4(inter, row0 + r, ng * 16 + kq * 4, ag[cb], au[cb]);
+            }
+        } else {
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) {
+                if (cb < ncb) {
+                    red[wave][0][cb][lane] = ag[cb];
+                    red[wave][1][cb][lane] = au[cb];
+                }
+            }
+            __syncthreads();
+            if (ks == 0) {
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb) {
+                    const int r = cb * 16 + r16;
+                    if (cb < ncb) {
+                        v4f g = red[wave][0][cb][lane], u = red[wave][1][cb][lane];
+#pragma unroll
+                        for (int q = 1; q < KSPLIT; ++q) {
+                            g += red[wave + q][0][cb][lane];
+                            u += red[wave + q][1][cb][lane];
+                        }
+                        if (r < nrows) store_swiglu4(inter, row0 + r, ng * 16 + kq * 4, g, u);
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// LDS-landed weight streaming (decode).  A wave owns a work item of 16 gate rows +
+// 16 up rows of one expert for one row tile, over KB consecutive K blocks.  Weight
+// bytes travel HBM -> LDS with global_load_lds_dwordx4, each instruction reading 8
+// rows x 128 B (full cache lines: a K block of 8 rows), into a per-wave ring of NS
+// K-block slots (4 KB each); the MFMA operands are then read with ds_read_b128 in
+// the MFMA register layout.  Inside a slot row r keeps its 16-byte chunk c at
+// position c ^ ((r >> 1) & 7), which makes the 16 lanes of each ds_read_b128 quarter
+// hit 16 different bank groups.  Token rows and scales come through L1/L2 into a
+// register ring of the same depth.
+//
+// The compiler does not order LDS DMA against later LDS reads, so every K block
+// issues a fixed number of vector-memory operations (4 DMA + 3 per token block),
+// fenced by sched_barrier, and the wave waits with an explicit vmcnt that leaves
+// exactly the younger K blocks in flight.
+// ---------------------------------------------------------------------------
+
+template <int CB, int KSPLIT, int NS>
+__global__ __launch_bounds__(256) void gemm1_dma_kernel(
+    const uint8_t* __restrict__ hidden, const float* __restrict__ hs_scale, int T,
+    const uint8_t* __restrict__ w1, const float* __restrict__ s1,
+    const int4* __restrict__ tiles, const int* __restrict__ num_tiles,
+    const int* __restrict__ sorted_tok, uint16_t* __restrict__ inter) {
+    constexpr int NGW = 4 / KSPLIT;
+    constexpr int KB = kHB / KSPLIT;
+    constexpr int kItems = (kI / 16) / NGW;
+    constexpr int kSlot = 32 * kBlk;                  // 32 rows x 128 B
+    constexpr int kVmPerKb = 4 + 3 * CB;              // vector-memory ops per K block
+    static_assert(NS >= 2 && (NS - 1) * kVmPerKb < 64, "ring too deep for vmcnt");
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[4][NS][kSlot];
+    __shared__ v4f red[KSPLIT > 1 ? 4 : 1][2][CB][64];
+
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int r16 = lane & 15, kq = lane >> 4;
+    const int ngl = wave / KSPLIT, ks = wave % KSPLIT;
+    const int nwork = (*num_tiles) * kItems;
+    const v4f zero = {0.f, 0.f, 0.f, 0.f};
+    uint8_t* myring = &ring[wave][0][0];
+
+    // DMA source: instruction i covers rows 8i..8i+7 of the item (0-15 gate, 16-31 up)
+    const int drow = lane >> 3;                         // row within the instruction
+    const int dchunk = (lane & 7);                      // LDS position of this lane's chunk
+    // MFMA read offsets inside a slot (gate row r16 and up row 16 + r16, halves h = 0, 1)
+    const int swz = (r16 >> 1) & 7;
+    const int rd_g0 = r16 * kBlk + (((2 * kq) ^ swz) << 4);
+    const int rd_g1 = r16 * kBlk + (((2 * kq + 1) ^ swz) << 4);
+    const int rd_u0 = rd_g0 + 16 * kBlk;
+    const int rd_u1 = rd_g1 + 16 * kBlk;
+
+    for (int work = blockIdx.x; work < nwork; work += gridDim.x) {
+        const int4 tile = tiles[work / kItems];
+        const int ng = (work % kItems) * NGW + ngl;
+        const int le = tile.x, row0 = tile.y, nrows = tile.z;
+        const int ncb = (nrows + 15) >> 4;
+
+        const uint8_t* ap[CB];
+        const float* sp[CB];
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) {
+            const int tok = sorted_tok[row0 + min(cb * 16 + r16, nrows - 1)];
+            ap[cb] = hidden + (size_t)tok * kH + kq * 32;
+            sp[cb] = hs_scale + tok;
+        }
+        const uint8_t* dsrc[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = 8 * i + drow;                           // 0..31
+            const int n = (r < 16) ? ng * 16 + r : kI + ng * 16 + (r - 16);
+            const int c = dchunk ^ ((r >> 1) & 7);                // global chunk for this slot position
+            dsrc[i] = w1 + (size_t)(le * kN1 + n) * kH + c * 16;
+        }
+        const float* sg = s1 + (size_t)(le * kN1B + (ng >> 3)) * kHB;
+        const float* su = sg + (size_t)kIB * kHB;
+        const int kb0 = ks * KB;
+
+        v8i ba[NS][CB];
+        float bs[NS][CB];
+        auto issue = [&](int k) {
+            const int kb = kb0 + k;
+            uint8_t* slot = myring + (k % NS) * kSlot;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                dma16(dsrc[i] + kb * kBlk, slot + i * 1024);
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) {
+                ba[k % NS][cb] = load_v8i(ap[cb] + kb * kBlk);
+                bs[k % NS][cb] = sp[cb][(size_t)kb * T];
+            }
+        };
+
+#pragma unroll
+        for (int k = 0; k < NS - 1 && k < KB; ++k) {
+            issue(k);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        v4f ag[CB], au[CB];
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) { ag[cb] = zero; au[cb] = zero; }
+
+#pragma unroll
+        for (int k = 0; k < KB; ++k) {
+            if (k + NS - 1 < KB) issue(k + NS - 1);
+            __builtin_amdgcn_sched_barrier(0);
+            // K blocks issued after k: min(NS - 1, KB - 1 - k)
+            constexpr int dummy = 0; (void)dummy;
+            const int younger = (KB - 1 - k) < (NS - 1) ? (KB - 1 - k) : (NS - 1);
+            switch (younger) {   // resolved at compile time after unrolling
+                case 0: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
+                case 1: __builtin_amdgcn_s_waitcnt(vmcnt_imm(1 * kVmPerKb)); break;
+                case 2: __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kVmPerKb)); break;
+                case 3: __builtin_amdgcn_s_waitcnt(vmcnt_imm(3 * kVmPerKb)); break;
+                case 4: __builtin_amdgcn_s_waitcnt(vmcnt_imm(4 * kVmPerKb)); break;
+                case 5: __builtin_amdgcn_s_waitcnt(vmcnt_imm(5 * kVmPerKb)); break;
+                case 6: __builtin_amdgcn_s_waitcnt(vmcnt_imm(6 * kVmPerKb)); break;
+                default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            const uint8_t* slot = myring + (k % NS) * kSlot;
+            const v4u g0 = *reinterpret_cast<const v4u*>(slot + rd_g0);
+            const v4u g1 = *reinterpret_cast<const v4u*>(slot + rd_g1);
+            const v4u u0 = *reinterpret_cast<const v4u*>(slot + rd_u0);
+            const v4u u1 = *reinterpret_cast<const v4u*>(slot + rd_u1);
+            const v8i bg = {(int)g0[0], (int)g0[1], (int)g0[2], (int)g0[3], (int)g1[0], (int)g1[1], (int)g1[2], (int)g1[3]};
+            const v8i bu = {(int)u0[0], (int)u0[1], (int)u0[2], (int)u0[3], (int)u1[0], (int)u1[1], (int)u1[2], (int)u1[3]};
+            const int kb = kb0 + k;
+            const float fsg = sg[kb], fsu = su[kb];
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) {
+                if (cb < ncb) {
+                    const v4f tg = mfma_fp8(bg, ba[k % NS][cb], zero);
+                    const v4f tu = mfma_fp8(bu, ba[k % NS][cb], zero);
+                    const float fg = bs[k % NS][cb] * fsg, fu = bs[k % NS][cb] * fsu;
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        ag[cb][v] = __builtin_fmaf(tg[v], fg, ag[cb][v]);
+                        au[cb][v] = __builtin_fmaf(tu[v], fu, au[cb][v]);
+                    }
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+
+        if constexpr (KSPLIT == 1) {
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) {
+                const int r = cb * 16 + r16;
+                if (cb < ncb && r < nrows) store_swiglu4(inter, row0 + r, ng * 16 + kq * 4, ag[cb], au[cb]);
+            }
+        } else {
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) {
+                if (cb < ncb) {
+                    red[wave][0][cb][lane] = ag[cb];
+                    red[wave][1][cb][lane] = au[cb];
+                }
+            }
+            __syncthreads();
+            if (ks == 0) {
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb) {
+                    const int r = cb * 16 + r16;
+                    if (cb < ncb) {
+                        v4f g = red[wave][0][cb][lane], u = red[wave][1][cb][lane];
+#pragma unroll
+                        for (int q = 1; q < KSPLIT; ++q) {
+                            g += red[wave + q][0][cb][lane];
+                            u += red[wave + q][1][cb][lane];
+                        }
+                        if (r < nrows) store_swiglu4(inter, row0 + r, ng * 16 + kq * 4, g, u);
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+static int grid_for(long long work) { return (int)(work < 4096 ? work : 4096); }
+
+// variant: 0..5 register-ring streaming, 6..11 LDS-landed streaming, both with
+// (CB, KSPLIT) = (1,1) (1,2) (1,4) (2,1) (2,2) (2,4); -1 the 64-row tile kernel
+bool launch_gemm1(int variant, const uint8_t* hidden, const float* hs_scale, int T,
+                  const uint8_t* w1, const float* s1, const int4* tiles, const int* num_tiles,
+                  int max_tiles, const int* sorted_tok, uint16_t* inter, hipStream_t stream) {
+    constexpr int G = kI / 16;
+    const long long mt = max_tiles;
+#define G1_STREAM(CB, KS, D)                                                                    \
+    hipLaunchKernelGGL((gemm1_stream_kernel<CB, KS, D>), dim3(grid_for(mt * G * KS / 4)),       \
+                       dim3(256), 0, stream, hidden, hs_scale, T, w1, s1, tiles, num_tiles,     \
+                       sorted_tok, inter)
+#define G1_DMA(CB, KS, NS)                                                                      \
+    hipLaunchKernelGGL((gemm1_dma_kernel<CB, KS, NS>), dim3(grid_for(mt * G * KS / 4)),        \
+                       dim3(256), 0, stream, hidden, hs_scale, T, w1, s1, tiles, num_tiles,     \
+                       sorted_tok, inter)
+    switch (variant) {
+        case 0: G1_STREAM(1, 1, 4); return true;
+        case 1: G1_STREAM(1, 2, 4); return true;
+        case 2: G1_STREAM(1, 4, 4); return true;
+        case 3: G1_STREAM(2, 1, 3); return true;
+        case 4: G1_STREAM(2, 2, 3); return true;
+        case 5: G1_STREAM(2, 4, 3); return true;
+        case 6: G1_DMA(1, 1, 4); return true;
+        case 7: G1_DMA(1, 2, 4); return true;
+        case 8: G1_DMA(1, 4, 4); return true;
+        case 9: G1_DMA(2, 1, 3); return true;
+        case 10: G1_DMA(2, 2, 3); return true;
+        case 11: G1_DMA(2, 4, 3); return true;
+        case -1:
+            hipLaunchKernelGGL(gemm1_swiglu_kernel<4>, dim3(grid_for(mt * G)), dim3(256), 0, stream,
+                               hidden, hs_scale, T, w1, s1, tiles, num_tiles, sorted_tok, inter);
+            return true;
+        default: return false;
+    }
+#undef G1_STREAM
+#undef G1_DMA
 }
 
 }  // namespace moe

@@ -118,6 +118,320 @@ __global__ __launch_bounds__(256) void gemm2_kernel(
     }
 }
 
+// Weight-streaming GEMM2 for small token counts (decode).  Same arithmetic as
+// gemm2_kernel; a work item is (row tile of <= 16*CB rows, HF groups of 16 output
+// columns), a workgroup runs 4/KSPLIT items side by side and KSPLIT waves split the
+// 16 K blocks.  Each wave keeps a ring of D K blocks of W2 bytes and C rows in
+// registers (non-temporal weight loads), refilled as soon as a stage is consumed;
+// the HF weight groups share every C-row load.
+template <int CB, int KSPLIT, int D, int HF>
+__global__ __launch_bounds__(256) void gemm2_stream_kernel(
+    const uint16_t* __restrict__ inter, const uint8_t* __restrict__ w2,
+    const float* __restrict__ s2, const int4* __restrict__ tiles,
+    const int* __restrict__ num_tiles, float* __restrict__ out_rows) {
+    constexpr int NGW = 4 / KSPLIT;
+    constexpr int KB = kIB / KSPLIT;
+    constexpr int kItems = (kH / 16) / (HF * NGW);
+    __shared__ v4f red[KSPLIT > 1 ? 4 : 1][HF][CB][64];
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r16 = lane & 15, kq = lane >> 4;
+    const int ngl = wave / KSPLIT, ks = wave % KSPLIT;
+    const int nwork = (*num_tiles) * kItems;
+    const v4f zero = {0.f, 0.f, 0.f, 0.f};
+
+    for (int work = blockIdx.x; work < nwork; work += gridDim.x) {
+        const int4 tile = tiles[work / kItems];
+        const int hg0 = ((work % kItems) * NGW + ngl) * HF;
+        const int le = tile.x, row0 = tile.y, nrows = tile.z;
+        const int ncb = (nrows + 15) >> 4;
+
+        const uint16_t* cp[CB];
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb)
+            cp[cb] = inter + (size_t)(row0 + min(cb * 16 + r16, nrows - 1)) * kI + kq * 32;
+        const uint8_t* wp[HF];
+        const float* sp[HF];
+#pragma unroll
+        for (int hf = 0; hf < HF; ++hf) {
+            wp[hf] = w2 + (size_t)(le * kH + (hg0 + hf) * 16 + r16) * kI + kq * 32;
+            sp[hf] = s2 + (size_t)(le * kHB + ((hg0 + hf) >> 3)) * kIB;
+        }
+        const int kb0 = ks * KB;
+
+        v4u bw[D][HF][2];
+        v4u bc[D][CB][4];
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            const int kb = kb0 + d;
+#pragma unroll
+            for (int hf = 0; hf < HF; ++hf) {
+                const v4u* q = reinterpret_cast<const v4u*>(wp[hf] + kb * kBlk);
+                bw[d][hf][0] = __builtin_nontemporal_load(q);
+                bw[d][hf][1] = __builtin_nontemporal_load(q + 1);
+            }
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) {
+                const v4u* q = reinterpret_cast<const v4u*>(cp[cb] + kb * kBlk);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) bc[d][cb][j] = q[j];
+            }
+        }
+        v4f acc[HF][CB];
+#pragma unroll
+        for (int hf = 0; hf < HF; ++hf)
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) acc[hf][cb] = zero;
+
+#pragma unroll
+        for (int k = 0; k < KB; ++k) {
+            const int d = k % D;
+            const int kb = kb0 + k;
+#pragma unroll
+            for (int hf = 0; hf < HF; ++hf) {
+                const uint32_t ww[8] = {bw[d][hf][0][0], bw[d][hf][0][1], bw[d][hf][0][2], bw[d][hf][0][3],
+                                        bw[d][hf][1][0], bw[d][hf][1][1], bw[d][hf][1][2], bw[d][hf][1][3]};
+                v8bf wb[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    uint32_t d0, d1, d2, d3;
+                    e4m3x4_to_bf16x4(ww[2 * j], d0, d1);
+                    e4m3x4_to_bf16x4(ww[2 * j + 1], d2, d3);
+                    wb[j] = as_v8bf(d0, d1, d2, d3);
+                }
+                const float sb = sp[hf][kb];
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb) {
+                    if (cb < ncb) {
+                        v4f t = zero;
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wb[j], __builtin_bit_cast(v8bf, bc[d][cb][j]), t, 0, 0, 0);
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) acc[hf][cb][v] = __builtin_fmaf(t[v], sb, acc[hf][cb][v]);
+                    }
+                }
+            }
+            if (k + D < KB) {
+                const int nkb = kb + D;
+#pragma unroll
+                for (int hf = 0; hf < HF; ++hf) {
+                    const v4u* q = reinterpret_cast<const v4u*>(wp[hf] + nkb * kBlk);
+                    bw[d][hf][0] = __builtin_nontemporal_load(q);
+                    bw[d][hf][1] = __builtin_nontemporal_load(q + 1);
+                }
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb) {
+                    const v4u* q = reinterpret_cast<const v4u*>(cp[cb] + nkb * kBlk);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) bc[d][cb][j] = q[j];
+                }
+            }
+        }
+
+        if constexpr (KSPLIT == 1) {
+#pragma unroll
+            for (int hf = 0; hf < HF; ++hf)
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb) {
+                    const int r = cb * 16 + r16;
+                    if (cb < ncb && r < nrows)
+                        *reinterpret_cast<v4f*>(out_rows + (size_t)(row0 + r) * kH + (hg0 + hf) * 16 + kq * 4) = acc[hf][cb];
+                }
+        } else {
+#pragma unroll
+            for (int hf = 0; hf < HF; ++hf)
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb)
+                    if (cb < ncb) red[wave][hf][cb][lane] = acc[hf][cb];
+            __syncthreads();
+            if (ks == 0) {
+#pragma unroll
+                for (int hf = 0; hf < HF; ++hf)
+#pragma unroll
+                    for (int cb = 0; cb < CB; ++cb) {
+                        const int r = cb * 16 + r16;
+                        if (cb < ncb) {
+                            v4f o = red[wave][hf][cb][lane];
+#pragma unroll
+                            for (int q = 1; q < KSPLIT; ++q) o += red[wave + q][hf][cb][lane];
+                            if (r < nrows)
+                                *reinterpret_cast<v4f*>(out_rows + (size_t)(row0 + r) * kH + (hg0 + hf) * 16 + kq * 4) = o;
+                        }
+                    }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// LDS-landed weight streaming GEMM2 (decode).  A wave owns HF groups of 16 output
+// columns (W2 rows) of one expert for one row tile, over KB consecutive K blocks.
+// W2 bytes travel HBM -> LDS with global_load_lds_dwordx4, 8 rows x 128 B (full
+// lines) per instruction, into a per-wave ring of NS slots of 16*HF rows x 128 B,
+// row r keeping its 16-byte chunk c at position c ^ ((r >> 1) & 7).  C rows (bf16,
+// L2-resident) come through a register ring of the same depth.  Each K block issues
+// exactly 2*HF DMA + 4*CB loads; an explicit vmcnt keeps the younger blocks in flight
+// (the compiler does not order LDS DMA against LDS reads).
+template <int CB, int KSPLIT, int NS, int HF>
+__global__ __launch_bounds__(256) void gemm2_dma_kernel(
+    const uint16_t* __restrict__ inter, const uint8_t* __restrict__ w2,
+    const float* __restrict__ s2, const int4* __restrict__ tiles,
+    const int* __restrict__ num_tiles, float* __restrict__ out_rows) {
+    constexpr int NGW = 4 / KSPLIT;
+    constexpr int KB = kIB / KSPLIT;
+    constexpr int kItems = (kH / 16) / (HF * NGW);
+    constexpr int kRows = 16 * HF;
+    constexpr int kSlot = kRows * kBlk;
+    constexpr int kVmPerKb = 2 * HF + 4 * CB;
+    static_assert(NS >= 2 && (NS - 1) * kVmPerKb < 64, "ring too deep for vmcnt");
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[4][NS][kSlot];
+    __shared__ v4f red[KSPLIT > 1 ? 4 : 1][HF][CB][64];
+
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int r16 = lane & 15, kq = lane >> 4;
+    const int ngl = wave / KSPLIT, ks = wave % KSPLIT;
+    const int nwork = (*num_tiles) * kItems;
+    const v4f zero = {0.f, 0.f, 0.f, 0.f};
+    uint8_t* myring = &ring[wave][0][0];
+
+    const int drow = lane >> 3, dchunk = lane & 7;
+    const int swz = (r16 >> 1) & 7;
+    const int rd0 = r16 * kBlk + (((2 * kq) ^ swz) << 4);
+    const int rd1 = r16 * kBlk + (((2 * kq + 1) ^ swz) << 4);
+
+    for (int work = blockIdx.x; work < nwork; work += gridDim.x) {
+        const int4 tile = tiles[work / kItems];
+        const int hg0 = ((work % kItems) * NGW + ngl) * HF;
+        const int le = tile.x, row0 = tile.y, nrows = tile.z;
+        const int ncb = (nrows + 15) >> 4;
+
+        const uint16_t* cp[CB];
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb)
+            cp[cb] = inter + (size_t)(row0 + min(cb * 16 + r16, nrows - 1)) * kI + kq * 32;
+        const uint8_t* dsrc[2 * HF];
+#pragma unroll
+        for (int i = 0; i < 2 * HF; ++i) {
+            const int r = 8 * i + drow;                   // 0 .. 16*HF-1
+            const int c = dchunk ^ ((r >> 1) & 7);
+            dsrc[i] = w2 + (size_t)(le * kH + hg0 * 16 + r) * kI + c * 16;
+        }
+        const float* sp[HF];
+#pragma unroll
+        for (int hf = 0; hf < HF; ++hf) sp[hf] = s2 + (size_t)(le * kHB + ((hg0 + hf) >> 3)) * kIB;
+        const int kb0 = ks * KB;
+
+        v4u bc[NS][CB][4];
+        auto issue = [&](int k) {
+            const int kb = kb0 + k;
+            uint8_t* slot = myring + (k % NS) * kSlot;
+#pragma unroll
+            for (int i = 0; i < 2 * HF; ++i)
+                dma16(dsrc[i] + kb * kBlk, slot + i * 1024);
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) {
+                const v4u* q = reinterpret_cast<const v4u*>(cp[cb] + kb * kBlk);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) bc[k % NS][cb][j] = q[j];
+            }
+        };
+
+#pragma unroll
+        for (int k = 0; k < NS - 1 && k < KB; ++k) {
+            issue(k);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        v4f acc[HF][CB];
+#pragma unroll
+        for (int hf = 0; hf < HF; ++hf)
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) acc[hf][cb] = zero;
+
+#pragma unroll
+        for (int k = 0; k < KB; ++k) {
+            if (k + NS - 1 < KB) issue(k + NS - 1);
+            __builtin_amdgcn_sched_barrier(0);
+            const int younger = (KB - 1 - k) < (NS - 1) ? (KB - 1 - k) : (NS - 1);
+            switch (younger) {
+                case 0: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
+                case 1: __builtin_amdgcn_s_waitcnt(vmcnt_imm(1 * kVmPerKb)); break;
+                case 2: __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kVmPerKb)); break;
+                case 3: __builtin_amdgcn_s_waitcnt(vmcnt_imm(3 * kVmPerKb)); break;
+                case 4: __builtin_amdgcn_s_waitcnt(vmcnt_imm(4 * kVmPerKb)); break;
+                case 5: __builtin_amdgcn_s_waitcnt(vmcnt_imm(5 * kVmPerKb)); break;
+                case 6: __builtin_amdgcn_s_waitcnt(vmcnt_imm(6 * kVmPerKb)); break;
+                default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            const uint8_t* slot = myring + (k % NS) * kSlot;
+            const int kb = kb0 + k;
+#pragma unroll
+            for (int hf = 0; hf < HF; ++hf) {
+                const v4u x0 = *reinterpret_cast<const v4u*>(slot + hf * 16 * kBlk + rd0);
+                const v4u x1 = *reinterpret_cast<const v4u*>(slot + hf * 16 * kBlk + rd1);
+                const uint32_t ww[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+                v8bf wb[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    uint32_t d0, d1, d2, d3;
+                    e4m3x4_to_bf16x4(ww[2 * j], d0, d1);
+                    e4m3x4_to_bf16x4(ww[2 * j + 1], d2, d3);
+                    wb[j] = as_v8bf(d0, d1, d2, d3);
+                }
+                const float sb = sp[hf][kb];
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb) {
+                    if (cb < ncb) {
+                        v4f t = zero;
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wb[j], __builtin_bit_cast(v8bf, bc[k % NS][cb][j]), t, 0, 0, 0);
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) acc[hf][cb][v] = __builtin_fmaf(t[v], sb, acc[hf][cb][v]);
+                    }
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+
+        if constexpr (KSPLIT == 1) {
+#pragma unroll
+            for (int hf = 0; hf < HF; ++hf)
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb) {
+                    const int r = cb * 16 + r16;
+                    if (cb < ncb && r < nrows)
+                        *reinterpret_cast<v4f*>(out_rows + (size_t)(row0 + r) * kH + (hg0 + hf) * 16 + kq * 4) = acc[hf][cb];
+                }
+        } else {
+#pragma unroll
+            for (int hf = 0; hf < HF; ++hf)
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb)
+                    if (cb < ncb) red[wave][hf][cb][lane] = acc[hf][cb];
+            __syncthreads();
+            if (ks == 0) {
+#pragma unroll
+                for (int hf = 0; hf < HF; ++hf)
+#pragma unroll
+                    for (int cb = 0; cb < CB; ++cb) {
+                        const int r = cb * 16 + r16;
+                        if (cb < ncb) {
+                            v4f o = red[wave][hf][cb][lane];
+#pragma unroll
+                            for (int q = 1; q < KSPLIT; ++q) o += red[wave + q][hf][cb][lane];
+                            if (r < nrows)
+                                *reinterpret_cast<v4f*>(out_rows + (size_t)(row0 + r) * kH + (hg0 + hf) * 16 + kq * 4) = o;
+                        }
+                    }
+            }
+            __syncthreads();
+        }
+    }
+}
+
 // Debug: widen e4m3 bytes to bf16 with the same conversion GEMM2 uses (n % 4 == 0).
 __global__ void e4m3_to_bf16_kernel(const uint32_t* __restrict__ in, uint2* __restrict__ out, int nwords) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -127,13 +441,44 @@ __global__ void e4m3_to_bf16_kernel(const uint32_t* __restrict__ in, uint2* __re
     out[i] = make_uint2(d0, d1);
 }
 
-void launch_gemm2(const uint16_t* inter, const uint8_t* w2, const float* s2, const int4* tiles,
-                  const int* num_tiles, int max_tiles, float* out_rows, hipStream_t stream) {
-    constexpr int kGroups = kH / 16;
-    long long work = (long long)max_tiles * kGroups;
-    const int grid = (int)(work < 4096 ? work : 4096);
-    hipLaunchKernelGGL(gemm2_kernel<4>, dim3(grid), dim3(256), 0, stream, inter, w2, s2, tiles,
-                       num_tiles, out_rows);
+static int grid_for2(long long work) { return (int)(work < 4096 ? work : 4096); }
+
+// variant: 0..5 register-ring streaming, 6..11 LDS-landed streaming, both with
+// (CB, KSPLIT, HF) = (1,1,2) (1,2,2) (1,4,1) (2,1,2) (2,2,2) (2,4,1); -1 the 64-row
+// tile kernel
+bool launch_gemm2(int variant, const uint16_t* inter, const uint8_t* w2, const float* s2,
+                  const int4* tiles, const int* num_tiles, int max_tiles, float* out_rows,
+                  hipStream_t stream) {
+    const long long mt = max_tiles;
+#define G2_STREAM(CB, KS, D, HF)                                                                  \
+    hipLaunchKernelGGL((gemm2_stream_kernel<CB, KS, D, HF>),                                      \
+                       dim3(grid_for2(mt * (kH / 16) / (HF * (4 / KS)))), dim3(256), 0, stream,   \
+                       inter, w2, s2, tiles, num_tiles, out_rows)
+#define G2_DMA(CB, KS, NS, HF)                                                                    \
+    hipLaunchKernelGGL((gemm2_dma_kernel<CB, KS, NS, HF>),                                        \
+                       dim3(grid_for2(mt * (kH / 16) / (HF * (4 / KS)))), dim3(256), 0, stream,   \
+                       inter, w2, s2, tiles, num_tiles, out_rows)
+    switch (variant) {
+        case 0: G2_STREAM(1, 1, 4, 2); return true;
+        case 1: G2_STREAM(1, 2, 4, 2); return true;
+        case 2: G2_STREAM(1, 4, 4, 1); return true;
+        case 3: G2_STREAM(2, 1, 3, 2); return true;
+        case 4: G2_STREAM(2, 2, 3, 2); return true;
+        case 5: G2_STREAM(2, 4, 4, 1); return true;
+        case 6: G2_DMA(1, 1, 4, 2); return true;
+        case 7: G2_DMA(1, 2, 4, 2); return true;
+        case 8: G2_DMA(1, 4, 4, 1); return true;
+        case 9: G2_DMA(2, 1, 3, 2); return true;
+        case 10: G2_DMA(2, 2, 3, 2); return true;
+        case 11: G2_DMA(2, 4, 3, 1); return true;
+        case -1:
+            hipLaunchKernelGGL(gemm2_kernel<4>, dim3(grid_for2(mt * (kH / 16))), dim3(256), 0, stream,
+                               inter, w2, s2, tiles, num_tiles, out_rows);
+            return true;
+        default: return false;
+    }
+#undef G2_STREAM
+#undef G2_DMA
 }
 
 void launch_e4m3_to_bf16(const uint8_t* in, uint16_t* out, int n, hipStream_t stream) {

@@ -51,4 +51,17 @@ __device__ __forceinline__ float order_bits_inv(uint32_t k) {
     return __uint_as_float(u);
 }
 
+// One global_load_lds_dwordx4: lane L copies the 16 bytes at its own address g to
+// LDS l + 16 L (l must be wave-uniform).
+__device__ __forceinline__ void dma16(const uint8_t* g, uint8_t* l) {
+    __builtin_amdgcn_global_load_lds(g, l, 16, 0, 0);
+}
+
+// s_waitcnt immediate that waits until at most v vector-memory operations are
+// outstanding (gfx9 layout: vmcnt[3:0] bits 3:0, vmcnt[5:4] bits 15:14; expcnt and
+// lgkmcnt left at their maxima).
+__device__ __forceinline__ constexpr int vmcnt_imm(int v) {
+    return (v & 15) | ((v >> 4) << 14) | (7 << 4) | (15 << 8);
+}
+
 }  // namespace moe

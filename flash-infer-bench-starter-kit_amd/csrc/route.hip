@@ -6,9 +6,9 @@
 // the selection-order weight sum of kernel.cu:181-185.
 //
 // Layout on the wave: lane l owns experts 4l..4l+3, so group g = l/8 lives on
-// lanes 8g..8g+7.  Scores travel as 64-bit keys (orderable fp32 bits << 32 |
-// 256 - expert) so one max-reduction picks the highest score and, among equal
-// scores, the lowest expert.
+// lanes 8g..8g+7.  Scores travel as order-preserving 32-bit images of fp32;
+// reductions use DPP (quad permutes and row shifts), and ties between equal scores
+// are broken toward the lower expert with a ballot.
 //
 // The sigmoid is evaluated in binary64 with an exp built from IEEE operations only
 // (Cody-Waite reduction, degree-13 Taylor polynomial, explicit fma) and rounded
@@ -53,28 +53,38 @@ __device__ __forceinline__ float canon_sigmoid(float x) {
     return (float)(1.0 / (1.0 + e));
 }
 
-__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+// ---- cross-lane helpers (DPP; identity 0 for unsigned max) ------------------
 
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
-    const int lo = __shfl_xor((int)(uint32_t)v, m);
-    const int hi = __shfl_xor((int)(uint32_t)(v >> 32), m);
-    return ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
+// max over the whole wave, result uniform (in an SGPR)
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, false));  // row_shr:1
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, false));  // row_shr:2
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x113, 0xf, 0xf, false));  // row_shr:3
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xe, false));  // row_shr:4
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xc, false));  // row_shr:8
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false));  // row_bcast:15
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false));  // row_bcast:31
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
-// max over the 8 lanes of an aligned lane octet (one expert group)
-__device__ __forceinline__ uint64_t octet_max(uint64_t v) {
-    v = max_u64(v, shfl_xor_u64(v, 1));
-    v = max_u64(v, shfl_xor_u64(v, 2));
-    v = max_u64(v, shfl_xor_u64(v, 4));
-    return v;
+// value of lane i^1, i^2 (quad permutes) and i^4 (swap of the two quads of an octet)
+__device__ __forceinline__ uint32_t xor1(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xb1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
+}
+__device__ __forceinline__ uint32_t xor2(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4e, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
+}
+__device__ __forceinline__ uint32_t xor4(uint32_t v) {
+    // banks 0,2 (lanes 0-3, 8-11 of a row) read lane+4; banks 1,3 read lane-4
+    const int a = __builtin_amdgcn_update_dpp((int)v, (int)v, 0x104, 0xf, 0x5, false);  // row_shl:4
+    return (uint32_t)__builtin_amdgcn_update_dpp(a, (int)v, 0x114, 0xf, 0xa, false);     // row_shr:4
 }
 
-__device__ __forceinline__ uint64_t wave_max(uint64_t v) {
-    v = octet_max(v);
-    v = max_u64(v, shfl_xor_u64(v, 8));
-    v = max_u64(v, shfl_xor_u64(v, 16));
-    v = max_u64(v, shfl_xor_u64(v, 32));
-    return v;
+// merge (a1 >= a2) with the pair of another lane: the two largest of the four
+__device__ __forceinline__ void top2_merge(uint32_t& a1, uint32_t& a2, uint32_t b1, uint32_t b2) {
+    const uint32_t hi = max(a1, b1), lo = min(a1, b1);
+    a2 = max(lo, max(a2, b2));
+    a1 = hi;
 }
 
 __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ logits,
@@ -92,28 +102,28 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
     const float bv[4] = {bf16_bits_to_f32(bb.x & 0xffffu), bf16_bits_to_f32(bb.x >> 16),
                          bf16_bits_to_f32(bb.y & 0xffffu), bf16_bits_to_f32(bb.y >> 16)};
     float s[4];
-    uint64_t key[4];
+    uint32_t key[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         s[j] = canon_sigmoid(lgv[j]);
-        const float sb = s[j] + bv[j];
-        key[j] = ((uint64_t)order_bits(sb) << 32) | (uint32_t)(256 - (4 * lane + j));
+        key[j] = order_bits(s[j] + bv[j]);
     }
 
-    // group score: best + second best of the group (moe.cu:186-188)
-    uint64_t m = max_u64(max_u64(key[0], key[1]), max_u64(key[2], key[3]));
-    const uint64_t m1 = octet_max(m);
-    uint64_t m2l = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-        if (key[j] != m1) m2l = max_u64(m2l, key[j]);
-    const uint64_t m2 = octet_max(m2l);
-    const float gscore = order_bits_inv((uint32_t)(m1 >> 32)) + order_bits_inv((uint32_t)(m2 >> 32));
+    // group score = best + second best s+bias of the group (moe.cu:186-188), on the
+    // octet of lanes holding the group; a duplicated maximum counts twice
+    uint32_t a1 = max(key[0], key[1]), a2 = min(key[0], key[1]);
+    top2_merge(a1, a2, max(key[2], key[3]), min(key[2], key[3]));
+    top2_merge(a1, a2, xor1(a1), xor1(a2));
+    top2_merge(a1, a2, xor2(a1), xor2(a2));
+    top2_merge(a1, a2, xor4(a1), xor4(a2));
+    const float gscore = order_bits_inv(a1) + order_bits_inv(a2);
 
-    // keep the 4 best groups, ties to the lower group (kernel.cu:96-115)
+    // keep the 4 best groups, ties to the lower group (kernel.cu:96-115); the group
+    // scores are wave-uniform after the read-lanes
     uint32_t gk[kNGroup];
 #pragma unroll
-    for (int g = 0; g < kNGroup; ++g) gk[g] = order_bits(__shfl(gscore, 8 * g));
+    for (int g = 0; g < kNGroup; ++g)
+        gk[g] = order_bits(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(gscore), 8 * g)));
     uint32_t keep = 0;
 #pragma unroll
     for (int j = 0; j < kTopKGroup; ++j) {
@@ -127,33 +137,39 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
         keep |= 1u << best;
     }
 
-    // top-8 over kept groups (moe.cu:198-200); pruned experts keep only the index
-    // part so they rank below every kept expert; 0 marks a taken expert.
+    // top-8 (moe.cu:198-200): candidate key = orderable score + 1 for kept experts,
+    // 1 for pruned ones, 0 once taken.  Per round the wave maximum is found with DPP,
+    // the lowest lane holding it with a ballot, and that lane's lowest slot with it;
+    // lane l holds experts 4l..4l+3, so this is the lowest expert index.
     const bool kept = ((keep >> (lane >> 3)) & 1u) != 0u;
-    uint64_t ck[4];
+    uint32_t ck[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) ck[j] = kept ? key[j] : (uint64_t)(uint32_t)(256 - (4 * lane + j));
+    for (int j = 0; j < 4; ++j) ck[j] = kept ? key[j] + 1u : 1u;
 
     int my_id = 0;
     float my_s = 0.0f;
     float ssel[kTopK];
 #pragma unroll
     for (int j = 0; j < kTopK; ++j) {
-        const uint64_t lm = max_u64(max_u64(ck[0], ck[1]), max_u64(ck[2], ck[3]));
-        const uint64_t wm = wave_max(lm);
-        const int e = 256 - (int)(uint32_t)(wm & 0x1ffu);
-        const int owner = e >> 2, sub = e & 3;
-        float spick = s[0];
+        const uint32_t lm = max(max(ck[0], ck[1]), max(ck[2], ck[3]));
+        const uint32_t m = wave_max_u32(lm);
+        const uint64_t holders = __ballot(lm == m);
+        const int owner = (int)__builtin_ctzll(holders);
+        int sub = 3;
 #pragma unroll
-        for (int q = 1; q < 4; ++q) spick = (sub == q) ? s[q] : spick;
-        const float se = __shfl(spick, owner);
+        for (int q = 2; q >= 0; --q) sub = (ck[q] == m) ? q : sub;
+        float sp = s[0];
+#pragma unroll
+        for (int q = 1; q < 4; ++q) sp = (sub == q) ? s[q] : sp;
+        const int osub = __builtin_amdgcn_readlane(sub, owner);
+        const float se = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sp), owner));
         if (lane == owner) {
 #pragma unroll
             for (int q = 0; q < 4; ++q)
-                if (q == sub) ck[q] = 0;
+                if (q == osub) ck[q] = 0u;
         }
         ssel[j] = se;
-        if (lane == j) { my_id = e; my_s = se; }
+        if (lane == j) { my_id = 4 * owner + osub; my_s = se; }
     }
 
     // w = s / (sum + 1e-20) * factor, summed in selection order
