@@ -23,7 +23,7 @@
 namespace moe {
 void launch_route(const float*, const uint16_t*, int, float, int*, float*, hipStream_t);
 bool launch_dispatch(const int*, const float*, int, int, int, int*, int*, int4*, int*, float*,
-                     int*, hipStream_t);
+                     int*, int*, hipStream_t);
 int dispatch_max_tiles(int T, int tm);
 bool launch_gemm1(int, const uint8_t*, const float*, int, const uint8_t*, const float*,
                   const int4*, const int*, int, const int*, uint16_t*, hipStream_t);
@@ -39,25 +39,32 @@ constexpr int32_t kMaxT = 1 << 20;      // keeps every row index inside int32
 constexpr int kMinTileM = 16;           // smallest row tile; sizes the tile list
 
 // Kernel plan per token count.  Small T streams weights through LDS with the
-// DMA kernels (row tiles of 16 or 32 rows); large T uses the 64-row tile kernels.
+// DMA kernels (row tiles of 16 or 32 rows); large T uses the 128-row MFMA-bound
+// prefill kernels.
 // Variant ids are those of launch_gemm1 / launch_gemm2; MOE_MI355_G1 / MOE_MI355_G2
 // override them for tuning sweeps (ignored unless both imply the same tile height).
 struct Plan {
     int tm, g1, g2;
 };
 
-int variant_tile_m(int v) { return v < 0 ? 64 : ((v % 6) < 3 ? 16 : 32); }
+int variant_tile_m(int v) {
+    if (v < 0) return 64;
+    if (v == 12) return 128;
+    if (v == 13) return 256;
+    return (v % 6) < 3 ? 16 : 32;
+}
 
 Plan choose_plan(int32_t T) {
     Plan p;
     if (T <= 96) p = {16, 8, 8};
     else if (T <= 256) p = {32, 11, 10};
-    else p = {64, -1, -1};
+    else if (T <= 2048) p = {128, 12, 12};
+    else p = {256, 13, 13};
     const char* e1 = getenv("MOE_MI355_G1");
     const char* e2 = getenv("MOE_MI355_G2");
     const int env_g1 = e1 ? atoi(e1) : -99;
     const int env_g2 = e2 ? atoi(e2) : -99;
-    if (env_g1 >= -1 && env_g1 <= 11 && env_g2 >= -1 && env_g2 <= 11 &&
+    if (env_g1 >= -1 && env_g1 <= 13 && env_g2 >= -1 && env_g2 <= 13 &&
         variant_tile_m(env_g1) == variant_tile_m(env_g2))
         p = {variant_tile_m(env_g1), env_g1, env_g2};
     return p;
@@ -84,6 +91,7 @@ bool fill_layout(int32_t T, moe_mi355_workspace_layout* L) {
     L->tiles = take((size_t)mt * 16);
     L->sorted_tokens = take(R * 4);
     L->sorted_weights = take(R * 4);
+    L->chunk_counts = take((size_t)((T + 1023) / 1024) * moe::kEL * 4);
     L->intermediate = take(R * moe::kI * 2);
     L->expert_out = take(R * moe::kH * 4);
     L->total = off;
@@ -172,18 +180,19 @@ int moe_mi355_route(const float* routing_logits, const uint16_t* routing_bias, i
 int moe_mi355_dispatch(const int32_t* topk_ids, const float* topk_weights, int32_t T,
                        int64_t local_expert_offset, int32_t tile_m, int32_t* expert_offsets,
                        int32_t* sorted_tokens, float* sorted_weights, int32_t* inverse_rows,
-                       int32_t* tiles, int32_t* num_tiles, void* stream) {
+                       int32_t* tiles, int32_t* num_tiles, int32_t* chunk_counts, void* stream) {
     if (T < 0 || T > kMaxT) return MOE_ERR_BAD_SIZE;
-    if (tile_m != 16 && tile_m != 32 && tile_m != 64) return MOE_ERR_BAD_TILE;
+    if (tile_m != 16 && tile_m != 32 && tile_m != 64 && tile_m != 128 && tile_m != 256)
+        return MOE_ERR_BAD_TILE;
     if (!topk_ids || !topk_weights || !expert_offsets || !sorted_tokens || !sorted_weights ||
-        !inverse_rows || !tiles || !num_tiles)
+        !inverse_rows || !tiles || !num_tiles || (T > 1024 && !chunk_counts))
         return MOE_ERR_NULL_POINTER;
     if (!aligned16(tiles) || !aligned16(topk_ids) || !aligned16(topk_weights))
         return MOE_ERR_MISALIGNED;
     hipStream_t s = (hipStream_t)stream;
     moe::launch_dispatch(topk_ids, topk_weights, T, clamp_offset(local_expert_offset), tile_m,
                          expert_offsets, num_tiles, reinterpret_cast<int4*>(tiles), sorted_tokens,
-                         sorted_weights, inverse_rows, s);
+                         sorted_weights, inverse_rows, chunk_counts, s);
     return hip_status(hipGetLastError());
 }
 
@@ -217,6 +226,7 @@ int moe_mi355_forward(const moe_mi355_args* a, void* stream) {
     float* sw = reinterpret_cast<float*>(ws + L.sorted_weights);
     uint16_t* inter = reinterpret_cast<uint16_t*>(ws + L.intermediate);
     float* rows = reinterpret_cast<float*>(ws + L.expert_out);
+    int* chunk_cnt = reinterpret_cast<int*>(ws + L.chunk_counts);
     int* num_tiles = meta + moe::kEL + 1;
 
     const bool prof = (a->flags & MOE_MI355_FLAG_PROFILE) && g_prof.ev && g_prof.used < g_prof.slots;
@@ -229,7 +239,7 @@ int moe_mi355_forward(const moe_mi355_args* a, void* stream) {
     const Plan plan = choose_plan(T);
     const int max_tiles = moe::dispatch_max_tiles(T, plan.tm);
     moe::launch_dispatch(ids, wts, T, clamp_offset(a->local_expert_offset), plan.tm, meta,
-                         num_tiles, tiles, stok, sw, inv, s);
+                         num_tiles, tiles, stok, sw, inv, chunk_cnt, s);
     if (prof) prof_record(slot, 2, s);
     moe::launch_gemm1(plan.g1, a->hidden_states, a->hidden_states_scale, T, a->gemm1_weights,
                       a->gemm1_weights_scale, tiles, num_tiles, max_tiles, stok, inter, s);

@@ -13,9 +13,10 @@
 // expert: tiles[i] = (expert, first row, rows, 0).
 //
 // Placement is atomic-free: tokens are taken in chunks of 1024 (one per thread); for
-// each expert a wave ballot gives every lane its rank inside the wave, a per-wave
-// count table gives the wave's base, and a running cursor per expert carries the
-// position across chunks.
+// each expert a wave ballot gives every lane its rank inside the wave and the wave's
+// count.  Up to 1024 tokens one workgroup does everything in one pass; beyond that a
+// count kernel writes per-chunk expert counts and a place kernel (one workgroup per
+// chunk) turns them into each chunk's base and writes the permutation.
 
 #include "moe_device.h"
 
@@ -31,115 +32,189 @@ __device__ __forceinline__ int scan32(int v, int lane) {
     return v;
 }
 
+// Per-thread view of one token's 8 assignments: local expert (or -1), weight, and a
+// 32-bit mask of its local experts.
+struct TokenRoutes {
+    int lek[kTopK];
+    float wk[kTopK];
+    uint32_t mask;
+};
+
+__device__ __forceinline__ TokenRoutes load_routes(const int* __restrict__ topk_ids,
+                                                   const float* __restrict__ topk_w, int t, int T,
+                                                   int offset) {
+    TokenRoutes r;
+    r.mask = 0;
+    if (t < T) {
+        const int4* ip = reinterpret_cast<const int4*>(topk_ids + (size_t)t * kTopK);
+        const float4* wp = reinterpret_cast<const float4*>(topk_w + (size_t)t * kTopK);
+        const int4 i0 = ip[0], i1 = ip[1];
+        const float4 w0 = wp[0], w1 = wp[1];
+        const int ids[kTopK] = {i0.x, i0.y, i0.z, i0.w, i1.x, i1.y, i1.z, i1.w};
+        const float ws[kTopK] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+        for (int k = 0; k < kTopK; ++k) {
+            const int le = ids[k] - offset;
+            const bool loc = (unsigned)le < (unsigned)kEL;
+            r.lek[k] = loc ? le : -1;
+            r.wk[k] = ws[k];
+            if (loc) r.mask |= 1u << le;
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < kTopK; ++k) { r.lek[k] = -1; r.wk[k] = 0.f; }
+    }
+    return r;
+}
+
+// For each expert e: the wave's count into wcnt[wave][e]; returns in rank[k] this
+// lane's rank among the wave's lanes holding expert lek[k].
+__device__ __forceinline__ void wave_ranks(const TokenRoutes& r, int wave, int lane,
+                                           int (*wcnt)[kEL], int* rank) {
+#pragma unroll
+    for (int k = 0; k < kTopK; ++k) rank[k] = 0;
+    for (int e = 0; e < kEL; ++e) {
+        const uint64_t b = __ballot((r.mask >> e) & 1u);
+        if (lane == 0) wcnt[wave][e] = __popcll(b);
+        const int below = __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32),
+                                                    __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+#pragma unroll
+        for (int k = 0; k < kTopK; ++k) rank[k] = (r.lek[k] == e) ? below : rank[k];
+    }
+}
+
+__device__ __forceinline__ void place(const TokenRoutes& r, const int* rank, int t, int T,
+                                      const int* base, int* __restrict__ sorted_tok,
+                                      float* __restrict__ sorted_w, int* __restrict__ inv) {
+    if (t >= T) return;
+#pragma unroll
+    for (int k = 0; k < kTopK; ++k) {
+        int row = -1;
+        if (r.lek[k] >= 0) {
+            row = base[r.lek[k]] + rank[k];
+            sorted_tok[row] = t;
+            sorted_w[row] = r.wk[k];
+        }
+        inv[(size_t)t * kTopK + k] = row;
+    }
+}
+
+// expert offsets, tile list and tile count from the per-expert totals (wave 0)
 template <int TM>
-__global__ __launch_bounds__(1024) void dispatch_kernel(
+__device__ __forceinline__ void write_offsets_and_tiles(int c, int lane, int* off_lds,
+                                                        int* __restrict__ exp_off,
+                                                        int* __restrict__ num_tiles,
+                                                        int4* __restrict__ tiles) {
+    const int nt = (c + TM - 1) / TM;
+    const int ci = scan32(c, lane);
+    const int ti = scan32(nt, lane);
+    if (lane < kEL) {
+        const int o = ci - c, to = ti - nt;
+        off_lds[lane] = o;
+        exp_off[lane] = o;
+        for (int j = 0; j < nt; ++j) tiles[to + j] = make_int4(lane, o + j * TM, min(TM, c - j * TM), 0);
+    }
+    if (lane == kEL - 1) {
+        exp_off[kEL] = ci;
+        *num_tiles = ti;
+    }
+}
+
+// T <= 1024: one workgroup, one token per thread, one pass over the routes.
+template <int TM>
+__global__ __launch_bounds__(1024) void dispatch_small_kernel(
     const int* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int offset,
     int* __restrict__ exp_off, int* __restrict__ num_tiles, int4* __restrict__ tiles,
     int* __restrict__ sorted_tok, float* __restrict__ sorted_w, int* __restrict__ inv) {
-    __shared__ int cnt[kEL];
-    __shared__ int off[kEL + 1];
-    __shared__ int cursor[kEL];
     __shared__ int wcnt[16][kEL];
     __shared__ int wbase[16][kEL];
+    __shared__ int off[kEL];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
 
-    const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63;
-
-    if (tid < kEL) cnt[tid] = 0;
+    const TokenRoutes r = load_routes(topk_ids, topk_w, tid, T, offset);
+    int rank[kTopK];
+    wave_ranks(r, wave, lane, wcnt, rank);
     __syncthreads();
-
-    // pass 1: per-expert counts (LDS atomics; the totals do not depend on order)
-    const long long nassign = (long long)T * kTopK;
-    for (long long i = tid; i < nassign; i += 1024) {
-        const int le = topk_ids[i] - offset;
-        if ((unsigned)le < (unsigned)kEL) atomicAdd(&cnt[le], 1);
-    }
-    __syncthreads();
-
-    // exclusive scans of the counts and of the tile counts (wave 0, lane = expert)
     if (wave == 0) {
-        const int c = lane < kEL ? cnt[lane] : 0;
-        const int nt = (c + TM - 1) / TM;
-        const int ci = scan32(c, lane);
-        const int ti = scan32(nt, lane);
-        if (lane < kEL) {
-            const int o = ci - c, to = ti - nt;
-            off[lane] = o;
-            cursor[lane] = o;
-            exp_off[lane] = o;
-            for (int j = 0; j < nt; ++j)
-                tiles[to + j] = make_int4(lane, o + j * TM, min(TM, c - j * TM), 0);
-        }
-        if (lane == kEL - 1) {
-            off[kEL] = ci;
-            exp_off[kEL] = ci;
-            *num_tiles = ti;
+        int c = 0;
+        if (lane < kEL)
+            for (int w = 0; w < 16; ++w) c += wcnt[w][lane];
+        write_offsets_and_tiles<TM>(lane < kEL ? c : 0, lane, off, exp_off, num_tiles, tiles);
+    }
+    __syncthreads();
+    if (tid < kEL) {
+        int run = off[tid];
+        for (int w = 0; w < 16; ++w) {
+            wbase[w][tid] = run;
+            run += wcnt[w][tid];
         }
     }
     __syncthreads();
+    place(r, rank, tid, T, wbase[wave], sorted_tok, sorted_w, inv);
+}
 
-    // pass 2: placement, 1024 tokens per chunk, one per thread
-    for (int base = 0; base < T; base += 1024) {
-        const int t = base + tid;
-        int lek[kTopK];
-        float wk[kTopK];
-        uint32_t mask = 0;
-        if (t < T) {
-            const int4* ip = reinterpret_cast<const int4*>(topk_ids + (size_t)t * kTopK);
-            const float4* wp = reinterpret_cast<const float4*>(topk_w + (size_t)t * kTopK);
-            const int4 i0 = ip[0], i1 = ip[1];
-            const float4 w0 = wp[0], w1 = wp[1];
-            const int ids[kTopK] = {i0.x, i0.y, i0.z, i0.w, i1.x, i1.y, i1.z, i1.w};
-            const float ws[kTopK] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-#pragma unroll
-            for (int k = 0; k < kTopK; ++k) {
-                const int le = ids[k] - offset;
-                const bool loc = (unsigned)le < (unsigned)kEL;
-                lek[k] = loc ? le : -1;
-                wk[k] = ws[k];
-                if (loc) mask |= 1u << le;
-            }
-        } else {
-#pragma unroll
-            for (int k = 0; k < kTopK; ++k) { lek[k] = -1; wk[k] = 0.f; }
-        }
-        // rank of this token among the chunk's tokens of each of its experts
-        int rank[kTopK];
-#pragma unroll
-        for (int k = 0; k < kTopK; ++k) rank[k] = 0;
-        for (int e = 0; e < kEL; ++e) {
-            const uint64_t b = __ballot((mask >> e) & 1u);
-            if (lane == 0) wcnt[wave][e] = __popcll(b);
-            const int below = __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32),
-                                                        __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
-#pragma unroll
-            for (int k = 0; k < kTopK; ++k) rank[k] = (lek[k] == e) ? below : rank[k];
-        }
-        __syncthreads();
-        if (tid < kEL) {
-            int run = cursor[tid];
-#pragma unroll
-            for (int w = 0; w < 16; ++w) {
-                wbase[w][tid] = run;
-                run += wcnt[w][tid];
-            }
-            cursor[tid] = run;
-        }
-        __syncthreads();
-        if (t < T) {
-#pragma unroll
-            for (int k = 0; k < kTopK; ++k) {
-                int r = -1;
-                if (lek[k] >= 0) {
-                    r = wbase[wave][lek[k]] + rank[k];
-                    sorted_tok[r] = t;
-                    sorted_w[r] = wk[k];
-                }
-                inv[(size_t)t * kTopK + k] = r;
-            }
-        }
-        __syncthreads();
+// T > 1024, pass 1: chunk c (1024 tokens) writes its per-expert counts.
+__global__ __launch_bounds__(1024) void dispatch_count_kernel(
+    const int* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int offset,
+    int* __restrict__ chunk_cnt) {
+    __shared__ int wcnt[16][kEL];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const TokenRoutes r = load_routes(topk_ids, topk_w, blockIdx.x * 1024 + tid, T, offset);
+    int rank[kTopK];
+    wave_ranks(r, wave, lane, wcnt, rank);
+    __syncthreads();
+    if (tid < kEL) {
+        int c = 0;
+        for (int w = 0; w < 16; ++w) c += wcnt[w][tid];
+        chunk_cnt[blockIdx.x * kEL + tid] = c;
     }
+}
+
+// T > 1024, pass 2: every chunk derives the expert offsets and its own base from the
+// chunk count table, places its tokens; chunk 0 also writes offsets and tiles.
+template <int TM>
+__global__ __launch_bounds__(1024) void dispatch_place_kernel(
+    const int* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int offset,
+    const int* __restrict__ chunk_cnt, int nchunks, int* __restrict__ exp_off,
+    int* __restrict__ num_tiles, int4* __restrict__ tiles, int* __restrict__ sorted_tok,
+    float* __restrict__ sorted_w, int* __restrict__ inv) {
+    __shared__ int wcnt[16][kEL];
+    __shared__ int wbase[16][kEL];
+    __shared__ int off[kEL];
+    __shared__ int cbase[kEL];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int chunk = blockIdx.x;
+
+    const TokenRoutes r = load_routes(topk_ids, topk_w, chunk * 1024 + tid, T, offset);
+    int rank[kTopK];
+    wave_ranks(r, wave, lane, wcnt, rank);
+    if (wave == 0) {
+        int total = 0, before = 0;
+        if (lane < kEL) {
+            for (int c = 0; c < nchunks; ++c) {
+                const int v = chunk_cnt[c * kEL + lane];
+                before += (c < chunk) ? v : 0;
+                total += v;
+            }
+        }
+        if (chunk == 0) {
+            write_offsets_and_tiles<TM>(lane < kEL ? total : 0, lane, off, exp_off, num_tiles, tiles);
+        } else {
+            const int ci = scan32(lane < kEL ? total : 0, lane);
+            if (lane < kEL) off[lane] = ci - total;
+        }
+        if (lane < kEL) cbase[lane] = before;
+    }
+    __syncthreads();
+    if (tid < kEL) {
+        int run = off[tid] + cbase[tid];
+        for (int w = 0; w < 16; ++w) {
+            wbase[w][tid] = run;
+            run += wcnt[w][tid];
+        }
+    }
+    __syncthreads();
+    place(r, rank, chunk * 1024 + tid, T, wbase[wave], sorted_tok, sorted_w, inv);
 }
 
 int dispatch_max_tiles(int T, int tm) {
@@ -147,27 +222,34 @@ int dispatch_max_tiles(int T, int tm) {
     return (int)((rows + tm - 1) / tm) + kEL;
 }
 
+template <int TM>
+static void launch_dispatch_tm(const int* topk_ids, const float* topk_w, int T, int offset,
+                               int* exp_off, int* num_tiles, int4* tiles, int* sorted_tok,
+                               float* sorted_w, int* inv, int* chunk_cnt, hipStream_t stream) {
+    if (T <= 1024) {
+        hipLaunchKernelGGL(dispatch_small_kernel<TM>, dim3(1), dim3(1024), 0, stream, topk_ids,
+                           topk_w, T, offset, exp_off, num_tiles, tiles, sorted_tok, sorted_w, inv);
+        return;
+    }
+    const int nchunks = (T + 1023) / 1024;
+    hipLaunchKernelGGL(dispatch_count_kernel, dim3(nchunks), dim3(1024), 0, stream, topk_ids, topk_w,
+                       T, offset, chunk_cnt);
+    hipLaunchKernelGGL(dispatch_place_kernel<TM>, dim3(nchunks), dim3(1024), 0, stream, topk_ids,
+                       topk_w, T, offset, chunk_cnt, nchunks, exp_off, num_tiles, tiles, sorted_tok,
+                       sorted_w, inv);
+}
+
+// chunk_cnt: int32 [ceil(T/1024) * 32] scratch, needed when T > 1024
 bool launch_dispatch(const int* topk_ids, const float* topk_w, int T, int offset, int tm,
                      int* exp_off, int* num_tiles, int4* tiles, int* sorted_tok,
-                     float* sorted_w, int* inv, hipStream_t stream) {
+                     float* sorted_w, int* inv, int* chunk_cnt, hipStream_t stream) {
     switch (tm) {
-        case 16:
-            hipLaunchKernelGGL(dispatch_kernel<16>, dim3(1), dim3(1024), 0, stream, topk_ids,
-                               topk_w, T, offset, exp_off, num_tiles, tiles, sorted_tok,
-                               sorted_w, inv);
-            return true;
-        case 32:
-            hipLaunchKernelGGL(dispatch_kernel<32>, dim3(1), dim3(1024), 0, stream, topk_ids,
-                               topk_w, T, offset, exp_off, num_tiles, tiles, sorted_tok,
-                               sorted_w, inv);
-            return true;
-        case 64:
-            hipLaunchKernelGGL(dispatch_kernel<64>, dim3(1), dim3(1024), 0, stream, topk_ids,
-                               topk_w, T, offset, exp_off, num_tiles, tiles, sorted_tok,
-                               sorted_w, inv);
-            return true;
-        default:
-            return false;
+        case 16: launch_dispatch_tm<16>(topk_ids, topk_w, T, offset, exp_off, num_tiles, tiles, sorted_tok, sorted_w, inv, chunk_cnt, stream); return true;
+        case 32: launch_dispatch_tm<32>(topk_ids, topk_w, T, offset, exp_off, num_tiles, tiles, sorted_tok, sorted_w, inv, chunk_cnt, stream); return true;
+        case 64: launch_dispatch_tm<64>(topk_ids, topk_w, T, offset, exp_off, num_tiles, tiles, sorted_tok, sorted_w, inv, chunk_cnt, stream); return true;
+        case 128: launch_dispatch_tm<128>(topk_ids, topk_w, T, offset, exp_off, num_tiles, tiles, sorted_tok, sorted_w, inv, chunk_cnt, stream); return true;
+        case 256: launch_dispatch_tm<256>(topk_ids, topk_w, T, offset, exp_off, num_tiles, tiles, sorted_tok, sorted_w, inv, chunk_cnt, stream); return true;
+        default: return false;
     }
 }
 

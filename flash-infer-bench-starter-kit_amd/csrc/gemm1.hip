@@ -289,8 +289,8 @@ __global__ __launch_bounds__(256) void gemm1_stream_kernel(
 // rows x 128 B (full cache lines: a K block of 8 rows), into a per-wave ring of NS
 // K-block slots (4 KB each); the MFMA operands are then read with ds_read_b128 in
 // the MFMA register layout.  Inside a slot row r keeps its 16-byte chunk c at
-// position c ^ ((r >> 1) & 7), which makes the 16 lanes of each ds_read_b128 quarter
-// hit 16 different bank groups.  Token rows and scales come through L1/L2 into a
+// position c ^ swz128(r), which keeps the ds_read_b128 operand reads free of bank
+// conflicts.  Token rows and scales come through L1/L2 into a
 // register ring of the same depth.
 //
 // The compiler does not order LDS DMA against later LDS reads, so every K block
@@ -326,7 +326,7 @@ __global__ __launch_bounds__(256) void gemm1_dma_kernel(
     const int drow = lane >> 3;                         // row within the instruction
     const int dchunk = (lane & 7);                      // LDS position of this lane's chunk
     // MFMA read offsets inside a slot (gate row r16 and up row 16 + r16, halves h = 0, 1)
-    const int swz = (r16 >> 1) & 7;
+    const int swz = swz128(r16);
     const int rd_g0 = r16 * kBlk + (((2 * kq) ^ swz) << 4);
     const int rd_g1 = r16 * kBlk + (((2 * kq + 1) ^ swz) << 4);
     const int rd_u0 = rd_g0 + 16 * kBlk;
@@ -351,7 +351,7 @@ __global__ __launch_bounds__(256) void gemm1_dma_kernel(
         for (int i = 0; i < 4; ++i) {
             const int r = 8 * i + drow;                           // 0..31
             const int n = (r < 16) ? ng * 16 + r : kI + ng * 16 + (r - 16);
-            const int c = dchunk ^ ((r >> 1) & 7);                // global chunk for this slot position
+            const int c = dchunk ^ swz128(r);                // global chunk for this slot position
             dsrc[i] = w1 + (size_t)(le * kN1 + n) * kH + c * 16;
         }
         const float* sg = s1 + (size_t)(le * kN1B + (ng >> 3)) * kHB;
@@ -460,13 +460,303 @@ __global__ __launch_bounds__(256) void gemm1_dma_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------
+// Prefill GEMM1 (many tokens per expert): MFMA-bound tiling.
+//
+// Workgroup tile: 128 gathered token rows x 256 weight rows (128 gate rows
+// n0..n0+127 and the matching 128 up rows 2048+n0..), i.e. 128 x 128 SwiGLU
+// outputs.  Wave w (2 x 2 arrangement) computes 64 tokens x (64 gate + 64 up) rows:
+// per K block 32 MFMA 16x16x128 (4 token blocks x 8 weight blocks) whose fresh
+// partials are scaled by sa[token] * sb[block] into fp32 accumulators.
+//
+// Operands travel HBM/L2 -> LDS with global_load_lds_dwordx4 (8 rows x 128 B per
+// instruction, each wave moving 32 token rows and 64 weight rows; token scales with
+// one global_load_lds_dword), into NS stages of 49 KB; rows keep 16-byte chunk c
+// at c ^ swz128(r) so ds_read_b128 in the MFMA layout is conflict-free.  One workgroup barrier per K block both publishes
+// the stage every wave waited for and frees the stage about to be refilled.
+// Work items (row tile, 128-column group) are grouped 4 row tiles x all column
+// groups (column-major inside a group) and each XCD takes a contiguous run of 32
+// items of a round: 4 row tiles x 8 column groups share one L2, so each token row
+// block is fetched about twice instead of 16 times and each weight block once per
+// 4 row tiles.
+// ---------------------------------------------------------------------------
+template <int NS>
+__global__ __launch_bounds__(256) void gemm1_prefill_kernel(
+    const uint8_t* __restrict__ hidden, const float* __restrict__ hs_scale, int T,
+    const uint8_t* __restrict__ w1, const float* __restrict__ s1,
+    const int4* __restrict__ tiles, const int* __restrict__ num_tiles,
+    const int* __restrict__ sorted_tok, uint16_t* __restrict__ inter) {
+    constexpr int BM = 128;                     // token rows per tile
+    constexpr int NG = kI / 128;                // 16 column groups
+    constexpr int kA = BM * kBlk;               // 16 KB token stage
+    constexpr int kW = 256 * kBlk;              // 32 KB weight stage
+    constexpr int kStage = kA + kW + 4 * 256;   // + per-wave token-scale rows
+    constexpr int kVm = 13;                     // per K block: 4 + 8 + 1 DMA
+    static_assert((NS - 1) * kVm < 64, "ring too deep for vmcnt");
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * kStage];
+
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int r16 = lane & 15, kq = lane >> 4;
+    const int wm = wave >> 1, wn = wave & 1;   // token half, weight half
+    const v4f zero = {0.f, 0.f, 0.f, 0.f};
+    const int nitems = (*num_tiles) * NG;
+
+    // XCD-aware mapping: round r covers items [r*G, (r+1)*G); XCD x = blockIdx % 8
+    // takes the contiguous slice x*(G/8) .. of that round.
+    const int G = gridDim.x;
+    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, per = G >> 3;
+
+    const int drow = lane >> 3, dchunk = lane & 7;
+    const int swz = swz128(r16);
+    const int c0 = ((2 * kq) ^ swz) << 4, c1 = ((2 * kq + 1) ^ swz) << 4;
+
+    for (int round = 0; round * G < nitems; ++round) {
+        const int item = round * G + xcd * per + slot;
+        if (item >= nitems) continue;            // uniform per workgroup
+        int tix, ng;
+        grouped_item(item, *num_tiles, NG, tix, ng);
+        const int4 tile = tiles[tix];
+        const int le = tile.x, row0 = tile.y, nrows = tile.z;
+
+        // DMA sources: wave w moves token rows 32w..32w+31 and weight rows
+        // 64w..64w+63 of the stage (rows 0-127 gate, 128-255 up)
+        const uint8_t* asrc[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = 32 * wave + 8 * i + drow;
+            const int tok = sorted_tok[row0 + min(r, nrows - 1)];
+            asrc[i] = hidden + (size_t)tok * kH + ((dchunk ^ swz128(r)) << 4);
+        }
+        const uint8_t* wsrc[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int r = 64 * wave + 8 * i + drow;          // 0..255
+            const int n = (r < 128) ? ng * 128 + r : kI + ng * 128 + (r - 128);
+            wsrc[i] = w1 + (size_t)(le * kN1 + n) * kH + ((dchunk ^ swz128(r)) << 4);
+        }
+        // token scales: lane l of wave w fetches the scale of token 64*wm + l
+        const float* sap = hs_scale + sorted_tok[row0 + min(64 * wm + lane, nrows - 1)];
+        const float* sgp = s1 + (size_t)(le * kN1B + ng) * kHB;
+        const float* sup = sgp + (size_t)kIB * kHB;
+
+        auto issue = [&](int kb) {
+            uint8_t* st = lds + (kb % NS) * kStage;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) dma16(asrc[i] + kb * kBlk, st + (32 * wave + 8 * i) * kBlk);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) dma16(wsrc[i] + kb * kBlk, st + kA + (64 * wave + 8 * i) * kBlk);
+            dma4(sap + (size_t)kb * T, st + kA + kW + wave * 256);
+        };
+
+        v4f acc[4][8];
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[s][j] = zero;
+
+        __syncthreads();   // previous item's reads of the ring are finished
+#pragma unroll
+        for (int kb = 0; kb < NS - 1; ++kb) {
+            issue(kb);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll 1
+        for (int kb = 0; kb < kHB; ++kb) {
+            // wait for this wave's part of stage kb (younger stages stay in flight)
+            if (kb + NS - 1 <= kHB) {
+                static_assert(NS >= 2, "");
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm((NS - 2) * kVm));
+            } else {
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+            }
+            __syncthreads();
+            if (kb + NS - 1 < kHB) issue(kb + NS - 1);
+            __builtin_amdgcn_sched_barrier(0);
+
+            const uint8_t* st = lds + (kb % NS) * kStage;
+            const float fsg = sgp[kb], fsu = sup[kb];
+            v8i bt[4];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const uint8_t* rp = st + (64 * wm + 16 * s + r16) * kBlk;
+                const v4u x0 = *reinterpret_cast<const v4u*>(rp + c0);
+                const v4u x1 = *reinterpret_cast<const v4u*>(rp + c1);
+                bt[s] = v8i{(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
+            }
+            const float* sar = reinterpret_cast<const float*>(st + kA + kW + wave * 256);
+            float fs[4][2];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const float sa = sar[16 * s + r16];
+                fs[s][0] = sa * fsg;
+                fs[s][1] = sa * fsu;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                // weight block j: gate rows 64*wn + 16j (j < 4) or up rows (j >= 4)
+                const int r = (j < 4) ? (64 * wn + 16 * j) : (128 + 64 * wn + 16 * (j - 4));
+                const uint8_t* rp = st + kA + (r + r16) * kBlk;
+                const v4u x0 = *reinterpret_cast<const v4u*>(rp + c0);
+                const v4u x1 = *reinterpret_cast<const v4u*>(rp + c1);
+                const v8i bw = {(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const v4f t = mfma_fp8(bw, bt[s], zero);
+                    const float f = fs[s][j >> 2];
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) acc[s][j][v] = __builtin_fmaf(t[v], f, acc[s][j][v]);
+                }
+            }
+        }
+
+        // epilogue: lane holds D[n = 4*kq + v][token = r16] of each 16 x 16 block
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int r = 64 * wm + 16 * s + r16;
+            if (r < nrows) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    store_swiglu4(inter, row0 + r, ng * 128 + 64 * wn + 16 * j + 4 * kq, acc[s][j], acc[s][j + 4]);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Prefill GEMM1, 8-wave variant: workgroup tile 256 token rows x 256 weight rows
+// (128 gate + 128 up -> 128 SwiGLU columns), waves 4 (tokens) x 2 (weights), each
+// 64 tokens x (64 gate + 64 up) as in gemm1_prefill_kernel.  Two waves per SIMD
+// let one wave's scale FMAs and LDS reads run under the other's MFMAs; registers
+// stay <= 256 per lane for that.  Two 66 KB stages.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(512, 1) void gemm1_prefill8_kernel(
+    const uint8_t* __restrict__ hidden, const float* __restrict__ hs_scale, int T,
+    const uint8_t* __restrict__ w1, const float* __restrict__ s1,
+    const int4* __restrict__ tiles, const int* __restrict__ num_tiles,
+    const int* __restrict__ sorted_tok, uint16_t* __restrict__ inter) {
+    constexpr int NS = 2;
+    constexpr int BM = 256;
+    constexpr int NG = kI / 128;
+    constexpr int kA = BM * kBlk;               // 32 KB token rows
+    constexpr int kW = 256 * kBlk;              // 32 KB weight rows
+    constexpr int kStage = kA + kW + 8 * 256;   // + per-wave token-scale rows
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * kStage];
+
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int r16 = lane & 15, kq = lane >> 4;
+    const int wm = wave >> 1, wn = wave & 1;
+    const v4f zero = {0.f, 0.f, 0.f, 0.f};
+    const int ntl = *num_tiles;
+    const int nitems = ntl * NG;
+    const int G = gridDim.x;
+    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, per = G >> 3;
+    const int drow = lane >> 3, dchunk = lane & 7;
+    const int swz = swz128(r16);
+    const int c0 = ((2 * kq) ^ swz) << 4, c1 = ((2 * kq + 1) ^ swz) << 4;
+
+    for (int round = 0; round * G < nitems; ++round) {
+        const int item = round * G + xcd * per + slot;
+        if (item >= nitems) continue;
+        int tix, ng;
+        grouped_item(item, ntl, NG, tix, ng);
+        const int4 tile = tiles[tix];
+        const int le = tile.x, row0 = tile.y, nrows = tile.z;
+
+        // wave w moves token rows 32w..32w+31 and weight rows 32w..32w+31
+        const uint8_t* asrc[4];
+        const uint8_t* wsrc[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = 32 * wave + 8 * i + drow;
+            const int tok = sorted_tok[row0 + min(r, nrows - 1)];
+            asrc[i] = hidden + (size_t)tok * kH + ((dchunk ^ swz128(r)) << 4);
+            const int n = (r < 128) ? ng * 128 + r : kI + ng * 128 + (r - 128);
+            wsrc[i] = w1 + (size_t)(le * kN1 + n) * kH + ((dchunk ^ swz128(r)) << 4);
+        }
+        const float* sap = hs_scale + sorted_tok[row0 + min(64 * wm + lane, nrows - 1)];
+        const float* sgp = s1 + (size_t)(le * kN1B + ng) * kHB;
+        const float* sup = sgp + (size_t)kIB * kHB;
+
+        auto issue = [&](int kb) {
+            uint8_t* st = lds + (kb & 1) * kStage;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) dma16(asrc[i] + kb * kBlk, st + (32 * wave + 8 * i) * kBlk);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) dma16(wsrc[i] + kb * kBlk, st + kA + (32 * wave + 8 * i) * kBlk);
+            dma4(sap + (size_t)kb * T, st + kA + kW + wave * 256);
+        };
+
+        v4f acc[4][8];
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[s][j] = zero;
+
+        __syncthreads();
+        issue(0);
+#pragma unroll 1
+        for (int kb = 0; kb < kHB; ++kb) {
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+            __syncthreads();
+            if (kb + 1 < kHB) issue(kb + 1);
+            __builtin_amdgcn_sched_barrier(0);
+
+            const uint8_t* st = lds + (kb & 1) * kStage;
+            const float fsg = sgp[kb], fsu = sup[kb];
+            const float* sar = reinterpret_cast<const float*>(st + kA + kW + wave * 256);
+            v8i bt[4];
+            float fg[4], fu[4];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const uint8_t* rp = st + (64 * wm + 16 * s + r16) * kBlk;
+                const v4u x0 = *reinterpret_cast<const v4u*>(rp + c0);
+                const v4u x1 = *reinterpret_cast<const v4u*>(rp + c1);
+                bt[s] = v8i{(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
+                const float sa = sar[16 * s + r16];
+                fg[s] = sa * fsg;
+                fu[s] = sa * fsu;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int r = (j < 4) ? (64 * wn + 16 * j) : (128 + 64 * wn + 16 * (j - 4));
+                const uint8_t* rp = st + kA + (r + r16) * kBlk;
+                const v4u x0 = *reinterpret_cast<const v4u*>(rp + c0);
+                const v4u x1 = *reinterpret_cast<const v4u*>(rp + c1);
+                const v8i bw = {(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const v4f t = mfma_fp8(bw, bt[s], zero);
+                    const float f = (j < 4) ? fg[s] : fu[s];
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) acc[s][j][v] = __builtin_fmaf(t[v], f, acc[s][j][v]);
+                }
+            }
+        }
+
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int r = 64 * wm + 16 * s + r16;
+            if (r < nrows) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    store_swiglu4(inter, row0 + r, ng * 128 + 64 * wn + 16 * j + 4 * kq, acc[s][j], acc[s][j + 4]);
+            }
+        }
+    }
+}
+
 static int grid_for(long long work) { return (int)(work < 4096 ? work : 4096); }
 
 // variant: 0..5 register-ring streaming, 6..11 LDS-landed streaming, both with
-// (CB, KSPLIT) = (1,1) (1,2) (1,4) (2,1) (2,2) (2,4); -1 the 64-row tile kernel
+// (CB, KSPLIT) = (1,1) (1,2) (1,4) (2,1) (2,2) (2,4); 12 the 128-row prefill
+// kernel; -1 the 64-row tile kernel
 bool launch_gemm1(int variant, const uint8_t* hidden, const float* hs_scale, int T,
                   const uint8_t* w1, const float* s1, const int4* tiles, const int* num_tiles,
                   int max_tiles, const int* sorted_tok, uint16_t* inter, hipStream_t stream) {
+    // one resident workgroup per CU (the prefill kernel holds 144 KB of LDS)
+    const int prefill_grid = 256;
     constexpr int G = kI / 16;
     const long long mt = max_tiles;
 #define G1_STREAM(CB, KS, D)                                                                    \
@@ -490,6 +780,14 @@ bool launch_gemm1(int variant, const uint8_t* hidden, const float* hs_scale, int
         case 9: G1_DMA(2, 1, 3); return true;
         case 10: G1_DMA(2, 2, 3); return true;
         case 11: G1_DMA(2, 4, 3); return true;
+        case 12:
+            hipLaunchKernelGGL(gemm1_prefill_kernel<3>, dim3(prefill_grid), dim3(256), 0, stream,
+                               hidden, hs_scale, T, w1, s1, tiles, num_tiles, sorted_tok, inter);
+            return true;
+        case 13:
+            hipLaunchKernelGGL(gemm1_prefill8_kernel, dim3(prefill_grid), dim3(512), 0, stream,
+                               hidden, hs_scale, T, w1, s1, tiles, num_tiles, sorted_tok, inter);
+            return true;
         case -1:
             hipLaunchKernelGGL(gemm1_swiglu_kernel<4>, dim3(grid_for(mt * G)), dim3(256), 0, stream,
                                hidden, hs_scale, T, w1, s1, tiles, num_tiles, sorted_tok, inter);

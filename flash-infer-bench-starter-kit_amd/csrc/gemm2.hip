@@ -6,7 +6,9 @@
 // moe_grouped_gemm_fp8.cu:274-322):
 //   O[r, h] = sum_kb sb2[e, h/128, kb] * sum_{i in kb} C[r, i] * W2[e, h, i]
 // C is the bf16 SwiGLU output of GEMM1; W2 e4m3 bytes are widened to bf16 in
-// registers (exact: every e4m3 value is a bf16 value).  The reference re-quantises
+// registers (exact: every e4m3 value is a bf16 value).  Expert rows O stay fp32
+// for the combine: rounding them to bf16 first breaks the 1e-2 tolerance where two
+// large expert rows cancel.  The reference re-quantises
 // C to fp8 per (row, 128) (kernel.cu:1086-1145); keeping C in bf16 keeps GEMM2 within
 // atol = rtol = 1e-2 of the fp32 restatement.
 //
@@ -269,7 +271,7 @@ __global__ __launch_bounds__(256) void gemm2_stream_kernel(
 // columns (W2 rows) of one expert for one row tile, over KB consecutive K blocks.
 // W2 bytes travel HBM -> LDS with global_load_lds_dwordx4, 8 rows x 128 B (full
 // lines) per instruction, into a per-wave ring of NS slots of 16*HF rows x 128 B,
-// row r keeping its 16-byte chunk c at position c ^ ((r >> 1) & 7).  C rows (bf16,
+// row r keeping its 16-byte chunk c at position c ^ swz128(r).  C rows (bf16,
 // L2-resident) come through a register ring of the same depth.  Each K block issues
 // exactly 2*HF DMA + 4*CB loads; an explicit vmcnt keeps the younger blocks in flight
 // (the compiler does not order LDS DMA against LDS reads).
@@ -297,7 +299,7 @@ __global__ __launch_bounds__(256) void gemm2_dma_kernel(
     uint8_t* myring = &ring[wave][0][0];
 
     const int drow = lane >> 3, dchunk = lane & 7;
-    const int swz = (r16 >> 1) & 7;
+    const int swz = swz128(r16);
     const int rd0 = r16 * kBlk + (((2 * kq) ^ swz) << 4);
     const int rd1 = r16 * kBlk + (((2 * kq + 1) ^ swz) << 4);
 
@@ -315,7 +317,7 @@ __global__ __launch_bounds__(256) void gemm2_dma_kernel(
 #pragma unroll
         for (int i = 0; i < 2 * HF; ++i) {
             const int r = 8 * i + drow;                   // 0 .. 16*HF-1
-            const int c = dchunk ^ ((r >> 1) & 7);
+            const int c = dchunk ^ swz128(r);
             dsrc[i] = w2 + (size_t)(le * kH + hg0 * 16 + r) * kI + c * 16;
         }
         const float* sp[HF];
@@ -432,6 +434,148 @@ __global__ __launch_bounds__(256) void gemm2_dma_kernel(
     }
 }
 
+// Prefill GEMM2 (many tokens per expert): MFMA-bound tiling on bf16 MFMA.
+// Workgroup tile: 128 C rows x 128 output columns h0..h0+127 (one W2 row block, so
+// one W2 scale per K block); wave w (2 x 2) computes 64 rows x 64 columns, per K
+// block 4 x 4 blocks x 4 MFMA 16x16x32 whose partial sums are scaled into fp32
+// accumulators.  W2 rows (fp8, 8 rows x 128 B per DMA instruction, chunk swizzle
+// c ^ swz128(r)) and C rows (bf16, 4 rows x 256 B per instruction, chunk
+// swizzle c ^ (r & 15)) land in LDS by global_load_lds_dwordx4 in NS stages; W2
+// bytes are widened to bf16 after the LDS read.  Items are grouped (4 row tiles x
+// all column groups) with an XCD-contiguous mapping, as in the prefill GEMM1.
+template <int NS, int SPLIT>
+__global__ __launch_bounds__(256) void gemm2_prefill_kernel(
+    const uint16_t* __restrict__ inter, const uint8_t* __restrict__ w2,
+    const float* __restrict__ s2, const int4* __restrict__ tiles,
+    const int* __restrict__ num_tiles, float* __restrict__ out_rows) {
+    constexpr int BM = 128;
+    constexpr int NG = kH / 128;                // 56 column groups
+    constexpr int kW = 128 * kBlk;              // 16 KB of W2 rows
+    constexpr int kC = BM * 2 * kBlk;           // 32 KB of C rows
+    constexpr int kStage = kW + kC;
+    constexpr int kVm = 4 + 8;                  // DMA per wave per K block
+    static_assert((NS - 1) * kVm < 64, "ring too deep for vmcnt");
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * kStage];
+
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int r16 = lane & 15, kq = lane >> 4;
+    const int wm = wave >> 1, wn = wave & 1;
+    const v4f zero = {0.f, 0.f, 0.f, 0.f};
+    const int nvt = (*num_tiles) * SPLIT;      // 128-row pieces of the row tiles
+    const int nitems = nvt * NG;
+    const int G = gridDim.x;
+    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, per = G >> 3;
+
+    // W2 read offsets (fp8 row: chunks 2kq, 2kq+1) and C read offsets (bf16 row:
+    // chunks 4kq .. 4kq+3)
+    const int swzw = swz128(r16);
+    const int w0 = ((2 * kq) ^ swzw) << 4, w1o = ((2 * kq + 1) ^ swzw) << 4;
+    int coff[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) coff[j] = ((4 * kq + j) ^ r16) << 4;
+
+    for (int round = 0; round * G < nitems; ++round) {
+        const int item = round * G + xcd * per + slot;
+        if (item >= nitems) continue;
+        int vix, hg;
+        grouped_item(item, nvt, NG, vix, hg);
+        const int4 tile = tiles[vix / SPLIT];
+        const int le = tile.x;
+        const int row0 = tile.y + (vix % SPLIT) * BM;
+        const int nrows = min(BM, tile.z - (vix % SPLIT) * BM);
+        if (nrows <= 0) continue;                // uniform per workgroup
+
+        const uint8_t* wsrc[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = 32 * wave + 8 * i + (lane >> 3);
+            wsrc[i] = w2 + (size_t)(le * kH + hg * 128 + r) * kI + (((lane & 7) ^ swz128(r)) << 4);
+        }
+        const uint8_t* csrc[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int r = 32 * wave + 4 * i + (lane >> 4);
+            const int rr = row0 + min(r, nrows - 1);
+            csrc[i] = reinterpret_cast<const uint8_t*>(inter + (size_t)rr * kI) + (((lane & 15) ^ (r & 15)) << 4);
+        }
+        const float* sbp = s2 + (size_t)(le * kHB + hg) * kIB;
+
+        auto issue = [&](int kb) {
+            uint8_t* st = lds + (kb % NS) * kStage;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) dma16(wsrc[i] + kb * kBlk, st + (32 * wave + 8 * i) * kBlk);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) dma16(csrc[i] + kb * 2 * kBlk, st + kW + (32 * wave + 4 * i) * 2 * kBlk);
+        };
+
+        v4f acc[4][4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[s][j] = zero;
+
+        __syncthreads();
+#pragma unroll
+        for (int kb = 0; kb < NS - 1; ++kb) {
+            issue(kb);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll 1
+        for (int kb = 0; kb < kIB; ++kb) {
+            if (kb + NS - 1 <= kIB) __builtin_amdgcn_s_waitcnt(vmcnt_imm((NS - 2) * kVm));
+            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+            __syncthreads();
+            if (kb + NS - 1 < kIB) issue(kb + NS - 1);
+            __builtin_amdgcn_sched_barrier(0);
+
+            const uint8_t* st = lds + (kb % NS) * kStage;
+            const float sb = sbp[kb];
+            // C operand blocks (4 x 16 rows of this wave's 64), 4 MFMA slices each
+            v8bf cf[4][4];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const uint8_t* rp = st + kW + (64 * wm + 16 * s + r16) * 2 * kBlk;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) cf[s][j] = __builtin_bit_cast(v8bf, *reinterpret_cast<const v4u*>(rp + coff[j]));
+            }
+#pragma unroll
+            for (int n = 0; n < 4; ++n) {
+                const uint8_t* rp = st + (64 * wn + 16 * n + r16) * kBlk;
+                const v4u x0 = *reinterpret_cast<const v4u*>(rp + w0);
+                const v4u x1 = *reinterpret_cast<const v4u*>(rp + w1o);
+                const uint32_t ww[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+                v8bf wb[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    uint32_t d0, d1, d2, d3;
+                    e4m3x4_to_bf16x4(ww[2 * j], d0, d1);
+                    e4m3x4_to_bf16x4(ww[2 * j + 1], d2, d3);
+                    wb[j] = as_v8bf(d0, d1, d2, d3);
+                }
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    v4f t = zero;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wb[j], cf[s][j], t, 0, 0, 0);
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) acc[s][n][v] = __builtin_fmaf(t[v], sb, acc[s][n][v]);
+                }
+            }
+        }
+
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int r = 64 * wm + 16 * s + r16;
+            if (r < nrows) {
+#pragma unroll
+                for (int n = 0; n < 4; ++n)
+                    *reinterpret_cast<v4f*>(out_rows + (size_t)(row0 + r) * kH + hg * 128 + 64 * wn + 16 * n + 4 * kq) = acc[s][n];
+            }
+        }
+    }
+}
+
 // Debug: widen e4m3 bytes to bf16 with the same conversion GEMM2 uses (n % 4 == 0).
 __global__ void e4m3_to_bf16_kernel(const uint32_t* __restrict__ in, uint2* __restrict__ out, int nwords) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -444,8 +588,8 @@ __global__ void e4m3_to_bf16_kernel(const uint32_t* __restrict__ in, uint2* __re
 static int grid_for2(long long work) { return (int)(work < 4096 ? work : 4096); }
 
 // variant: 0..5 register-ring streaming, 6..11 LDS-landed streaming, both with
-// (CB, KSPLIT, HF) = (1,1,2) (1,2,2) (1,4,1) (2,1,2) (2,2,2) (2,4,1); -1 the 64-row
-// tile kernel
+// (CB, KSPLIT, HF) = (1,1,2) (1,2,2) (1,4,1) (2,1,2) (2,2,2) (2,4,1); 12 the 128-row
+// prefill kernel; -1 the 64-row tile kernel
 bool launch_gemm2(int variant, const uint16_t* inter, const uint8_t* w2, const float* s2,
                   const int4* tiles, const int* num_tiles, int max_tiles, float* out_rows,
                   hipStream_t stream) {
@@ -471,6 +615,14 @@ bool launch_gemm2(int variant, const uint16_t* inter, const uint8_t* w2, const f
         case 9: G2_DMA(2, 1, 3, 2); return true;
         case 10: G2_DMA(2, 2, 3, 2); return true;
         case 11: G2_DMA(2, 4, 3, 1); return true;
+        case 12:
+            hipLaunchKernelGGL((gemm2_prefill_kernel<3, 1>), dim3(256), dim3(256), 0, stream, inter,
+                               w2, s2, tiles, num_tiles, out_rows);
+            return true;
+        case 13:  // 256-row tiles, each processed as two 128-row pieces
+            hipLaunchKernelGGL((gemm2_prefill_kernel<3, 2>), dim3(256), dim3(256), 0, stream, inter,
+                               w2, s2, tiles, num_tiles, out_rows);
+            return true;
         case -1:
             hipLaunchKernelGGL(gemm2_kernel<4>, dim3(grid_for2(mt * (kH / 16))), dim3(256), 0, stream,
                                inter, w2, s2, tiles, num_tiles, out_rows);

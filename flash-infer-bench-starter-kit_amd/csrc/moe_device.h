@@ -51,10 +51,32 @@ __device__ __forceinline__ float order_bits_inv(uint32_t k) {
     return __uint_as_float(u);
 }
 
+// Chunk swizzle for LDS rows of 128 bytes (8 chunks of 16 B): row r keeps chunk c at
+// position c ^ swz128(r).  For the MFMA operand reads (16 consecutive rows, the same
+// chunk) this puts any 8 consecutive rows on 8 different 16-byte bank groups of a
+// 128-byte bank line, and any 16 on 16 groups of a 256-byte line.
+__device__ __forceinline__ constexpr int swz128(int r) { return ((r >> 1) ^ ((r & 1) << 2)) & 7; }
+
+// Work-item order of the prefill GEMMs: groups of 4 row tiles x all ncol column
+// groups, row tile fastest inside a group (the last group may hold fewer tiles).
+__device__ __forceinline__ void grouped_item(int item, int ntiles, int ncol, int& tile, int& col) {
+    constexpr int GM = 4;
+    const int first = (item / (GM * ncol)) * GM;
+    const int gm = min(ntiles - first, GM);
+    const int in = item - first * ncol;
+    tile = first + in % gm;
+    col = in / gm;
+}
+
 // One global_load_lds_dwordx4: lane L copies the 16 bytes at its own address g to
 // LDS l + 16 L (l must be wave-uniform).
 __device__ __forceinline__ void dma16(const uint8_t* g, uint8_t* l) {
     __builtin_amdgcn_global_load_lds(g, l, 16, 0, 0);
+}
+
+// One global_load_lds_dword: lane L copies the 4 bytes at g to LDS l + 4 L.
+__device__ __forceinline__ void dma4(const void* g, void* l) {
+    __builtin_amdgcn_global_load_lds(g, l, 4, 0, 0);
 }
 
 // s_waitcnt immediate that waits until at most v vector-memory operations are

@@ -56,7 +56,7 @@ class WorkspaceLayout(ctypes.Structure):
     """``moe_mi355_workspace_layout`` of include/moe_mi355.h."""
     _fields_ = [(n, ctypes.c_size_t) for n in (
         "topk_ids", "topk_weights", "inverse_rows", "meta", "tiles", "sorted_tokens",
-        "sorted_weights", "intermediate", "expert_out", "total")] + [
+        "sorted_weights", "chunk_counts", "intermediate", "expert_out", "total")] + [
         ("tile_m", ctypes.c_int32), ("max_tiles", ctypes.c_int32)]
 
 
@@ -71,7 +71,7 @@ def _declare(L: ctypes.CDLL) -> ctypes.CDLL:
         "moe_mi355_workspace_bytes": (SZ, [I32]),
         "moe_mi355_forward": (ctypes.c_int, [ctypes.POINTER(MoeArgs), P]),
         "moe_mi355_route": (ctypes.c_int, [P, P, I32, D, P, P, P]),
-        "moe_mi355_dispatch": (ctypes.c_int, [P, P, I32, I64, I32, P, P, P, P, P, P, P]),
+        "moe_mi355_dispatch": (ctypes.c_int, [P, P, I32, I64, I32, P, P, P, P, P, P, P, P]),
         "moe_mi355_max_tiles": (I32, [I32, I32]),
         "moe_mi355_get_workspace_layout": (ctypes.c_int, [I32, ctypes.POINTER(WorkspaceLayout)]),
         "moe_mi355_profile_begin": (ctypes.c_int, [I32]),
@@ -288,13 +288,15 @@ def dispatch(topk_ids: torch.Tensor, topk_weights: torch.Tensor, local_expert_of
         inv=torch.empty(T, TOP_K, dtype=torch.int32, device=dev),
         tiles=torch.empty(max(1, mt), 4, dtype=torch.int32, device=dev),
         num_tiles=torch.empty(1, dtype=torch.int32, device=dev),
+        chunk_counts=torch.empty(max(1, (T + 1023) // 1024) * E_LOCAL, dtype=torch.int32, device=dev),
     )
     with torch.cuda.device(dev):
         rc = L.moe_mi355_dispatch(ids.data_ptr(), w.data_ptr(), T, int(local_expert_offset),
                                   int(tile_m), out["exp_off"].data_ptr(),
                                   out["sorted_tok"].data_ptr(), out["sorted_w"].data_ptr(),
                                   out["inv"].data_ptr(), out["tiles"].data_ptr(),
-                                  out["num_tiles"].data_ptr(), ctypes.c_void_p(_stream_ptr(dev)))
+                                  out["num_tiles"].data_ptr(), out["chunk_counts"].data_ptr(),
+                                  ctypes.c_void_p(_stream_ptr(dev)))
     _check(rc, "moe_mi355_dispatch")
     return out
 

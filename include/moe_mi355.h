@@ -114,12 +114,13 @@ MOE_MI355_API int moe_mi355_route(const float* routing_logits, const uint16_t* r
  *   tiles          int32 [moe_mi355_max_tiles(T,tile_m), 4]  (expert, first row,
  *                               rows, 0) per tile of <= tile_m rows
  *   num_tiles      int32 [1]
- * tile_m must be 16, 32 or 64. */
+ *   chunk_counts   int32 [ceil(T/1024) * 32] scratch (may be NULL when T <= 1024)
+ * tile_m must be 16, 32, 64, 128 or 256. */
 MOE_MI355_API int moe_mi355_dispatch(const int32_t* topk_ids, const float* topk_weights, int32_t T,
                        int64_t local_expert_offset, int32_t tile_m,
                        int32_t* expert_offsets, int32_t* sorted_tokens,
                        float* sorted_weights, int32_t* inverse_rows, int32_t* tiles,
-                       int32_t* num_tiles, void* stream);
+                       int32_t* num_tiles, int32_t* chunk_counts, void* stream);
 
 /* Upper bound on the number of row tiles for T tokens and tile height tile_m. */
 MOE_MI355_API int32_t moe_mi355_max_tiles(int32_t T, int32_t tile_m);
@@ -134,6 +135,7 @@ typedef struct moe_mi355_workspace_layout {
     size_t tiles;           /* int32 [max_tiles,4] */
     size_t sorted_tokens;   /* int32 [8T] */
     size_t sorted_weights;  /* fp32  [8T] */
+    size_t chunk_counts;    /* int32 [ceil(T/1024), 32] dispatch scratch */
     size_t intermediate;    /* bf16  [8T, 2048]  SwiGLU output rows */
     size_t expert_out;      /* fp32  [8T, 7168]  GEMM2 output rows */
     size_t total;

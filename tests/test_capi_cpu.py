@@ -51,7 +51,7 @@ def test_workspace_bytes(lib):
     lay = k.workspace_layout(64)
     assert lay.total == sizes[3]
     offs = [lay.topk_ids, lay.topk_weights, lay.inverse_rows, lay.meta, lay.tiles,
-            lay.sorted_tokens, lay.sorted_weights, lay.intermediate, lay.expert_out]
+            lay.sorted_tokens, lay.sorted_weights, lay.chunk_counts, lay.intermediate, lay.expert_out]
     assert offs == sorted(offs) and all(o % 256 == 0 for o in offs)
     assert lay.expert_out + 64 * 8 * 7168 * 4 <= lay.total
     assert lay.max_tiles == (64 * 8 + 15) // 16 + 32   # sized for the smallest tile height
@@ -81,7 +81,7 @@ def test_forward_rejects_bad_arguments_without_a_gpu(lib):
     a.workspace = fake
     a.workspace_bytes = 100
     assert lib.moe_mi355_forward(ctypes.byref(a), None) == -3  # too small
-    assert lib.moe_mi355_dispatch(None, None, 4, 0, 48, None, None, None, None, None, None, None) == -6
+    assert lib.moe_mi355_dispatch(None, None, 4, 0, 48, None, None, None, None, None, None, None, None) == -6
     assert lib.moe_mi355_route(None, None, -1, 1.0, None, None, None) == -2
     assert lib.moe_mi355_strerror(-3).decode().startswith("workspace")
     assert lib.moe_mi355_debug_e4m3_to_bf16(None, None, 4, None) == -1

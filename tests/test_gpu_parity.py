@@ -90,7 +90,7 @@ def test_route_edge_cases(case):
 
 
 @pytest.mark.parametrize("idx", CFG_IDS)
-@pytest.mark.parametrize("tile_m", [16, 64])
+@pytest.mark.parametrize("tile_m", [16, 64, 256])
 def test_dispatch_bit_exact(idx, tile_m):
     k = pkg("kernel")
     o = oracle()
