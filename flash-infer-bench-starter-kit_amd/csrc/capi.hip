@@ -7,7 +7,7 @@
 // allocation:
 //   route    (T/4 workgroups)      -> topk ids / weights
 //   dispatch (1 workgroup)         -> expert offsets, row tiles, permutation, inverse map
-//   gemm1    (persistent)          -> bf16 SwiGLU rows   [N_a, 2048]
+//   gemm1    (persistent)          -> SwiGLU rows C      [N_a, 2048] (bf16 or fp8 hi/lo)
 //   gemm2    (persistent)          -> fp32 expert rows   [N_a, 7168]
 //   combine  (7 T workgroups)      -> bf16 output        [T, 7168]
 // The GEMM grids are sized from the host-known bound on the tile count; each
@@ -26,8 +26,8 @@ bool launch_dispatch(const int*, const float*, int, int, int, int*, int*, int4*,
                      int*, int*, hipStream_t);
 int dispatch_max_tiles(int T, int tm);
 bool launch_gemm1(int, const uint8_t*, const float*, int, const uint8_t*, const float*,
-                  const int4*, const int*, int, const int*, uint16_t*, hipStream_t);
-bool launch_gemm2(int, const uint16_t*, const uint8_t*, const float*, const int4*, const int*,
+                  const int4*, const int*, int, const int*, const Intermediate&, hipStream_t);
+bool launch_gemm2(int, const Intermediate&, const uint8_t*, const float*, const int4*, const int*,
                   int, float*, hipStream_t);
 void launch_combine(const float*, const float*, const int*, int, uint16_t*, hipStream_t);
 void launch_e4m3_to_bf16(const uint8_t*, uint16_t*, int, hipStream_t);
@@ -35,14 +35,17 @@ void launch_e4m3_to_bf16(const uint8_t*, uint16_t*, int, hipStream_t);
 
 namespace {
 
-constexpr int32_t kMaxT = 1 << 20;      // keeps every row index inside int32
+// Largest T: 8T rows stay inside int32 and T * 7168 (the byte offset of the last
+// token row, used as a 32-bit buffer offset by the prefill kernels) below 2^32.
+constexpr int32_t kMaxT = 1 << 19;
 constexpr int kMinTileM = 16;           // smallest row tile; sizes the tile list
 
 // Kernel plan per token count.  Small T streams weights through LDS with the
-// DMA kernels (row tiles of 16 or 32 rows); large T uses the 128-row MFMA-bound
-// prefill kernels.
+// DMA kernels (row tiles of 16 or 32 rows, C in bf16); large T uses the MFMA-bound
+// prefill kernels (128- or 256-row tiles, C in the fp8 hi/lo form).
 // Variant ids are those of launch_gemm1 / launch_gemm2; MOE_MI355_G1 / MOE_MI355_G2
-// override them for tuning sweeps (ignored unless both imply the same tile height).
+// override them for tuning sweeps (ignored unless both imply the same tile height
+// and the same form of C).
 struct Plan {
     int tm, g1, g2;
 };
@@ -53,6 +56,8 @@ int variant_tile_m(int v) {
     if (v == 13) return 256;
     return (v % 6) < 3 ? 16 : 32;
 }
+
+bool variant_c_hilo(int v) { return v == 12 || v == 13; }
 
 Plan choose_plan(int32_t T) {
     Plan p;
@@ -65,7 +70,8 @@ Plan choose_plan(int32_t T) {
     const int env_g1 = e1 ? atoi(e1) : -99;
     const int env_g2 = e2 ? atoi(e2) : -99;
     if (env_g1 >= -1 && env_g1 <= 13 && env_g2 >= -1 && env_g2 <= 13 &&
-        variant_tile_m(env_g1) == variant_tile_m(env_g2))
+        variant_tile_m(env_g1) == variant_tile_m(env_g2) &&
+        variant_c_hilo(env_g1) == variant_c_hilo(env_g2))
         p = {variant_tile_m(env_g1), env_g1, env_g2};
     return p;
 }
@@ -93,10 +99,13 @@ bool fill_layout(int32_t T, moe_mi355_workspace_layout* L) {
     L->sorted_weights = take(R * 4);
     L->chunk_counts = take((size_t)((T + 1023) / 1024) * moe::kEL * 4);
     L->intermediate = take(R * moe::kI * 2);
+    L->intermediate_scales = take(R * moe::kIB * 4);
     L->expert_out = take(R * moe::kH * 4);
     L->total = off;
-    L->tile_m = choose_plan(T).tm;
+    const Plan plan = choose_plan(T);
+    L->tile_m = plan.tm;
     L->max_tiles = mt;
+    L->intermediate_format = variant_c_hilo(plan.g1) ? 1 : 0;
     return true;
 }
 
@@ -224,7 +233,8 @@ int moe_mi355_forward(const moe_mi355_args* a, void* stream) {
     int4* tiles = reinterpret_cast<int4*>(ws + L.tiles);
     int* stok = reinterpret_cast<int*>(ws + L.sorted_tokens);
     float* sw = reinterpret_cast<float*>(ws + L.sorted_weights);
-    uint16_t* inter = reinterpret_cast<uint16_t*>(ws + L.intermediate);
+    const moe::Intermediate inter{ws + L.intermediate, reinterpret_cast<float*>(ws + L.intermediate_scales),
+                                  T * moe::kTopK};
     float* rows = reinterpret_cast<float*>(ws + L.expert_out);
     int* chunk_cnt = reinterpret_cast<int*>(ws + L.chunk_counts);
     int* num_tiles = meta + moe::kEL + 1;

@@ -5,7 +5,8 @@
 // mainloop):
 //   G1[r, n] = sum_kb sa[kb, tok(r)] * sb[e, n/128, kb] * sum_{k in kb} A[tok(r), k] W1[e, n, k]
 //   C[r, i]  = silu(G1[r, 2048 + i]) * G1[r, i]        (kernel.cu:1104-1108 convention)
-// C is written as bf16 rows (one per routed assignment) for GEMM2.
+// C is written as one row per routed assignment for GEMM2: bf16 by the decode
+// kernels, the fp8 hi/lo form (moe_device.h, Intermediate) by the prefill kernels.
 //
 // Work item = (row tile of <= 16*MAXCB rows of one expert, group of 16 gate rows
 // n..n+15 paired with the 16 up rows 2048+n..).  The 4 waves of a workgroup split
@@ -460,6 +461,76 @@ __global__ __launch_bounds__(256) void gemm1_dma_kernel(
     }
 }
 
+// Four floats -> four e4m3 bytes (v_cvt_pk_fp8_f32: round to nearest even, OCP e4m3fn,
+// the same rounding as torch's float8_e4m3fn cast; inputs are clamped to +-448
+// beforehand so nothing overflows to NaN).
+__device__ __forceinline__ uint32_t e4m3x4_from_f32(float a, float b, float c, float d) {
+    int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+    return (uint32_t)w;
+}
+
+__device__ __forceinline__ float clamp448(float x) { return fminf(fmaxf(x, -448.f), 448.f); }
+
+// Epilogue of the prefill GEMM1 kernels: SwiGLU, then the fp8 hi/lo form of C.
+// The wave holds 64 rows x 64 SwiGLU columns (acc[s][j]: j < 4 gate, j >= 4 up; lane
+// holds D[col 16j + 4kq + v][row 16s + r16]); its partner wave (wn ^ 1) holds the other
+// 64 columns of the 128-column block ng, so the row amax is combined across the two
+// through LDS (xch, 2 KB, reusing the operand ring: every wave must have left the
+// K loop, hence the first barrier).  Per row: s = amax/448 (1 for an all-zero row),
+// hi = e4m3(c * 448/amax), lo = e4m3((c - hi*s) * 16*448/amax).
+__device__ __forceinline__ void store_c_hilo(const v4f (&acc)[4][8], float* xch, int wm, int wn,
+                                             int kq, int r16, int row0, int nrows, int ng,
+                                             const Intermediate& C) {
+    float c[4][4][4];
+    float m[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        m[s] = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                c[s][j][v] = silu_f32(acc[s][j + 4][v]) * acc[s][j][v];
+                m[s] = fmaxf(m[s], fabsf(c[s][j][v]));
+            }
+        m[s] = fmaxf(m[s], __shfl_xor(m[s], 16));
+        m[s] = fmaxf(m[s], __shfl_xor(m[s], 32));
+    }
+    __syncthreads();
+    if (kq == 0) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) xch[(wm * 2 + wn) * 64 + 16 * s + r16] = m[s];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const float amax = fmaxf(m[s], xch[(wm * 2 + (wn ^ 1)) * 64 + 16 * s + r16]);
+        const int r = 64 * wm + 16 * s + r16;
+        if (r >= nrows) continue;
+        const float sc = amax > 0.f ? amax / 448.f : 1.f;
+        const float inv = amax > 0.f ? 448.f / amax : 1.f;
+        const float inv16 = inv * 16.f;
+        const size_t off = (size_t)(row0 + r) * kI + ng * 128 + 64 * wn + 4 * kq;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float* x = c[s][j];
+            const uint32_t h = e4m3x4_from_f32(clamp448(x[0] * inv), clamp448(x[1] * inv),
+                                               clamp448(x[2] * inv), clamp448(x[3] * inv));
+            const auto h01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)h, false);
+            const auto h23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)h, true);
+            const float hv[4] = {h01[0], h01[1], h23[0], h23[1]};
+            float lq[4];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) lq[v] = clamp448(__builtin_fmaf(-hv[v], sc, x[v]) * inv16);
+            const uint32_t l = e4m3x4_from_f32(lq[0], lq[1], lq[2], lq[3]);
+            *reinterpret_cast<uint32_t*>(C.hi() + off + 16 * j) = h;
+            *reinterpret_cast<uint32_t*>(C.lo() + off + 16 * j) = l;
+        }
+        if (wn == 0 && kq == 0) C.scales[(size_t)ng * C.rows_cap + row0 + r] = sc;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Prefill GEMM1 (many tokens per expert): MFMA-bound tiling.
 //
@@ -485,7 +556,7 @@ __global__ __launch_bounds__(256) void gemm1_prefill_kernel(
     const uint8_t* __restrict__ hidden, const float* __restrict__ hs_scale, int T,
     const uint8_t* __restrict__ w1, const float* __restrict__ s1,
     const int4* __restrict__ tiles, const int* __restrict__ num_tiles,
-    const int* __restrict__ sorted_tok, uint16_t* __restrict__ inter) {
+    const int* __restrict__ sorted_tok, Intermediate C) {
     constexpr int BM = 128;                     // token rows per tile
     constexpr int NG = kI / 128;                // 16 column groups
     constexpr int kA = BM * kBlk;               // 16 KB token stage
@@ -611,15 +682,7 @@ __global__ __launch_bounds__(256) void gemm1_prefill_kernel(
         }
 
         // epilogue: lane holds D[n = 4*kq + v][token = r16] of each 16 x 16 block
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const int r = 64 * wm + 16 * s + r16;
-            if (r < nrows) {
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    store_swiglu4(inter, row0 + r, ng * 128 + 64 * wn + 16 * j + 4 * kq, acc[s][j], acc[s][j + 4]);
-            }
-        }
+        store_c_hilo(acc, reinterpret_cast<float*>(lds), wm, wn, kq, r16, row0, nrows, ng, C);
     }
 }
 
@@ -629,18 +692,26 @@ __global__ __launch_bounds__(256) void gemm1_prefill_kernel(
 // 64 tokens x (64 gate + 64 up) as in gemm1_prefill_kernel.  Two waves per SIMD
 // let one wave's scale FMAs and LDS reads run under the other's MFMAs; registers
 // stay <= 256 per lane for that.  Two 66 KB stages.
+//
+// Operand DMA is buffer_load ... lds (addresses in SGPR resources, 32-bit lane
+// offsets, the K step in the scalar offset), issued in two bursts per K block:
+// the token rows right after the barrier, the weight rows and token scales after
+// the third weight block's MFMAs, so the texture path is not flooded at once.
+// Each weight operand is read from LDS one block ahead of its MFMAs.
+// Token offsets are 32-bit: T * 7168 < 2^32 (T <= 2^19, checked by the host).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(512, 1) void gemm1_prefill8_kernel(
     const uint8_t* __restrict__ hidden, const float* __restrict__ hs_scale, int T,
     const uint8_t* __restrict__ w1, const float* __restrict__ s1,
     const int4* __restrict__ tiles, const int* __restrict__ num_tiles,
-    const int* __restrict__ sorted_tok, uint16_t* __restrict__ inter) {
+    const int* __restrict__ sorted_tok, Intermediate C) {
     constexpr int NS = 2;
     constexpr int BM = 256;
     constexpr int NG = kI / 128;
     constexpr int kA = BM * kBlk;               // 32 KB token rows
     constexpr int kW = 256 * kBlk;              // 32 KB weight rows
     constexpr int kStage = kA + kW + 8 * 256;   // + per-wave token-scale rows
+    constexpr int kWeightBurstAfter = 2;        // weight block after which burst 2 goes
     __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * kStage];
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -655,6 +726,8 @@ __global__ __launch_bounds__(512, 1) void gemm1_prefill8_kernel(
     const int drow = lane >> 3, dchunk = lane & 7;
     const int swz = swz128(r16);
     const int c0 = ((2 * kq) ^ swz) << 4, c1 = ((2 * kq + 1) ^ swz) << 4;
+    const __amdgpu_buffer_rsrc_t rs_tok = buffer_rsrc(hidden, (uint32_t)T * kH);
+    const __amdgpu_buffer_rsrc_t rs_sca = buffer_rsrc(hs_scale, (uint32_t)T * kHB * 4);
 
     for (int round = 0; round * G < nitems; ++round) {
         const int item = round * G + xcd * per + slot;
@@ -663,29 +736,32 @@ __global__ __launch_bounds__(512, 1) void gemm1_prefill8_kernel(
         grouped_item(item, ntl, NG, tix, ng);
         const int4 tile = tiles[tix];
         const int le = tile.x, row0 = tile.y, nrows = tile.z;
+        const __amdgpu_buffer_rsrc_t rs_w = buffer_rsrc(w1 + (size_t)le * kN1 * kH, (uint32_t)kN1 * kH);
 
         // wave w moves token rows 32w..32w+31 and weight rows 32w..32w+31
-        const uint8_t* asrc[4];
-        const uint8_t* wsrc[4];
+        uint32_t aoff[4], woff[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int r = 32 * wave + 8 * i + drow;
             const int tok = sorted_tok[row0 + min(r, nrows - 1)];
-            asrc[i] = hidden + (size_t)tok * kH + ((dchunk ^ swz128(r)) << 4);
+            aoff[i] = (uint32_t)tok * kH + ((dchunk ^ swz128(r)) << 4);
             const int n = (r < 128) ? ng * 128 + r : kI + ng * 128 + (r - 128);
-            wsrc[i] = w1 + (size_t)(le * kN1 + n) * kH + ((dchunk ^ swz128(r)) << 4);
+            woff[i] = (uint32_t)n * kH + ((dchunk ^ swz128(r)) << 4);
         }
-        const float* sap = hs_scale + sorted_tok[row0 + min(64 * wm + lane, nrows - 1)];
+        const uint32_t soff = (uint32_t)sorted_tok[row0 + min(64 * wm + lane, nrows - 1)] * 4;
         const float* sgp = s1 + (size_t)(le * kN1B + ng) * kHB;
         const float* sup = sgp + (size_t)kIB * kHB;
 
-        auto issue = [&](int kb) {
+        auto issue_tokens = [&](int kb) {
             uint8_t* st = lds + (kb & 1) * kStage;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) dma16(asrc[i] + kb * kBlk, st + (32 * wave + 8 * i) * kBlk);
+            for (int i = 0; i < 4; ++i) bdma16(rs_tok, aoff[i], (uint32_t)kb * kBlk, st + (32 * wave + 8 * i) * kBlk);
+        };
+        auto issue_weights = [&](int kb) {
+            uint8_t* st = lds + (kb & 1) * kStage;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) dma16(wsrc[i] + kb * kBlk, st + kA + (32 * wave + 8 * i) * kBlk);
-            dma4(sap + (size_t)kb * T, st + kA + kW + wave * 256);
+            for (int i = 0; i < 4; ++i) bdma16(rs_w, woff[i], (uint32_t)kb * kBlk, st + kA + (32 * wave + 8 * i) * kBlk);
+            bdma4(rs_sca, soff, (uint32_t)kb * T * 4, st + kA + kW + wave * 256);
         };
 
         v4f acc[4][8];
@@ -695,12 +771,13 @@ __global__ __launch_bounds__(512, 1) void gemm1_prefill8_kernel(
             for (int j = 0; j < 8; ++j) acc[s][j] = zero;
 
         __syncthreads();
-        issue(0);
+        issue_tokens(0);
+        issue_weights(0);
 #pragma unroll 1
         for (int kb = 0; kb < kHB; ++kb) {
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
             __syncthreads();
-            if (kb + 1 < kHB) issue(kb + 1);
+            if (kb + 1 < kHB) issue_tokens(kb + 1);
             __builtin_amdgcn_sched_barrier(0);
 
             const uint8_t* st = lds + (kb & 1) * kStage;
@@ -718,13 +795,24 @@ __global__ __launch_bounds__(512, 1) void gemm1_prefill8_kernel(
                 fg[s] = sa * fsg;
                 fu[s] = sa * fsu;
             }
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
+            auto read_w = [&](int j) {
                 const int r = (j < 4) ? (64 * wn + 16 * j) : (128 + 64 * wn + 16 * (j - 4));
                 const uint8_t* rp = st + kA + (r + r16) * kBlk;
                 const v4u x0 = *reinterpret_cast<const v4u*>(rp + c0);
                 const v4u x1 = *reinterpret_cast<const v4u*>(rp + c1);
-                const v8i bw = {(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
+                return v8i{(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
+            };
+            v8i bw_next = read_w(0);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                __builtin_amdgcn_sched_barrier(0);
+                const v8i bw = bw_next;
+                if (j < 7) bw_next = read_w(j + 1);
+                if (j == kWeightBurstAfter && kb + 1 < kHB) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    issue_weights(kb + 1);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
 #pragma unroll
                 for (int s = 0; s < 4; ++s) {
                     const v4f t = mfma_fp8(bw, bt[s], zero);
@@ -735,26 +823,20 @@ __global__ __launch_bounds__(512, 1) void gemm1_prefill8_kernel(
             }
         }
 
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const int r = 64 * wm + 16 * s + r16;
-            if (r < nrows) {
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    store_swiglu4(inter, row0 + r, ng * 128 + 64 * wn + 16 * j + 4 * kq, acc[s][j], acc[s][j + 4]);
-            }
-        }
+        store_c_hilo(acc, reinterpret_cast<float*>(lds), wm, wn, kq, r16, row0, nrows, ng, C);
     }
 }
 
 static int grid_for(long long work) { return (int)(work < 4096 ? work : 4096); }
 
 // variant: 0..5 register-ring streaming, 6..11 LDS-landed streaming, both with
-// (CB, KSPLIT) = (1,1) (1,2) (1,4) (2,1) (2,2) (2,4); 12 the 128-row prefill
-// kernel; -1 the 64-row tile kernel
+// (CB, KSPLIT) = (1,1) (1,2) (1,4) (2,1) (2,2) (2,4) and bf16 C; 12 the 128-row and
+// 13 the 256-row prefill kernel, both writing C in the fp8 hi/lo form; -1 the
+// 64-row tile kernel (bf16 C)
 bool launch_gemm1(int variant, const uint8_t* hidden, const float* hs_scale, int T,
                   const uint8_t* w1, const float* s1, const int4* tiles, const int* num_tiles,
-                  int max_tiles, const int* sorted_tok, uint16_t* inter, hipStream_t stream) {
+                  int max_tiles, const int* sorted_tok, const Intermediate& C, hipStream_t stream) {
+    uint16_t* inter = C.bf16();
     // one resident workgroup per CU (the prefill kernel holds 144 KB of LDS)
     const int prefill_grid = 256;
     constexpr int G = kI / 16;
@@ -782,11 +864,11 @@ bool launch_gemm1(int variant, const uint8_t* hidden, const float* hs_scale, int
         case 11: G1_DMA(2, 4, 3); return true;
         case 12:
             hipLaunchKernelGGL(gemm1_prefill_kernel<3>, dim3(prefill_grid), dim3(256), 0, stream,
-                               hidden, hs_scale, T, w1, s1, tiles, num_tiles, sorted_tok, inter);
+                               hidden, hs_scale, T, w1, s1, tiles, num_tiles, sorted_tok, C);
             return true;
         case 13:
             hipLaunchKernelGGL(gemm1_prefill8_kernel, dim3(prefill_grid), dim3(512), 0, stream,
-                               hidden, hs_scale, T, w1, s1, tiles, num_tiles, sorted_tok, inter);
+                               hidden, hs_scale, T, w1, s1, tiles, num_tiles, sorted_tok, C);
             return true;
         case -1:
             hipLaunchKernelGGL(gemm1_swiglu_kernel<4>, dim3(grid_for(mt * G)), dim3(256), 0, stream,

@@ -1,4 +1,5 @@
-// gemm2.hip -- grouped GEMM2 (2048 -> 7168) on bf16 MFMA.
+// gemm2.hip -- grouped GEMM2 (2048 -> 7168): bf16 MFMA for the decode kernels, FP8
+// MFMA on the hi/lo form of C for the prefill kernel.
 //
 // Semantics: reference solution/cuda/moe.cu:231 (O = C @ W2[e]^T) with the 128x128
 // block scales of gemm2_weights_scale applied per K block in the fp32 accumulator
@@ -434,50 +435,53 @@ __global__ __launch_bounds__(256) void gemm2_dma_kernel(
     }
 }
 
-// Prefill GEMM2 (many tokens per expert): MFMA-bound tiling on bf16 MFMA.
-// Workgroup tile: 128 C rows x 128 output columns h0..h0+127 (one W2 row block, so
-// one W2 scale per K block); wave w (2 x 2) computes 64 rows x 64 columns, per K
-// block 4 x 4 blocks x 4 MFMA 16x16x32 whose partial sums are scaled into fp32
-// accumulators.  W2 rows (fp8, 8 rows x 128 B per DMA instruction, chunk swizzle
-// c ^ swz128(r)) and C rows (bf16, 4 rows x 256 B per instruction, chunk
-// swizzle c ^ (r & 15)) land in LDS by global_load_lds_dwordx4 in NS stages; W2
-// bytes are widened to bf16 after the LDS read.  Items are grouped (4 row tiles x
-// all column groups) with an XCD-contiguous mapping, as in the prefill GEMM1.
-template <int NS, int SPLIT>
-__global__ __launch_bounds__(256) void gemm2_prefill_kernel(
-    const uint16_t* __restrict__ inter, const uint8_t* __restrict__ w2,
-    const float* __restrict__ s2, const int4* __restrict__ tiles,
-    const int* __restrict__ num_tiles, float* __restrict__ out_rows) {
+// Prefill GEMM2 (many tokens per expert): MFMA-bound tiling on FP8 MFMA with C in
+// the fp8 hi/lo form written by the prefill GEMM1 kernels (C ~ sC * (hi + lo/16)).
+// Per K block and 16 x 16 output block:
+//   t   = mfma(W2, C_hi)                          v_mfma_f32_16x16x128_f8f6f4
+//   t   = mfma_scaled(W2, C_lo, t, B scale 2^-4)  v_mfma_scale_..., E8M0 scale 123:
+//                                                  exact, the products are fp8 x fp8
+//   acc = fma(t, sC[row, kb] * sW2[h/128, kb], acc)
+// so GEMM2 runs at the FP8 rate with no operand widening, and C keeps about 8
+// significant bits (the fp32 SwiGLU value to within 2^-8 of its block maximum).
+// Workgroup tile: 128 C rows x 256 output columns; waves 2 (rows) x 4 (columns),
+// each 64 rows x 64 columns, inside one W2 row block (one W2 scale per K block).
+// Stage (two, 64.5 KB each): C hi rows 16 KB | C lo rows 16 KB | W2 rows 32 KB |
+// C row scales 512 B, all by buffer_load ... lds in two bursts per K block (C after
+// the barrier, W2 after the second column block's MFMAs); rows keep 16-byte chunk c
+// at c ^ swz128(r).  Items (128-row piece, 256-column group) are grouped 4 pieces x
+// all column groups with an XCD-contiguous mapping, as in the prefill GEMM1.
+// SPLIT = 2 processes 256-row tiles as two 128-row pieces.
+template <int SPLIT>
+__global__ __launch_bounds__(512, 1) void gemm2_prefill8_kernel(
+    Intermediate C, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
+    const int4* __restrict__ tiles, const int* __restrict__ num_tiles,
+    float* __restrict__ out_rows) {
+    constexpr int NS = 2;
     constexpr int BM = 128;
-    constexpr int NG = kH / 128;                // 56 column groups
-    constexpr int kW = 128 * kBlk;              // 16 KB of W2 rows
-    constexpr int kC = BM * 2 * kBlk;           // 32 KB of C rows
-    constexpr int kStage = kW + kC;
-    constexpr int kVm = 4 + 8;                  // DMA per wave per K block
-    static_assert((NS - 1) * kVm < 64, "ring too deep for vmcnt");
+    constexpr int NG = kH / 256;                // 28 column groups
+    constexpr int kC = BM * kBlk;               // 16 KB per C half
+    constexpr int kW = 256 * kBlk;              // 32 KB of W2 rows
+    constexpr int kStage = 2 * kC + kW + BM * 4;
+    constexpr int kWeightBurstAfter = 1;
     __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * kStage];
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int r16 = lane & 15, kq = lane >> 4;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave >> 2, wn = wave & 3;
     const v4f zero = {0.f, 0.f, 0.f, 0.f};
-    const int nvt = (*num_tiles) * SPLIT;      // 128-row pieces of the row tiles
+    const int nvt = (*num_tiles) * SPLIT;
     const int nitems = nvt * NG;
     const int G = gridDim.x;
     const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, per = G >> 3;
-
-    // W2 read offsets (fp8 row: chunks 2kq, 2kq+1) and C read offsets (bf16 row:
-    // chunks 4kq .. 4kq+3)
-    const int swzw = swz128(r16);
-    const int w0 = ((2 * kq) ^ swzw) << 4, w1o = ((2 * kq + 1) ^ swzw) << 4;
-    int coff[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) coff[j] = ((4 * kq + j) ^ r16) << 4;
+    const int drow = lane >> 3, dchunk = lane & 7;
+    const int swz = swz128(r16);
+    const int c0 = ((2 * kq) ^ swz) << 4, c1 = ((2 * kq + 1) ^ swz) << 4;
 
     for (int round = 0; round * G < nitems; ++round) {
         const int item = round * G + xcd * per + slot;
-        if (item >= nitems) continue;
+        if (item >= nitems) continue;            // uniform per workgroup
         int vix, hg;
         grouped_item(item, nvt, NG, vix, hg);
         const int4 tile = tiles[vix / SPLIT];
@@ -486,91 +490,110 @@ __global__ __launch_bounds__(256) void gemm2_prefill_kernel(
         const int nrows = min(BM, tile.z - (vix % SPLIT) * BM);
         if (nrows <= 0) continue;                // uniform per workgroup
 
-        const uint8_t* wsrc[4];
+        const __amdgpu_buffer_rsrc_t rs_hi = buffer_rsrc(C.hi() + (size_t)row0 * kI, BM * kI);
+        const __amdgpu_buffer_rsrc_t rs_lo = buffer_rsrc(C.lo() + (size_t)row0 * kI, BM * kI);
+        const __amdgpu_buffer_rsrc_t rs_cs = buffer_rsrc(C.scales + row0, (uint32_t)(kIB * C.rows_cap - row0) * 4);
+        const __amdgpu_buffer_rsrc_t rs_w = buffer_rsrc(w2 + ((size_t)le * kH + hg * 256) * kI, 256 * kI);
+        // wave w moves C rows 16w..16w+15 (hi and lo) and W2 rows 32w..32w+31; waves 0
+        // and 1 move the row scales of rows 64w..64w+63
+        uint32_t coff[2], woff[4];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int r = 16 * wave + 8 * i + drow;
+            coff[i] = (uint32_t)min(r, nrows - 1) * kI + ((dchunk ^ swz128(r)) << 4);
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int r = 32 * wave + 8 * i + (lane >> 3);
-            wsrc[i] = w2 + (size_t)(le * kH + hg * 128 + r) * kI + (((lane & 7) ^ swz128(r)) << 4);
+            const int r = 32 * wave + 8 * i + drow;
+            woff[i] = (uint32_t)r * kI + ((dchunk ^ swz128(r)) << 4);
         }
-        const uint8_t* csrc[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int r = 32 * wave + 4 * i + (lane >> 4);
-            const int rr = row0 + min(r, nrows - 1);
-            csrc[i] = reinterpret_cast<const uint8_t*>(inter + (size_t)rr * kI) + (((lane & 15) ^ (r & 15)) << 4);
-        }
-        const float* sbp = s2 + (size_t)(le * kHB + hg) * kIB;
+        const uint32_t csoff = (uint32_t)min(64 * wave + lane, nrows - 1) * 4;
+        const float* sbp = s2 + (size_t)(le * kHB + 2 * hg + (wn >> 1)) * kIB;
 
-        auto issue = [&](int kb) {
-            uint8_t* st = lds + (kb % NS) * kStage;
+        auto issue_c = [&](int kb) {
+            uint8_t* st = lds + (kb & 1) * kStage;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) dma16(wsrc[i] + kb * kBlk, st + (32 * wave + 8 * i) * kBlk);
+            for (int i = 0; i < 2; ++i) {
+                bdma16(rs_hi, coff[i], (uint32_t)kb * kBlk, st + (16 * wave + 8 * i) * kBlk);
+                bdma16(rs_lo, coff[i], (uint32_t)kb * kBlk, st + kC + (16 * wave + 8 * i) * kBlk);
+            }
+            if (wave < 2) bdma4(rs_cs, csoff, (uint32_t)kb * C.rows_cap * 4, st + 2 * kC + kW + wave * 256);
+        };
+        auto issue_w = [&](int kb) {
+            uint8_t* st = lds + (kb & 1) * kStage;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) dma16(csrc[i] + kb * 2 * kBlk, st + kW + (32 * wave + 4 * i) * 2 * kBlk);
+            for (int i = 0; i < 4; ++i) bdma16(rs_w, woff[i], (uint32_t)kb * kBlk, st + 2 * kC + (32 * wave + 8 * i) * kBlk);
         };
 
         v4f acc[4][4];
 #pragma unroll
         for (int s = 0; s < 4; ++s)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[s][j] = zero;
+            for (int n = 0; n < 4; ++n) acc[s][n] = zero;
 
         __syncthreads();
-#pragma unroll
-        for (int kb = 0; kb < NS - 1; ++kb) {
-            issue(kb);
-            __builtin_amdgcn_sched_barrier(0);
-        }
+        issue_c(0);
+        issue_w(0);
 #pragma unroll 1
         for (int kb = 0; kb < kIB; ++kb) {
-            if (kb + NS - 1 <= kIB) __builtin_amdgcn_s_waitcnt(vmcnt_imm((NS - 2) * kVm));
-            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
             __syncthreads();
-            if (kb + NS - 1 < kIB) issue(kb + NS - 1);
+            if (kb + 1 < kIB) issue_c(kb + 1);
             __builtin_amdgcn_sched_barrier(0);
 
-            const uint8_t* st = lds + (kb % NS) * kStage;
-            const float sb = sbp[kb];
-            // C operand blocks (4 x 16 rows of this wave's 64), 4 MFMA slices each
-            v8bf cf[4][4];
+            const uint8_t* st = lds + (kb & 1) * kStage;
+            const float sw = sbp[kb];
+            const float* csr = reinterpret_cast<const float*>(st + 2 * kC + kW);
+            v8i ch[4], cl[4];
+            float f[4];
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                const uint8_t* rp = st + kW + (64 * wm + 16 * s + r16) * 2 * kBlk;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) cf[s][j] = __builtin_bit_cast(v8bf, *reinterpret_cast<const v4u*>(rp + coff[j]));
+                const int r = 64 * wm + 16 * s + r16;
+                const uint8_t* ph = st + r * kBlk;
+                const uint8_t* pl = st + kC + r * kBlk;
+                const v4u h0 = *reinterpret_cast<const v4u*>(ph + c0);
+                const v4u h1 = *reinterpret_cast<const v4u*>(ph + c1);
+                const v4u l0 = *reinterpret_cast<const v4u*>(pl + c0);
+                const v4u l1 = *reinterpret_cast<const v4u*>(pl + c1);
+                ch[s] = v8i{(int)h0[0], (int)h0[1], (int)h0[2], (int)h0[3], (int)h1[0], (int)h1[1], (int)h1[2], (int)h1[3]};
+                cl[s] = v8i{(int)l0[0], (int)l0[1], (int)l0[2], (int)l0[3], (int)l1[0], (int)l1[1], (int)l1[2], (int)l1[3]};
+                f[s] = csr[r] * sw;
             }
+            auto read_w = [&](int n) {
+                const uint8_t* rp = st + 2 * kC + (64 * wn + 16 * n + r16) * kBlk;
+                const v4u x0 = *reinterpret_cast<const v4u*>(rp + c0);
+                const v4u x1 = *reinterpret_cast<const v4u*>(rp + c1);
+                return v8i{(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
+            };
+            v8i w_next = read_w(0);
 #pragma unroll
             for (int n = 0; n < 4; ++n) {
-                const uint8_t* rp = st + (64 * wn + 16 * n + r16) * kBlk;
-                const v4u x0 = *reinterpret_cast<const v4u*>(rp + w0);
-                const v4u x1 = *reinterpret_cast<const v4u*>(rp + w1o);
-                const uint32_t ww[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-                v8bf wb[4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    uint32_t d0, d1, d2, d3;
-                    e4m3x4_to_bf16x4(ww[2 * j], d0, d1);
-                    e4m3x4_to_bf16x4(ww[2 * j + 1], d2, d3);
-                    wb[j] = as_v8bf(d0, d1, d2, d3);
+                __builtin_amdgcn_sched_barrier(0);
+                const v8i w = w_next;
+                if (n < 3) w_next = read_w(n + 1);
+                if (n == kWeightBurstAfter && kb + 1 < kIB) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    issue_w(kb + 1);
+                    __builtin_amdgcn_sched_barrier(0);
                 }
 #pragma unroll
                 for (int s = 0; s < 4; ++s) {
-                    v4f t = zero;
+                    v4f t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(w, ch[s], zero, 0, 0, 0, 0, 0, 0);
+                    t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(w, cl[s], t, 0, 0, 0, 127, 0, 123);
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wb[j], cf[s][j], t, 0, 0, 0);
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) acc[s][n][v] = __builtin_fmaf(t[v], sb, acc[s][n][v]);
+                    for (int v = 0; v < 4; ++v) acc[s][n][v] = __builtin_fmaf(t[v], f[s], acc[s][n][v]);
                 }
             }
         }
 
+        // lane holds D[h = 64 wn + 16 n + 4 kq + v][row = 64 wm + 16 s + r16]
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             const int r = 64 * wm + 16 * s + r16;
             if (r < nrows) {
 #pragma unroll
                 for (int n = 0; n < 4; ++n)
-                    *reinterpret_cast<v4f*>(out_rows + (size_t)(row0 + r) * kH + hg * 128 + 64 * wn + 16 * n + 4 * kq) = acc[s][n];
+                    *reinterpret_cast<v4f*>(out_rows + (size_t)(row0 + r) * kH + hg * 256 + 64 * wn + 16 * n + 4 * kq) = acc[s][n];
             }
         }
     }
@@ -588,11 +611,13 @@ __global__ void e4m3_to_bf16_kernel(const uint32_t* __restrict__ in, uint2* __re
 static int grid_for2(long long work) { return (int)(work < 4096 ? work : 4096); }
 
 // variant: 0..5 register-ring streaming, 6..11 LDS-landed streaming, both with
-// (CB, KSPLIT, HF) = (1,1,2) (1,2,2) (1,4,1) (2,1,2) (2,2,2) (2,4,1); 12 the 128-row
-// prefill kernel; -1 the 64-row tile kernel
-bool launch_gemm2(int variant, const uint16_t* inter, const uint8_t* w2, const float* s2,
+// (CB, KSPLIT, HF) = (1,1,2) (1,2,2) (1,4,1) (2,1,2) (2,2,2) (2,4,1) and bf16 C; 12 the
+// prefill kernel on 128-row tiles and 13 on 256-row tiles, both reading C in the fp8
+// hi/lo form; -1 the 64-row tile kernel (bf16 C)
+bool launch_gemm2(int variant, const Intermediate& C, const uint8_t* w2, const float* s2,
                   const int4* tiles, const int* num_tiles, int max_tiles, float* out_rows,
                   hipStream_t stream) {
+    const uint16_t* inter = C.bf16();
     const long long mt = max_tiles;
 #define G2_STREAM(CB, KS, D, HF)                                                                  \
     hipLaunchKernelGGL((gemm2_stream_kernel<CB, KS, D, HF>),                                      \
@@ -616,12 +641,12 @@ bool launch_gemm2(int variant, const uint16_t* inter, const uint8_t* w2, const f
         case 10: G2_DMA(2, 2, 3, 2); return true;
         case 11: G2_DMA(2, 4, 3, 1); return true;
         case 12:
-            hipLaunchKernelGGL((gemm2_prefill_kernel<3, 1>), dim3(256), dim3(256), 0, stream, inter,
-                               w2, s2, tiles, num_tiles, out_rows);
+            hipLaunchKernelGGL((gemm2_prefill8_kernel<1>), dim3(256), dim3(512), 0, stream, C, w2,
+                               s2, tiles, num_tiles, out_rows);
             return true;
         case 13:  // 256-row tiles, each processed as two 128-row pieces
-            hipLaunchKernelGGL((gemm2_prefill_kernel<3, 2>), dim3(256), dim3(256), 0, stream, inter,
-                               w2, s2, tiles, num_tiles, out_rows);
+            hipLaunchKernelGGL((gemm2_prefill8_kernel<2>), dim3(256), dim3(512), 0, stream, C, w2,
+                               s2, tiles, num_tiles, out_rows);
             return true;
         case -1:
             hipLaunchKernelGGL(gemm2_kernel<4>, dim3(grid_for2(mt * (kH / 16))), dim3(256), 0, stream,

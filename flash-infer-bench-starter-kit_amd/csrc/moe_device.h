@@ -86,4 +86,46 @@ __device__ __forceinline__ constexpr int vmcnt_imm(int v) {
     return (v & 15) | ((v >> 4) << 14) | (7 << 4) | (15 << 8);
 }
 
+// Raw buffer resource over [base, base + bytes): 32-bit offsets, the address kept in
+// SGPRs (saves the per-lane 64-bit pointers of global_load_lds), out-of-range reads
+// return zero.  Word 3 = 0x00020000: raw (unformatted) 32-bit data, stride 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                             0x00020000);
+}
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// buffer_load_dwordx4 ... lds: lane L copies 16 bytes from voff + soff to LDS l + 16 L.
+__device__ __forceinline__ void bdma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
+                                       void* l) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)l, 16, voff, soff, 0, 0);
+}
+
+// buffer_load_dword ... lds: lane L copies 4 bytes from voff + soff to LDS l + 4 L.
+__device__ __forceinline__ void bdma4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
+                                      void* l) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)l, 4, voff, soff, 0, 0);
+}
+
+// The SwiGLU rows C [rows, 2048] between GEMM1 and GEMM2 live in one workspace
+// region in one of two forms, chosen by the kernel plan:
+//   bf16: C as bf16 rows (decode kernels);
+//   fp8 hi/lo: per row and 128-column block b a scale s = amax/448 and two e4m3
+//     rows hi = e4m3(C/s), lo = e4m3((C - hi*s) * 16/s), so C ~ s*(hi + lo/16)
+//     with about 8 significant bits (prefill kernels; GEMM2 then runs two FP8
+//     MFMAs per block, the second with an exact 2^-4 operand scale).
+// hi occupies the first rows_cap*2048 bytes of the region, lo the next; the scales
+// are fp32 [16, rows_cap] (block-major, so a tile's rows are contiguous).
+struct Intermediate {
+    void* base;
+    float* scales;
+    int rows_cap;
+    __host__ __device__ uint16_t* bf16() const { return static_cast<uint16_t*>(base); }
+    __host__ __device__ uint8_t* hi() const { return static_cast<uint8_t*>(base); }
+    __host__ __device__ uint8_t* lo() const {
+        return static_cast<uint8_t*>(base) + (size_t)rows_cap * kI;
+    }
+};
+
 }  // namespace moe

@@ -56,8 +56,13 @@ class WorkspaceLayout(ctypes.Structure):
     """``moe_mi355_workspace_layout`` of include/moe_mi355.h."""
     _fields_ = [(n, ctypes.c_size_t) for n in (
         "topk_ids", "topk_weights", "inverse_rows", "meta", "tiles", "sorted_tokens",
-        "sorted_weights", "chunk_counts", "intermediate", "expert_out", "total")] + [
-        ("tile_m", ctypes.c_int32), ("max_tiles", ctypes.c_int32)]
+        "sorted_weights", "chunk_counts", "intermediate", "intermediate_scales", "expert_out",
+        "total")] + [
+        ("tile_m", ctypes.c_int32), ("max_tiles", ctypes.c_int32),
+        ("intermediate_format", ctypes.c_int32)]
+
+
+MAX_TOKENS = 1 << 19    # MOE_MI355_MAX_TOKENS
 
 
 FLAG_PROFILE = 1
@@ -157,6 +162,8 @@ def validate(routing_logits, routing_bias, hidden_states, hidden_states_scale, g
     if not isinstance(routing_logits, torch.Tensor) or routing_logits.dim() != 2:
         raise ValueError("routing_logits must be a 2-D tensor [T, 256]")
     T = int(routing_logits.shape[0])
+    if T > MAX_TOKENS:
+        raise ValueError(f"at most {MAX_TOKENS} tokens per call, got {T}")
     dev = routing_logits.device
     tensors = (
         (routing_logits, "routing_logits", torch.float32, (T, E_GLOBAL)),

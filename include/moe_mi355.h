@@ -46,10 +46,13 @@ extern "C" {
 #define MOE_MI355_TOPK_GROUP 4
 #define MOE_MI355_BLOCK 128
 
+/* Largest token count of one call (8T rows stay inside int32 and T * 7168 below 2^32). */
+#define MOE_MI355_MAX_TOKENS 524288
+
 typedef enum moe_mi355_status {
     MOE_OK = 0,
     MOE_ERR_NULL_POINTER = -1,     /* a required pointer is NULL */
-    MOE_ERR_BAD_SIZE = -2,         /* T < 0 or T too large for 32-bit row indices */
+    MOE_ERR_BAD_SIZE = -2,         /* T < 0 or T > MOE_MI355_MAX_TOKENS */
     MOE_ERR_WORKSPACE = -3,        /* workspace NULL, misaligned or too small */
     MOE_ERR_MISALIGNED = -4,       /* a tensor pointer is not 16-byte aligned */
     MOE_ERR_HIP = -5,              /* a HIP launch failed (see moe_mi355_last_hip_error) */
@@ -136,11 +139,17 @@ typedef struct moe_mi355_workspace_layout {
     size_t sorted_tokens;   /* int32 [8T] */
     size_t sorted_weights;  /* fp32  [8T] */
     size_t chunk_counts;    /* int32 [ceil(T/1024), 32] dispatch scratch */
-    size_t intermediate;    /* bf16  [8T, 2048]  SwiGLU output rows */
+    size_t intermediate;    /* SwiGLU output rows C, 8T x 2048 x 2 bytes, in one of two
+                               forms (intermediate_format):
+                               0: bf16 [8T, 2048];
+                               1: fp8 hi/lo: e4m3 hi [8T, 2048] then e4m3 lo [8T, 2048],
+                                  C = s * (hi + lo / 16) with s from intermediate_scales */
+    size_t intermediate_scales; /* fp32 [16, 8T]: s of row r, 128-column block b at [b][r] */
     size_t expert_out;      /* fp32  [8T, 7168]  GEMM2 output rows */
     size_t total;
     int32_t tile_m;
     int32_t max_tiles;
+    int32_t intermediate_format;
 } moe_mi355_workspace_layout;
 
 MOE_MI355_API int moe_mi355_get_workspace_layout(int32_t T, moe_mi355_workspace_layout* out);

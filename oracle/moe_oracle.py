@@ -194,6 +194,47 @@ def silu(x: torch.Tensor) -> torch.Tensor:
     return x * torch.sigmoid(x)
 
 
+def hilo_split(C: torch.Tensor):
+    """The fp8 hi/lo form of the SwiGLU rows used between the prefill GEMMs (the
+    build's own format; the reference re-quantises C to one e4m3 per element with a
+    per-128 scale instead, kernel.cu:1086-1145).
+
+    Per row and 128-column block: ``s = amax/448`` (1 if the block is all zero),
+    ``hi = e4m3(clamp(c * (448/amax)))``, ``lo = e4m3(clamp((c - hi*s) * 16*448/amax))``
+    with ``c - hi*s`` rounded once (an fma).  Returns (hi uint8 [R,2048],
+    lo uint8 [R,2048], s fp32 [R,16])."""
+    C = C.detach().to(torch.float32)
+    R = C.shape[0]
+    b = C.reshape(R, I // BLK, BLK)
+    amax = b.abs().amax(dim=2, keepdim=True)
+    nz = amax > 0
+    s = torch.where(nz, amax / 448.0, torch.ones_like(amax))
+    inv = torch.where(nz, 448.0 / amax, torch.ones_like(amax))
+    hi = (b * inv).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+    res = (b.double() - hi.to(torch.float64) * s.double()).to(torch.float32)
+    lo = (res * (inv * 16.0)).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+    return (hi.view(torch.uint8).reshape(R, I), lo.view(torch.uint8).reshape(R, I),
+            s.reshape(R, I // BLK))
+
+
+def hilo_join(hi: torch.Tensor, lo: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
+    """``s * (e4m3(hi) + e4m3(lo) / 16)`` per 128-column block, fp32 [R, 2048]."""
+    R = hi.shape[0]
+    h = hi.view(torch.float8_e4m3fn).to(torch.float32).reshape(R, I // BLK, BLK)
+    l = lo.view(torch.float8_e4m3fn).to(torch.float32).reshape(R, I // BLK, BLK)
+    return ((h + l / 16.0) * s.reshape(R, I // BLK, 1)).reshape(R, I)
+
+
+def swiglu_rows(hidden_states, hidden_states_scale, gemm1_weights, gemm1_weights_scale,
+                le: int, tokens: Sequence[int]) -> torch.Tensor:
+    """fp32 C rows ``silu(G1[:, I:]) * G1[:, :I]`` of local expert ``le`` for ``tokens``
+    (moe.cu:226-229)."""
+    A = dequant_hidden(hidden_states, hidden_states_scale, torch.as_tensor(list(tokens), dtype=torch.int64))
+    W13 = dequant_weight(gemm1_weights[le], gemm1_weights_scale[le])
+    G1 = A @ W13.t()
+    return silu(G1[:, I:]) * G1[:, :I]
+
+
 def expert_forward(hidden_states, hidden_states_scale, gemm1_weights, gemm1_weights_scale,
                    gemm2_weights, gemm2_weights_scale, ids, w, offset: int,
                    tokens: Optional[Sequence[int]] = None,
@@ -203,7 +244,8 @@ def expert_forward(hidden_states, hidden_states_scale, gemm1_weights, gemm1_weig
     ``tokens`` restricts the computation to a subset of tokens (each output row
     depends only on its own token, so a subset is an exact restatement for those
     rows).  ``intermediate_dtype`` rounds C = silu(x2)*x1 before GEMM2 (fp32 = the
-    reference; bf16/float8 are used to study the precision of a GEMM2 variant)."""
+    reference; bf16, float8 or "hilo" (``hilo_split``) study the precision of the
+    forms the GPU path keeps C in)."""
     ids = torch.as_tensor(_np(ids)).to(torch.int64)
     wt = torch.as_tensor(_np(w)).to(torch.float32)
     T = ids.shape[0]
@@ -226,7 +268,9 @@ def expert_forward(hidden_states, hidden_states_scale, gemm1_weights, gemm1_weig
         W2 = dequant_weight(gemm2_weights[le], gemm2_weights_scale[le])
         G1 = A[sel] @ W13.t()
         C = silu(G1[:, I:]) * G1[:, :I]
-        if intermediate_dtype != torch.float32:
+        if intermediate_dtype == "hilo":
+            C = hilo_join(*hilo_split(C))
+        elif intermediate_dtype != torch.float32:
             C = C.to(intermediate_dtype).to(torch.float32)
         O = C @ W2.t()
         wk = (sub_w[sel] * hit[sel].to(torch.float32)).sum(dim=1, keepdim=True)

@@ -149,3 +149,41 @@ def test_forward_routing_in_workspace_is_bit_exact():
     na = int(r["exp_off"][-1])
     stok = ws[lay.sorted_tokens:lay.sorted_tokens + na * 4].view(torch.int32).cpu().numpy()
     assert np.array_equal(stok, r["sorted_tok"])
+
+
+@pytest.mark.parametrize("idx", [2, 3])
+def test_prefill_intermediate_hilo_rows(idx):
+    """The prefill GEMM1 writes C in the fp8 hi/lo form; rebuilt rows match the fp32
+    SwiGLU of the oracle to within the form's precision (2^-8 relative, plus the
+    fp32 GEMM's own rounding)."""
+    k = pkg("kernel")
+    o = oracle()
+    wl = pkg("workloads")
+    d = config_inputs(idx)
+    T = d["routing_logits"].shape[0]
+    lay = k.workspace_layout(T)
+    assert lay.intermediate_format == 1
+    ws = torch.empty(lay.total, dtype=torch.uint8, device="cuda")
+    out = torch.empty_like(d["output"])
+    note(f"[gpu] hi/lo intermediate config {idx}")
+    k.kernel(*wl.as_args({**d, "output": out}), workspace=ws)
+    torch.cuda.synchronize()
+    R = T * 8
+    exp_off = ws[lay.meta:lay.meta + 33 * 4].view(torch.int32).cpu().numpy()
+    na = int(exp_off[32])
+    stok = ws[lay.sorted_tokens:lay.sorted_tokens + na * 4].view(torch.int32).cpu().numpy()
+    rng = np.random.default_rng(7 + idx)
+    rows = sorted(rng.choice(na, 24, replace=False).tolist())
+    ridx = torch.as_tensor(rows, device="cuda", dtype=torch.int64)
+    hi = ws[lay.intermediate:lay.intermediate + R * 2048].view(R, 2048)[ridx].cpu()
+    lo = ws[lay.intermediate + R * 2048:lay.intermediate + 2 * R * 2048].view(R, 2048)[ridx].cpu()
+    sc = ws[lay.intermediate_scales:lay.intermediate_scales + 16 * R * 4].view(torch.float32).view(16, R)
+    sc = sc[:, ridx].t().contiguous().cpu()
+    got = o.hilo_join(hi, lo, sc)
+    for i, r in enumerate(rows):
+        le = int(np.searchsorted(exp_off, r, side="right") - 1)
+        ref = o.swiglu_rows(d["hidden_states"], d["hidden_states_scale"], d["gemm1_weights"],
+                            d["gemm1_weights_scale"], le, [int(stok[r])])[0]
+        bmax = ref.view(16, 128).abs().amax(dim=1).repeat_interleave(128)
+        err = (got[i] - ref).abs()
+        assert (err <= ref.abs() * 2.0 ** -7 + bmax * 2.0 ** -10).all(), (r, float(err.max()))

@@ -443,3 +443,52 @@ def test_combine_linear_in_factor_and_zero_for_nonlocal():
     nonlocal_tok = [t for t in range(12) if not any(int(e) < 32 for e in ids[t])]
     for t in nonlocal_tok:
         assert (a1[t] == 0).all()
+
+
+# --------------------------------------------------------------------------- fp8 hi/lo form of C
+
+def _hilo_blocks():
+    g = torch.Generator().manual_seed(11)
+    C = torch.randn(48, I, generator=g) * torch.logspace(-3, 2, 48).unsqueeze(1)
+    C[3, :128] = 0.0                                  # an all-zero block
+    C[4, 128:256] = 1e-30                             # a denormal-scale block
+    C[5, 256:384] = torch.linspace(-1, 1, 128)        # exact zero inside a block
+    C[6, ::7] *= 1e-4                                 # elements far below the block max
+    return C
+
+
+def test_hilo_reconstruction_bound():
+    """|s(hi + lo/16) - c| <= 2^-8 |c| + 2^-13 s for every element (lo carries the
+    residual of hi with e4m3's relative precision 2^-4, or its subnormal step)."""
+    o = oracle()
+    C = _hilo_blocks()
+    hi, lo, s = o.hilo_split(C)
+    back = o.hilo_join(hi, lo, s)
+    sfull = s.repeat_interleave(BLK, 1)
+    err = (back - C).abs()
+    assert (err <= C.abs() * 2.0 ** -8 + sfull * 2.0 ** -13).all()
+    assert (back[3, :128] == 0).all()
+
+
+def test_hilo_lo_term_matters():
+    """Dropping lo (a plausible mistake) loses ~4 bits: the pin above then fails."""
+    o = oracle()
+    C = _hilo_blocks()
+    hi, lo, s = o.hilo_split(C)
+    no_lo = o.hilo_join(hi, torch.zeros_like(lo), s)
+    sfull = s.repeat_interleave(BLK, 1)
+    assert not ((no_lo - C).abs() <= C.abs() * 2.0 ** -8 + sfull * 2.0 ** -13).all()
+
+
+def test_hilo_exact_for_representable_values():
+    """Values of the form s * (e4m3 + e4m3/16) with s = amax/448 come back exactly."""
+    o = oracle()
+    codes = torch.arange(0, 126, dtype=torch.uint8)          # positive finite e4m3 codes
+    vals = codes.view(torch.float8_e4m3fn).float()
+    C = torch.zeros(1, I)
+    C[0, :126] = vals                                          # block 0: amax = 448 -> s = 1
+    C[0, 126] = 448.0
+    C[0, 127] = -(1.0 + 1.0 / 16)                              # hi = -1, lo = -1
+    hi, lo, s = o.hilo_split(C)
+    assert float(s[0, 0]) == 1.0
+    assert torch.equal(o.hilo_join(hi, lo, s)[0, :128], C[0, :128])
