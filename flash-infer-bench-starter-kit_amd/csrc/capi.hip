@@ -23,7 +23,7 @@
 namespace moe {
 void launch_route(const float*, const uint16_t*, int, float, int*, float*, hipStream_t);
 bool launch_dispatch(const int*, const float*, int, int, int, int*, int*, int4*, int*, float*,
-                     int*, int*, hipStream_t);
+                     int*, int*, hipStream_t, int*, int4*);
 int dispatch_max_tiles(int T, int tm);
 bool launch_gemm1(int, const uint8_t*, const float*, int, const uint8_t*, const float*,
                   const int4*, const int*, int, const int*, const Intermediate&, hipStream_t);
@@ -94,7 +94,7 @@ bool fill_layout(int32_t T, moe_mi355_workspace_layout* L) {
     L->topk_weights = take(R * 4);
     L->inverse_rows = take(R * 4);
     L->meta = take(64 * 4);
-    L->tiles = take((size_t)mt * 16);
+    L->tiles = take((size_t)mt * 2 * 16);   // room for a second, half-height tile list
     L->sorted_tokens = take(R * 4);
     L->sorted_weights = take(R * 4);
     L->chunk_counts = take((size_t)((T + 1023) / 1024) * moe::kEL * 4);
@@ -201,7 +201,7 @@ int moe_mi355_dispatch(const int32_t* topk_ids, const float* topk_weights, int32
     hipStream_t s = (hipStream_t)stream;
     moe::launch_dispatch(topk_ids, topk_weights, T, clamp_offset(local_expert_offset), tile_m,
                          expert_offsets, num_tiles, reinterpret_cast<int4*>(tiles), sorted_tokens,
-                         sorted_weights, inverse_rows, chunk_counts, s);
+                         sorted_weights, inverse_rows, chunk_counts, s, nullptr, nullptr);
     return hip_status(hipGetLastError());
 }
 
@@ -248,14 +248,23 @@ int moe_mi355_forward(const moe_mi355_args* a, void* stream) {
     if (prof) prof_record(slot, 1, s);
     const Plan plan = choose_plan(T);
     const int max_tiles = moe::dispatch_max_tiles(T, plan.tm);
+    // GEMM2 variant 13 walks the half-height (128-row) tiles of a 256-row dispatch
+    const bool half = plan.g2 == 13;
+    int4* tiles2 = tiles + max_tiles;
+    int* num_tiles2 = meta + moe::kEL + 2;
     moe::launch_dispatch(ids, wts, T, clamp_offset(a->local_expert_offset), plan.tm, meta,
-                         num_tiles, tiles, stok, sw, inv, chunk_cnt, s);
+                         num_tiles, tiles, stok, sw, inv, chunk_cnt, s, half ? num_tiles2 : nullptr,
+                         half ? tiles2 : nullptr);
     if (prof) prof_record(slot, 2, s);
     moe::launch_gemm1(plan.g1, a->hidden_states, a->hidden_states_scale, T, a->gemm1_weights,
                       a->gemm1_weights_scale, tiles, num_tiles, max_tiles, stok, inter, s);
     if (prof) prof_record(slot, 3, s);
-    moe::launch_gemm2(plan.g2, inter, a->gemm2_weights, a->gemm2_weights_scale, tiles, num_tiles,
-                      max_tiles, rows, s);
+    if (half)
+        moe::launch_gemm2(plan.g2, inter, a->gemm2_weights, a->gemm2_weights_scale, tiles2,
+                          num_tiles2, moe::dispatch_max_tiles(T, plan.tm / 2), rows, s);
+    else
+        moe::launch_gemm2(plan.g2, inter, a->gemm2_weights, a->gemm2_weights_scale, tiles,
+                          num_tiles, max_tiles, rows, s);
     if (prof) prof_record(slot, 4, s);
     moe::launch_combine(rows, sw, inv, T, a->output, s);
     if (prof) prof_record(slot, 5, s);

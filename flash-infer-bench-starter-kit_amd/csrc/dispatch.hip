@@ -99,24 +99,37 @@ __device__ __forceinline__ void place(const TokenRoutes& r, const int* rank, int
     }
 }
 
-// expert offsets, tile list and tile count from the per-expert totals (wave 0)
+// expert offsets, tile list and tile count from the per-expert totals (wave 0).
+// With tiles2 set, also a second list of tiles of TM/2 rows (num_tiles2 = its count):
+// the prefill GEMM2 walks finer tiles than the GEMM1 over the same rows.
 template <int TM>
 __device__ __forceinline__ void write_offsets_and_tiles(int c, int lane, int* off_lds,
                                                         int* __restrict__ exp_off,
                                                         int* __restrict__ num_tiles,
-                                                        int4* __restrict__ tiles) {
+                                                        int4* __restrict__ tiles,
+                                                        int* __restrict__ num_tiles2,
+                                                        int4* __restrict__ tiles2) {
+    constexpr int TM2 = TM / 2;
     const int nt = (c + TM - 1) / TM;
+    const int nt2 = (c + TM2 - 1) / TM2;
     const int ci = scan32(c, lane);
     const int ti = scan32(nt, lane);
+    const int ti2 = scan32(nt2, lane);
     if (lane < kEL) {
         const int o = ci - c, to = ti - nt;
         off_lds[lane] = o;
         exp_off[lane] = o;
         for (int j = 0; j < nt; ++j) tiles[to + j] = make_int4(lane, o + j * TM, min(TM, c - j * TM), 0);
+        if (tiles2) {
+            const int to2 = ti2 - nt2;
+            for (int j = 0; j < nt2; ++j)
+                tiles2[to2 + j] = make_int4(lane, o + j * TM2, min(TM2, c - j * TM2), 0);
+        }
     }
     if (lane == kEL - 1) {
         exp_off[kEL] = ci;
         *num_tiles = ti;
+        if (tiles2) *num_tiles2 = ti2;
     }
 }
 
@@ -125,6 +138,7 @@ template <int TM>
 __global__ __launch_bounds__(1024) void dispatch_small_kernel(
     const int* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int offset,
     int* __restrict__ exp_off, int* __restrict__ num_tiles, int4* __restrict__ tiles,
+    int* __restrict__ num_tiles2, int4* __restrict__ tiles2,
     int* __restrict__ sorted_tok, float* __restrict__ sorted_w, int* __restrict__ inv) {
     __shared__ int wcnt[16][kEL];
     __shared__ int wbase[16][kEL];
@@ -139,7 +153,8 @@ __global__ __launch_bounds__(1024) void dispatch_small_kernel(
         int c = 0;
         if (lane < kEL)
             for (int w = 0; w < 16; ++w) c += wcnt[w][lane];
-        write_offsets_and_tiles<TM>(lane < kEL ? c : 0, lane, off, exp_off, num_tiles, tiles);
+        write_offsets_and_tiles<TM>(lane < kEL ? c : 0, lane, off, exp_off, num_tiles, tiles,
+                                    num_tiles2, tiles2);
     }
     __syncthreads();
     if (tid < kEL) {
@@ -176,8 +191,9 @@ template <int TM>
 __global__ __launch_bounds__(1024) void dispatch_place_kernel(
     const int* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int offset,
     const int* __restrict__ chunk_cnt, int nchunks, int* __restrict__ exp_off,
-    int* __restrict__ num_tiles, int4* __restrict__ tiles, int* __restrict__ sorted_tok,
-    float* __restrict__ sorted_w, int* __restrict__ inv) {
+    int* __restrict__ num_tiles, int4* __restrict__ tiles, int* __restrict__ num_tiles2,
+    int4* __restrict__ tiles2, int* __restrict__ sorted_tok, float* __restrict__ sorted_w,
+    int* __restrict__ inv) {
     __shared__ int wcnt[16][kEL];
     __shared__ int wbase[16][kEL];
     __shared__ int off[kEL];
@@ -198,7 +214,8 @@ __global__ __launch_bounds__(1024) void dispatch_place_kernel(
             }
         }
         if (chunk == 0) {
-            write_offsets_and_tiles<TM>(lane < kEL ? total : 0, lane, off, exp_off, num_tiles, tiles);
+            write_offsets_and_tiles<TM>(lane < kEL ? total : 0, lane, off, exp_off, num_tiles, tiles,
+                                        num_tiles2, tiles2);
         } else {
             const int ci = scan32(lane < kEL ? total : 0, lane);
             if (lane < kEL) off[lane] = ci - total;
@@ -224,33 +241,39 @@ int dispatch_max_tiles(int T, int tm) {
 
 template <int TM>
 static void launch_dispatch_tm(const int* topk_ids, const float* topk_w, int T, int offset,
-                               int* exp_off, int* num_tiles, int4* tiles, int* sorted_tok,
-                               float* sorted_w, int* inv, int* chunk_cnt, hipStream_t stream) {
+                               int* exp_off, int* num_tiles, int4* tiles, int* num_tiles2,
+                               int4* tiles2, int* sorted_tok, float* sorted_w, int* inv,
+                               int* chunk_cnt, hipStream_t stream) {
     if (T <= 1024) {
         hipLaunchKernelGGL(dispatch_small_kernel<TM>, dim3(1), dim3(1024), 0, stream, topk_ids,
-                           topk_w, T, offset, exp_off, num_tiles, tiles, sorted_tok, sorted_w, inv);
+                           topk_w, T, offset, exp_off, num_tiles, tiles, num_tiles2, tiles2,
+                           sorted_tok, sorted_w, inv);
         return;
     }
     const int nchunks = (T + 1023) / 1024;
     hipLaunchKernelGGL(dispatch_count_kernel, dim3(nchunks), dim3(1024), 0, stream, topk_ids, topk_w,
                        T, offset, chunk_cnt);
     hipLaunchKernelGGL(dispatch_place_kernel<TM>, dim3(nchunks), dim3(1024), 0, stream, topk_ids,
-                       topk_w, T, offset, chunk_cnt, nchunks, exp_off, num_tiles, tiles, sorted_tok,
-                       sorted_w, inv);
+                       topk_w, T, offset, chunk_cnt, nchunks, exp_off, num_tiles, tiles,
+                       num_tiles2, tiles2, sorted_tok, sorted_w, inv);
 }
 
-// chunk_cnt: int32 [ceil(T/1024) * 32] scratch, needed when T > 1024
+// chunk_cnt: int32 [ceil(T/1024) * 32] scratch, needed when T > 1024.  tiles2 /
+// num_tiles2 (may be null): a second tile list of tm/2 rows over the same rows.
 bool launch_dispatch(const int* topk_ids, const float* topk_w, int T, int offset, int tm,
                      int* exp_off, int* num_tiles, int4* tiles, int* sorted_tok,
-                     float* sorted_w, int* inv, int* chunk_cnt, hipStream_t stream) {
+                     float* sorted_w, int* inv, int* chunk_cnt, hipStream_t stream,
+                     int* num_tiles2, int4* tiles2) {
+#define DISPATCH_TM(TM)                                                                               launch_dispatch_tm<TM>(topk_ids, topk_w, T, offset, exp_off, num_tiles, tiles, num_tiles2,                               tiles2, sorted_tok, sorted_w, inv, chunk_cnt, stream)
     switch (tm) {
-        case 16: launch_dispatch_tm<16>(topk_ids, topk_w, T, offset, exp_off, num_tiles, tiles, sorted_tok, sorted_w, inv, chunk_cnt, stream); return true;
-        case 32: launch_dispatch_tm<32>(topk_ids, topk_w, T, offset, exp_off, num_tiles, tiles, sorted_tok, sorted_w, inv, chunk_cnt, stream); return true;
-        case 64: launch_dispatch_tm<64>(topk_ids, topk_w, T, offset, exp_off, num_tiles, tiles, sorted_tok, sorted_w, inv, chunk_cnt, stream); return true;
-        case 128: launch_dispatch_tm<128>(topk_ids, topk_w, T, offset, exp_off, num_tiles, tiles, sorted_tok, sorted_w, inv, chunk_cnt, stream); return true;
-        case 256: launch_dispatch_tm<256>(topk_ids, topk_w, T, offset, exp_off, num_tiles, tiles, sorted_tok, sorted_w, inv, chunk_cnt, stream); return true;
+        case 16: DISPATCH_TM(16); return true;
+        case 32: DISPATCH_TM(32); return true;
+        case 64: DISPATCH_TM(64); return true;
+        case 128: DISPATCH_TM(128); return true;
+        case 256: DISPATCH_TM(256); return true;
         default: return false;
     }
+#undef DISPATCH_TM
 }
 
 }  // namespace moe

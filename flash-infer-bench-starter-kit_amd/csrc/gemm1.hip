@@ -632,6 +632,9 @@ __global__ __launch_bounds__(256) void gemm1_prefill_kernel(
             issue(kb);
             __builtin_amdgcn_sched_barrier(0);
         }
+        // 16-row token blocks of this wave that exist: padding blocks skip their MFMAs
+        auto kloop = [&](auto live) {
+        constexpr int NLIVE = decltype(live)::value;
 #pragma unroll 1
         for (int kb = 0; kb < kHB; ++kb) {
             // wait for this wave's part of stage kb (younger stages stay in flight)
@@ -647,9 +650,10 @@ __global__ __launch_bounds__(256) void gemm1_prefill_kernel(
 
             const uint8_t* st = lds + (kb % NS) * kStage;
             const float fsg = sgp[kb], fsu = sup[kb];
+            if (NLIVE == 0) continue;
             v8i bt[4];
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
+            for (int s = 0; s < NLIVE; ++s) {
                 const uint8_t* rp = st + (64 * wm + 16 * s + r16) * kBlk;
                 const v4u x0 = *reinterpret_cast<const v4u*>(rp + c0);
                 const v4u x1 = *reinterpret_cast<const v4u*>(rp + c1);
@@ -658,7 +662,7 @@ __global__ __launch_bounds__(256) void gemm1_prefill_kernel(
             const float* sar = reinterpret_cast<const float*>(st + kA + kW + wave * 256);
             float fs[4][2];
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
+            for (int s = 0; s < NLIVE; ++s) {
                 const float sa = sar[16 * s + r16];
                 fs[s][0] = sa * fsg;
                 fs[s][1] = sa * fsu;
@@ -672,7 +676,7 @@ __global__ __launch_bounds__(256) void gemm1_prefill_kernel(
                 const v4u x1 = *reinterpret_cast<const v4u*>(rp + c1);
                 const v8i bw = {(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
 #pragma unroll
-                for (int s = 0; s < 4; ++s) {
+                for (int s = 0; s < NLIVE; ++s) {
                     const v4f t = mfma_fp8(bw, bt[s], zero);
                     const float f = fs[s][j >> 2];
 #pragma unroll
@@ -680,6 +684,8 @@ __global__ __launch_bounds__(256) void gemm1_prefill_kernel(
                 }
             }
         }
+        };
+        with_live_blocks(live_blocks(64 * wm, nrows), kloop);
 
         // epilogue: lane holds D[n = 4*kq + v][token = r16] of each 16 x 16 block
         store_c_hilo(acc, reinterpret_cast<float*>(lds), wm, wn, kq, r16, row0, nrows, ng, C);
@@ -773,6 +779,10 @@ __global__ __launch_bounds__(512, 1) void gemm1_prefill8_kernel(
         __syncthreads();
         issue_tokens(0);
         issue_weights(0);
+        // token rows 64 wm + 16 s .. of this wave that exist: the MFMAs of padding
+        // blocks are skipped (the DMA and barriers stay the same for every wave)
+        auto kloop = [&](auto live) {
+        constexpr int NLIVE = decltype(live)::value;
 #pragma unroll 1
         for (int kb = 0; kb < kHB; ++kb) {
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
@@ -786,7 +796,7 @@ __global__ __launch_bounds__(512, 1) void gemm1_prefill8_kernel(
             v8i bt[4];
             float fg[4], fu[4];
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
+            for (int s = 0; s < NLIVE; ++s) {
                 const uint8_t* rp = st + (64 * wm + 16 * s + r16) * kBlk;
                 const v4u x0 = *reinterpret_cast<const v4u*>(rp + c0);
                 const v4u x1 = *reinterpret_cast<const v4u*>(rp + c1);
@@ -802,19 +812,19 @@ __global__ __launch_bounds__(512, 1) void gemm1_prefill8_kernel(
                 const v4u x1 = *reinterpret_cast<const v4u*>(rp + c1);
                 return v8i{(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
             };
-            v8i bw_next = read_w(0);
+            v8i bw_next = NLIVE ? read_w(0) : v8i{};
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 __builtin_amdgcn_sched_barrier(0);
                 const v8i bw = bw_next;
-                if (j < 7) bw_next = read_w(j + 1);
+                if (NLIVE && j < 7) bw_next = read_w(j + 1);
                 if (j == kWeightBurstAfter && kb + 1 < kHB) {
                     __builtin_amdgcn_sched_barrier(0);
                     issue_weights(kb + 1);
                     __builtin_amdgcn_sched_barrier(0);
                 }
 #pragma unroll
-                for (int s = 0; s < 4; ++s) {
+                for (int s = 0; s < NLIVE; ++s) {
                     const v4f t = mfma_fp8(bw, bt[s], zero);
                     const float f = (j < 4) ? fg[s] : fu[s];
 #pragma unroll
@@ -822,6 +832,8 @@ __global__ __launch_bounds__(512, 1) void gemm1_prefill8_kernel(
                 }
             }
         }
+        };
+        with_live_blocks(live_blocks(64 * wm, nrows), kloop);
 
         store_c_hilo(acc, reinterpret_cast<float*>(lds), wm, wn, kq, r16, row0, nrows, ng, C);
     }

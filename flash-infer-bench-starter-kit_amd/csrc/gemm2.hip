@@ -451,8 +451,7 @@ __global__ __launch_bounds__(256) void gemm2_dma_kernel(
 // the barrier, W2 after the second column block's MFMAs); rows keep 16-byte chunk c
 // at c ^ swz128(r).  Items (128-row piece, 256-column group) are grouped 4 pieces x
 // all column groups with an XCD-contiguous mapping, as in the prefill GEMM1.
-// SPLIT = 2 processes 256-row tiles as two 128-row pieces.
-template <int SPLIT>
+// Tiles hold at most 128 rows.
 __global__ __launch_bounds__(512, 1) void gemm2_prefill8_kernel(
     Intermediate C, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
     const int4* __restrict__ tiles, const int* __restrict__ num_tiles,
@@ -471,7 +470,7 @@ __global__ __launch_bounds__(512, 1) void gemm2_prefill8_kernel(
     const int r16 = lane & 15, kq = lane >> 4;
     const int wm = wave >> 2, wn = wave & 3;
     const v4f zero = {0.f, 0.f, 0.f, 0.f};
-    const int nvt = (*num_tiles) * SPLIT;
+    const int nvt = *num_tiles;
     const int nitems = nvt * NG;
     const int G = gridDim.x;
     const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, per = G >> 3;
@@ -484,11 +483,8 @@ __global__ __launch_bounds__(512, 1) void gemm2_prefill8_kernel(
         if (item >= nitems) continue;            // uniform per workgroup
         int vix, hg;
         grouped_item(item, nvt, NG, vix, hg);
-        const int4 tile = tiles[vix / SPLIT];
-        const int le = tile.x;
-        const int row0 = tile.y + (vix % SPLIT) * BM;
-        const int nrows = min(BM, tile.z - (vix % SPLIT) * BM);
-        if (nrows <= 0) continue;                // uniform per workgroup
+        const int4 tile = tiles[vix];
+        const int le = tile.x, row0 = tile.y, nrows = tile.z;
 
         const __amdgpu_buffer_rsrc_t rs_hi = buffer_rsrc(C.hi() + (size_t)row0 * kI, BM * kI);
         const __amdgpu_buffer_rsrc_t rs_lo = buffer_rsrc(C.lo() + (size_t)row0 * kI, BM * kI);
@@ -534,6 +530,9 @@ __global__ __launch_bounds__(512, 1) void gemm2_prefill8_kernel(
         __syncthreads();
         issue_c(0);
         issue_w(0);
+        // 16-row blocks of this wave that exist: padding blocks skip their MFMAs
+        auto kloop = [&](auto live) {
+        constexpr int NLIVE = decltype(live)::value;
 #pragma unroll 1
         for (int kb = 0; kb < kIB; ++kb) {
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
@@ -547,7 +546,7 @@ __global__ __launch_bounds__(512, 1) void gemm2_prefill8_kernel(
             v8i ch[4], cl[4];
             float f[4];
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
+            for (int s = 0; s < NLIVE; ++s) {
                 const int r = 64 * wm + 16 * s + r16;
                 const uint8_t* ph = st + r * kBlk;
                 const uint8_t* pl = st + kC + r * kBlk;
@@ -565,19 +564,19 @@ __global__ __launch_bounds__(512, 1) void gemm2_prefill8_kernel(
                 const v4u x1 = *reinterpret_cast<const v4u*>(rp + c1);
                 return v8i{(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
             };
-            v8i w_next = read_w(0);
+            v8i w_next = NLIVE ? read_w(0) : v8i{};
 #pragma unroll
             for (int n = 0; n < 4; ++n) {
                 __builtin_amdgcn_sched_barrier(0);
                 const v8i w = w_next;
-                if (n < 3) w_next = read_w(n + 1);
+                if (NLIVE && n < 3) w_next = read_w(n + 1);
                 if (n == kWeightBurstAfter && kb + 1 < kIB) {
                     __builtin_amdgcn_sched_barrier(0);
                     issue_w(kb + 1);
                     __builtin_amdgcn_sched_barrier(0);
                 }
 #pragma unroll
-                for (int s = 0; s < 4; ++s) {
+                for (int s = 0; s < NLIVE; ++s) {
                     v4f t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(w, ch[s], zero, 0, 0, 0, 0, 0, 0);
                     t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(w, cl[s], t, 0, 0, 0, 127, 0, 123);
 #pragma unroll
@@ -585,6 +584,8 @@ __global__ __launch_bounds__(512, 1) void gemm2_prefill8_kernel(
                 }
             }
         }
+        };
+        with_live_blocks(live_blocks(64 * wm, nrows), kloop);
 
         // lane holds D[h = 64 wn + 16 n + 4 kq + v][row = 64 wm + 16 s + r16]
 #pragma unroll
@@ -612,8 +613,9 @@ static int grid_for2(long long work) { return (int)(work < 4096 ? work : 4096); 
 
 // variant: 0..5 register-ring streaming, 6..11 LDS-landed streaming, both with
 // (CB, KSPLIT, HF) = (1,1,2) (1,2,2) (1,4,1) (2,1,2) (2,2,2) (2,4,1) and bf16 C; 12 the
-// prefill kernel on 128-row tiles and 13 on 256-row tiles, both reading C in the fp8
-// hi/lo form; -1 the 64-row tile kernel (bf16 C)
+// prefill kernel on 128-row tiles (13: the same kernel over the 128-row second tile
+// list of a 256-row dispatch), reading C in the fp8 hi/lo form; -1 the 64-row tile
+// kernel (bf16 C)
 bool launch_gemm2(int variant, const Intermediate& C, const uint8_t* w2, const float* s2,
                   const int4* tiles, const int* num_tiles, int max_tiles, float* out_rows,
                   hipStream_t stream) {
@@ -641,11 +643,11 @@ bool launch_gemm2(int variant, const Intermediate& C, const uint8_t* w2, const f
         case 10: G2_DMA(2, 2, 3, 2); return true;
         case 11: G2_DMA(2, 4, 3, 1); return true;
         case 12:
-            hipLaunchKernelGGL((gemm2_prefill8_kernel<1>), dim3(256), dim3(512), 0, stream, C, w2,
+            hipLaunchKernelGGL(gemm2_prefill8_kernel, dim3(256), dim3(512), 0, stream, C, w2,
                                s2, tiles, num_tiles, out_rows);
             return true;
-        case 13:  // 256-row tiles, each processed as two 128-row pieces
-            hipLaunchKernelGGL((gemm2_prefill8_kernel<2>), dim3(256), dim3(512), 0, stream, C, w2,
+        case 13:  // the 128-row second tile list of a 256-row dispatch
+            hipLaunchKernelGGL(gemm2_prefill8_kernel, dim3(256), dim3(512), 0, stream, C, w2,
                                s2, tiles, num_tiles, out_rows);
             return true;
         case -1:

@@ -86,6 +86,30 @@ __device__ __forceinline__ constexpr int vmcnt_imm(int v) {
     return (v & 15) | ((v >> 4) << 14) | (7 << 4) | (15 << 8);
 }
 
+// Compile-time int for generic lambdas (kernels specialise their K loop on the number
+// of 16-row blocks of a tile a wave actually has to compute).
+template <int N>
+struct IntC {
+    static constexpr int value = N;
+};
+
+// Calls f(IntC<n>{}) for n in 0..4.
+template <typename F>
+__device__ __forceinline__ void with_live_blocks(int n, F&& f) {
+    switch (n) {
+        case 4: f(IntC<4>{}); break;
+        case 3: f(IntC<3>{}); break;
+        case 2: f(IntC<2>{}); break;
+        case 1: f(IntC<1>{}); break;
+        default: f(IntC<0>{}); break;
+    }
+}
+
+// 16-row blocks of a wave's 64 rows starting at row `first` that hold rows < nrows.
+__device__ __forceinline__ int live_blocks(int first, int nrows) {
+    return min(4, max(0, (nrows - first + 15) >> 4));
+}
+
 // Raw buffer resource over [base, base + bytes): 32-bit offsets, the address kept in
 // SGPRs (saves the per-lane 64-bit pointers of global_load_lds), out-of-range reads
 // return zero.  Word 3 = 0x00020000: raw (unformatted) 32-bit data, stride 0.

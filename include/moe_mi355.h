@@ -134,8 +134,10 @@ typedef struct moe_mi355_workspace_layout {
     size_t topk_ids;        /* int32 [T,8] */
     size_t topk_weights;    /* fp32  [T,8] */
     size_t inverse_rows;    /* int32 [T,8] */
-    size_t meta;            /* int32 [64]: [0..32] expert offsets, [33] num tiles */
-    size_t tiles;           /* int32 [max_tiles,4] */
+    size_t meta;            /* int32 [64]: [0..32] expert offsets, [33] num tiles,
+                               [34] tiles of the second list (256-row plans) */
+    size_t tiles;           /* int32 [2*max_tiles,4]: the tile list, then (256-row
+                               plans) a second list of 128-row tiles for GEMM2 */
     size_t sorted_tokens;   /* int32 [8T] */
     size_t sorted_weights;  /* fp32  [8T] */
     size_t chunk_counts;    /* int32 [ceil(T/1024), 32] dispatch scratch */
