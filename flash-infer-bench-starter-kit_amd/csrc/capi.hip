@@ -54,6 +54,7 @@ int variant_tile_m(int v) {
     if (v < 0) return 64;
     if (v == 12) return 128;
     if (v == 13) return 256;
+    if (v == 14) return 16;
     return (v % 6) < 3 ? 16 : 32;
 }
 
@@ -69,7 +70,7 @@ Plan choose_plan(int32_t T) {
     const char* e2 = getenv("MOE_MI355_G2");
     const int env_g1 = e1 ? atoi(e1) : -99;
     const int env_g2 = e2 ? atoi(e2) : -99;
-    if (env_g1 >= -1 && env_g1 <= 13 && env_g2 >= -1 && env_g2 <= 13 &&
+    if (env_g1 >= -1 && env_g1 <= 14 && env_g2 >= -1 && env_g2 <= 14 &&
         variant_tile_m(env_g1) == variant_tile_m(env_g2) &&
         variant_c_hilo(env_g1) == variant_c_hilo(env_g2))
         p = {variant_tile_m(env_g1), env_g1, env_g2};

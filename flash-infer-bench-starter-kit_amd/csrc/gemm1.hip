@@ -461,6 +461,168 @@ __global__ __launch_bounds__(256) void gemm1_dma_kernel(
     }
 }
 
+// Persistent form of gemm1_dma_kernel<1, 4, NS> (decode): a workgroup walks the items
+// blockIdx, blockIdx + gridDim, ... and each wave's LDS ring runs on across item
+// boundaries, so the first NS-1 K blocks of the next item are in flight while the
+// current item finishes and its four K quarters are reduced.  The ring position of a
+// K block is its running index mod NS; 14 K blocks per quarter make that position
+// alternate between two phases (PH = 0 or 14 mod NS), one instantiation each.
+// ---------------------------------------------------------------------------
+template <int NS>
+__global__ __launch_bounds__(256) void gemm1_pstream_kernel(
+    const uint8_t* __restrict__ hidden, const float* __restrict__ hs_scale, int T,
+    const uint8_t* __restrict__ w1, const float* __restrict__ s1,
+    const int4* __restrict__ tiles, const int* __restrict__ num_tiles,
+    const int* __restrict__ sorted_tok, uint16_t* __restrict__ inter) {
+    constexpr int KSPLIT = 4;
+    constexpr int KB = kHB / KSPLIT;                  // 14 K blocks per wave and item
+    constexpr int kItems = kI / 16;                   // 128 column groups per tile
+    constexpr int kSlot = 32 * kBlk;
+    constexpr int kVmPerKb = 4 + 3;
+    static_assert(NS >= 2 && NS <= 7 && (NS - 1) * kVmPerKb < 64, "ring depth");
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[4][NS][kSlot];
+    __shared__ v4f red[4][2][64];
+
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int r16 = lane & 15, kq = lane >> 4;
+    const int ks = wave;
+    const int nwork = (*num_tiles) * kItems;
+    const v4f zero = {0.f, 0.f, 0.f, 0.f};
+    uint8_t* myring = &ring[wave][0][0];
+    const int drow = lane >> 3, dchunk = lane & 7;
+    const int swz = swz128(r16);
+    const int rd_g0 = r16 * kBlk + (((2 * kq) ^ swz) << 4);
+    const int rd_g1 = r16 * kBlk + (((2 * kq + 1) ^ swz) << 4);
+    const int rd_u0 = rd_g0 + 16 * kBlk;
+    const int rd_u1 = rd_g1 + 16 * kBlk;
+    const int kb0 = ks * KB;
+
+    // where the operands of one item come from
+    struct Src {
+        const uint8_t* w[4];      // DMA rows 8i + drow (0-15 gate, 16-31 up), K block 0
+        const uint8_t* a;         // token row, this lane's 32 bytes of K block 0
+        const float* sa;          // token scale column
+        const float* sg;          // gate / up weight scales of the column group
+        const float* su;
+        int row0, nrows, ng;
+    };
+    auto make_src = [&](int work) {
+        Src s;
+        const int4 tile = tiles[work / kItems];
+        s.ng = work % kItems;
+        const int le = tile.x;
+        s.row0 = tile.y;
+        s.nrows = tile.z;
+        const int tok = sorted_tok[s.row0 + min(r16, s.nrows - 1)];
+        s.a = hidden + (size_t)tok * kH + kq * 32;
+        s.sa = hs_scale + tok;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = 8 * i + drow;
+            const int n = (r < 16) ? s.ng * 16 + r : kI + s.ng * 16 + (r - 16);
+            s.w[i] = w1 + (size_t)(le * kN1 + n) * kH + ((dchunk ^ swz128(r)) << 4);
+        }
+        s.sg = s1 + (size_t)(le * kN1B + (s.ng >> 3)) * kHB;
+        s.su = s.sg + (size_t)kIB * kHB;
+        return s;
+    };
+
+    v8i ba[NS];
+    float bs[NS];
+    // K block k (0..KB-1 of this wave's quarter) of item src into ring position p
+    auto issue = [&](const Src& s, int k, auto pc) {
+        constexpr int p = decltype(pc)::value;
+        const int kb = kb0 + k;
+        uint8_t* slot = myring + p * kSlot;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dma16(s.w[i] + kb * kBlk, slot + i * 1024);
+        ba[p] = load_v8i(s.a + kb * kBlk);
+        bs[p] = s.sa[(size_t)kb * T];
+    };
+
+    int work = blockIdx.x;
+    if (work >= nwork) return;                        // uniform per workgroup
+    Src cur = make_src(work);
+    // prologue: the first NS-1 K blocks of the first item (phase 0)
+    [&]<int... P>(std::integer_sequence<int, P...>) {
+        (issue(cur, P, IntC<P>{}), ...);
+    }(std::make_integer_sequence<int, NS - 1>{});
+    __builtin_amdgcn_sched_barrier(0);
+
+    auto item = [&](auto phc) {
+        constexpr int PH = decltype(phc)::value;
+        const int next = work + gridDim.x;
+        const bool has_next = next < nwork;           // uniform
+        const Src nxt = make_src(has_next ? next : work);
+        v4f ag = zero, au = zero;
+        [&]<int... K>(std::integer_sequence<int, K...>) {
+            ([&] {
+                constexpr int k = K;
+                constexpr int ki = k + NS - 1;        // K block issued at this step
+                if constexpr (ki < KB) {
+                    issue(cur, ki, IntC<(PH + ki) % NS>{});
+                } else {
+                    if (has_next) issue(nxt, ki - KB, IntC<(PH + ki) % NS>{});
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                // K blocks issued after k: NS-1, fewer at the end of the last item
+                const int younger = (ki < KB || has_next) ? NS - 1 : (KB - 1 - k);
+                switch (younger) {
+                    case 6: __builtin_amdgcn_s_waitcnt(vmcnt_imm(6 * kVmPerKb)); break;
+                    case 5: __builtin_amdgcn_s_waitcnt(vmcnt_imm(5 * kVmPerKb)); break;
+                    case 4: __builtin_amdgcn_s_waitcnt(vmcnt_imm(4 * kVmPerKb)); break;
+                    case 3: __builtin_amdgcn_s_waitcnt(vmcnt_imm(3 * kVmPerKb)); break;
+                    case 2: __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kVmPerKb)); break;
+                    case 1: __builtin_amdgcn_s_waitcnt(vmcnt_imm(1 * kVmPerKb)); break;
+                    default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                constexpr int p = (PH + k) % NS;
+                const uint8_t* slot = myring + p * kSlot;
+                const v4u g0 = *reinterpret_cast<const v4u*>(slot + rd_g0);
+                const v4u g1 = *reinterpret_cast<const v4u*>(slot + rd_g1);
+                const v4u u0 = *reinterpret_cast<const v4u*>(slot + rd_u0);
+                const v4u u1 = *reinterpret_cast<const v4u*>(slot + rd_u1);
+                const v8i bg = {(int)g0[0], (int)g0[1], (int)g0[2], (int)g0[3], (int)g1[0], (int)g1[1], (int)g1[2], (int)g1[3]};
+                const v8i bu = {(int)u0[0], (int)u0[1], (int)u0[2], (int)u0[3], (int)u1[0], (int)u1[1], (int)u1[2], (int)u1[3]};
+                const int kb = kb0 + k;
+                const float fg = bs[p] * cur.sg[kb], fu = bs[p] * cur.su[kb];
+                const v4f tg = mfma_fp8(bg, ba[p], zero);
+                const v4f tu = mfma_fp8(bu, ba[p], zero);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    ag[v] = __builtin_fmaf(tg[v], fg, ag[v]);
+                    au[v] = __builtin_fmaf(tu[v], fu, au[v]);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }(), ...);
+        }(std::make_integer_sequence<int, KB>{});
+
+        // reduce the four K quarters (fixed order) and store the SwiGLU rows
+        red[wave][0][lane] = ag;
+        red[wave][1][lane] = au;
+        __syncthreads();
+        if (wave == 0) {
+            v4f g = red[0][0][lane], u = red[0][1][lane];
+#pragma unroll
+            for (int q = 1; q < KSPLIT; ++q) {
+                g += red[q][0][lane];
+                u += red[q][1][lane];
+            }
+            if (r16 < cur.nrows) store_swiglu4(inter, cur.row0 + r16, cur.ng * 16 + kq * 4, g, u);
+        }
+        __syncthreads();
+        cur = nxt;
+        work = next;
+        return has_next;
+    };
+    for (;;) {
+        if (!item(IntC<0>{})) break;
+        if (!item(IntC<(KB % NS)>{})) break;
+    }
+}
+
 // Four floats -> four e4m3 bytes (v_cvt_pk_fp8_f32: round to nearest even, OCP e4m3fn,
 // the same rounding as torch's float8_e4m3fn cast; inputs are clamped to +-448
 // beforehand so nothing overflows to NaN).
@@ -881,6 +1043,11 @@ bool launch_gemm1(int variant, const uint8_t* hidden, const float* hs_scale, int
         case 13:
             hipLaunchKernelGGL(gemm1_prefill8_kernel, dim3(prefill_grid), dim3(512), 0, stream,
                                hidden, hs_scale, T, w1, s1, tiles, num_tiles, sorted_tok, C);
+            return true;
+        case 14:   // persistent streaming, 16-row tiles, two workgroups per CU
+            hipLaunchKernelGGL(gemm1_pstream_kernel<4>, dim3(grid_for(mt * G) < 512 ? grid_for(mt * G) : 512),
+                               dim3(256), 0, stream, hidden, hs_scale, T, w1, s1, tiles, num_tiles,
+                               sorted_tok, inter);
             return true;
         case -1:
             hipLaunchKernelGGL(gemm1_swiglu_kernel<4>, dim3(grid_for(mt * G)), dim3(256), 0, stream,

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <utility>
+
 namespace moe {
 
 // Geometry (reference solution/python/kernel.h:9-25).
