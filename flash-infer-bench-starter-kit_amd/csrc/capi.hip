@@ -40,9 +40,10 @@ namespace {
 constexpr int32_t kMaxT = 1 << 19;
 constexpr int kMinTileM = 16;           // smallest row tile; sizes the tile list
 
-// Kernel plan per token count.  Small T streams weights through LDS with the
-// DMA kernels (row tiles of 16 or 32 rows, C in bf16); large T uses the MFMA-bound
-// prefill kernels (128- or 256-row tiles, C in the fp8 hi/lo form).
+// Kernel plan per token count.  Small T streams weights with the register-staged
+// kernels (T <= 96, 16-row tiles) or the LDS-landed DMA kernels (32-row tiles), C in
+// bf16; large T uses the MFMA-bound prefill kernels (128- or 256-row tiles, C in the
+// fp8 hi/lo form).
 // Variant ids are those of launch_gemm1 / launch_gemm2; MOE_MI355_G1 / MOE_MI355_G2
 // override them for tuning sweeps (ignored unless both imply the same tile height
 // and the same form of C).
@@ -54,7 +55,7 @@ int variant_tile_m(int v) {
     if (v < 0) return 64;
     if (v == 12) return 128;
     if (v == 13) return 256;
-    if (v == 14) return 16;
+    if (v >= 14) return 16;
     return (v % 6) < 3 ? 16 : 32;
 }
 
@@ -62,7 +63,7 @@ bool variant_c_hilo(int v) { return v == 12 || v == 13; }
 
 Plan choose_plan(int32_t T) {
     Plan p;
-    if (T <= 96) p = {16, 8, 8};
+    if (T <= 96) p = {16, 15, 15};
     else if (T <= 256) p = {32, 11, 10};
     else if (T <= 2048) p = {128, 12, 12};
     else p = {256, 13, 13};
@@ -70,7 +71,7 @@ Plan choose_plan(int32_t T) {
     const char* e2 = getenv("MOE_MI355_G2");
     const int env_g1 = e1 ? atoi(e1) : -99;
     const int env_g2 = e2 ? atoi(e2) : -99;
-    if (env_g1 >= -1 && env_g1 <= 14 && env_g2 >= -1 && env_g2 <= 14 &&
+    if (env_g1 >= -1 && env_g1 <= 16 && env_g2 >= -1 && env_g2 <= 16 &&
         variant_tile_m(env_g1) == variant_tile_m(env_g2) &&
         variant_c_hilo(env_g1) == variant_c_hilo(env_g2))
         p = {variant_tile_m(env_g1), env_g1, env_g2};

@@ -133,15 +133,16 @@ __device__ __forceinline__ void write_offsets_and_tiles(int c, int lane, int* of
     }
 }
 
-// T <= 1024: one workgroup, one token per thread, one pass over the routes.
-template <int TM>
-__global__ __launch_bounds__(1024) void dispatch_small_kernel(
+// T <= 1024: one workgroup of NW waves (64 NW >= T), one token per thread, one pass
+// over the routes.
+template <int TM, int NW>
+__global__ __launch_bounds__(64 * NW) void dispatch_small_kernel(
     const int* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int offset,
     int* __restrict__ exp_off, int* __restrict__ num_tiles, int4* __restrict__ tiles,
     int* __restrict__ num_tiles2, int4* __restrict__ tiles2,
     int* __restrict__ sorted_tok, float* __restrict__ sorted_w, int* __restrict__ inv) {
-    __shared__ int wcnt[16][kEL];
-    __shared__ int wbase[16][kEL];
+    __shared__ int wcnt[NW][kEL];
+    __shared__ int wbase[NW][kEL];
     __shared__ int off[kEL];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
 
@@ -152,14 +153,14 @@ __global__ __launch_bounds__(1024) void dispatch_small_kernel(
     if (wave == 0) {
         int c = 0;
         if (lane < kEL)
-            for (int w = 0; w < 16; ++w) c += wcnt[w][lane];
+            for (int w = 0; w < NW; ++w) c += wcnt[w][lane];
         write_offsets_and_tiles<TM>(lane < kEL ? c : 0, lane, off, exp_off, num_tiles, tiles,
                                     num_tiles2, tiles2);
     }
     __syncthreads();
     if (tid < kEL) {
         int run = off[tid];
-        for (int w = 0; w < 16; ++w) {
+        for (int w = 0; w < NW; ++w) {
             wbase[w][tid] = run;
             run += wcnt[w][tid];
         }
@@ -245,9 +246,14 @@ static void launch_dispatch_tm(const int* topk_ids, const float* topk_w, int T, 
                                int4* tiles2, int* sorted_tok, float* sorted_w, int* inv,
                                int* chunk_cnt, hipStream_t stream) {
     if (T <= 1024) {
-        hipLaunchKernelGGL(dispatch_small_kernel<TM>, dim3(1), dim3(1024), 0, stream, topk_ids,
-                           topk_w, T, offset, exp_off, num_tiles, tiles, num_tiles2, tiles2,
-                           sorted_tok, sorted_w, inv);
+#define DISPATCH_SMALL(NW)                                                                        \
+    hipLaunchKernelGGL((dispatch_small_kernel<TM, NW>), dim3(1), dim3(64 * NW), 0, stream,        \
+                       topk_ids, topk_w, T, offset, exp_off, num_tiles, tiles, num_tiles2, tiles2, \
+                       sorted_tok, sorted_w, inv)
+        if (T <= 64) DISPATCH_SMALL(1);
+        else if (T <= 256) DISPATCH_SMALL(4);
+        else DISPATCH_SMALL(16);
+#undef DISPATCH_SMALL
         return;
     }
     const int nchunks = (T + 1023) / 1024;

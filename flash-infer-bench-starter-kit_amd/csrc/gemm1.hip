@@ -461,6 +461,136 @@ __global__ __launch_bounds__(256) void gemm1_dma_kernel(
     }
 }
 
+// Register-staged weight streaming (decode): the same work split as
+// gemm1_dma_kernel<1, 4, NS>, but weight bytes come into registers with full-line
+// loads (global_load_dwordx4, lane l reads row 8i + l/8, 16-byte chunk l%8 of the K
+// block: 8 rows x 128 B per instruction) through a ring of D K blocks held in VGPRs,
+// and each K block is turned into the MFMA layout through a 4 KB per-wave LDS slot
+// (ds_write_b128 at the swizzled position, then ds_read_b128 by the MFMA lanes).
+// Keeping the in-flight bytes in VGPRs instead of LDS lets more waves run per CU, so
+// more bytes are in flight per CU than with LDS-landed DMA (a streaming probe of this
+// access pattern: 7.1 TB/s against 6.3 TB/s for the LDS ring).
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(256) void gemm1_rstream_kernel(
+    const uint8_t* __restrict__ hidden, const float* __restrict__ hs_scale, int T,
+    const uint8_t* __restrict__ w1, const float* __restrict__ s1,
+    const int4* __restrict__ tiles, const int* __restrict__ num_tiles,
+    const int* __restrict__ sorted_tok, uint16_t* __restrict__ inter) {
+    constexpr int KSPLIT = 4;
+    constexpr int KB = kHB / KSPLIT;                  // 14 K blocks per wave
+    constexpr int kItems = kI / 16;
+    constexpr int kVmPerKb = 4 + 3;                   // 4 weight loads, 2 token loads, 1 scale
+    static_assert(D >= 2 && D <= 8 && (D - 1) * kVmPerKb < 64, "ring depth");
+    __shared__ __attribute__((aligned(1024))) uint8_t slot_lds[4][32 * kBlk];
+    __shared__ v4f red[4][2][64];
+
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int r16 = lane & 15, kq = lane >> 4;
+    const int ks = wave;
+    const int nwork = (*num_tiles) * kItems;
+    const v4f zero = {0.f, 0.f, 0.f, 0.f};
+    uint8_t* slot = &slot_lds[wave][0];
+    const int drow = lane >> 3, dchunk = lane & 7;
+    const int swz = swz128(r16);
+    const int rd_g0 = r16 * kBlk + (((2 * kq) ^ swz) << 4);
+    const int rd_g1 = r16 * kBlk + (((2 * kq + 1) ^ swz) << 4);
+    const int rd_u0 = rd_g0 + 16 * kBlk;
+    const int rd_u1 = rd_g1 + 16 * kBlk;
+    int wr[4];                                         // LDS position of this lane's chunk
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = 8 * i + drow;
+        wr[i] = r * kBlk + ((dchunk ^ swz128(r)) << 4);
+    }
+    const int kb0 = ks * KB;
+
+    for (int work = blockIdx.x; work < nwork; work += gridDim.x) {
+        const int4 tile = tiles[work / kItems];
+        const int ng = work % kItems;
+        const int le = tile.x, row0 = tile.y, nrows = tile.z;
+        const int tok = sorted_tok[row0 + min(r16, nrows - 1)];
+        const uint8_t* ap = hidden + (size_t)tok * kH + kq * 32;
+        const float* sp = hs_scale + tok;
+        const uint8_t* wsrc[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = 8 * i + drow;
+            const int n = (r < 16) ? ng * 16 + r : kI + ng * 16 + (r - 16);
+            wsrc[i] = w1 + (size_t)(le * kN1 + n) * kH + dchunk * 16;
+        }
+        const float* sg = s1 + (size_t)(le * kN1B + (ng >> 3)) * kHB;
+        const float* su = sg + (size_t)kIB * kHB;
+
+        v4u bw[D][4];
+        v8i ba[D];
+        float bs[D];
+        auto issue = [&](int k) {
+            const int kb = kb0 + k;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) bw[k % D][i] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(wsrc[i] + kb * kBlk));
+            ba[k % D] = load_v8i(ap + kb * kBlk);
+            bs[k % D] = sp[(size_t)kb * T];
+        };
+#pragma unroll
+        for (int k = 0; k < D - 1; ++k) {
+            issue(k);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        v4f ag = zero, au = zero;
+#pragma unroll
+        for (int k = 0; k < KB; ++k) {
+            if (k + D - 1 < KB) issue(k + D - 1);
+            __builtin_amdgcn_sched_barrier(0);
+            const int younger = (KB - 1 - k) < (D - 1) ? (KB - 1 - k) : (D - 1);
+            switch (younger) {   // resolved at compile time after unrolling
+                case 0: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
+                case 1: __builtin_amdgcn_s_waitcnt(vmcnt_imm(1 * kVmPerKb)); break;
+                case 2: __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kVmPerKb)); break;
+                case 3: __builtin_amdgcn_s_waitcnt(vmcnt_imm(3 * kVmPerKb)); break;
+                case 4: __builtin_amdgcn_s_waitcnt(vmcnt_imm(4 * kVmPerKb)); break;
+                case 5: __builtin_amdgcn_s_waitcnt(vmcnt_imm(5 * kVmPerKb)); break;
+                case 6: __builtin_amdgcn_s_waitcnt(vmcnt_imm(6 * kVmPerKb)); break;
+                default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(7 * kVmPerKb)); break;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) *reinterpret_cast<v4u*>(slot + wr[i]) = bw[k % D][i];
+            const v4u g0 = *reinterpret_cast<const v4u*>(slot + rd_g0);
+            const v4u g1 = *reinterpret_cast<const v4u*>(slot + rd_g1);
+            const v4u u0 = *reinterpret_cast<const v4u*>(slot + rd_u0);
+            const v4u u1 = *reinterpret_cast<const v4u*>(slot + rd_u1);
+            const v8i bg = {(int)g0[0], (int)g0[1], (int)g0[2], (int)g0[3], (int)g1[0], (int)g1[1], (int)g1[2], (int)g1[3]};
+            const v8i bu = {(int)u0[0], (int)u0[1], (int)u0[2], (int)u0[3], (int)u1[0], (int)u1[1], (int)u1[2], (int)u1[3]};
+            const int kb = kb0 + k;
+            const float fg = bs[k % D] * sg[kb], fu = bs[k % D] * su[kb];
+            const v4f tg = mfma_fp8(bg, ba[k % D], zero);
+            const v4f tu = mfma_fp8(bu, ba[k % D], zero);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                ag[v] = __builtin_fmaf(tg[v], fg, ag[v]);
+                au[v] = __builtin_fmaf(tu[v], fu, au[v]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+
+        red[wave][0][lane] = ag;
+        red[wave][1][lane] = au;
+        __syncthreads();
+        if (wave == 0) {
+            v4f g = red[0][0][lane], u = red[0][1][lane];
+#pragma unroll
+            for (int q = 1; q < KSPLIT; ++q) {
+                g += red[q][0][lane];
+                u += red[q][1][lane];
+            }
+            if (r16 < nrows) store_swiglu4(inter, row0 + r16, ng * 16 + kq * 4, g, u);
+        }
+        __syncthreads();
+    }
+}
+
 // Persistent form of gemm1_dma_kernel<1, 4, NS> (decode): a workgroup walks the items
 // blockIdx, blockIdx + gridDim, ... and each wave's LDS ring runs on across item
 // boundaries, so the first NS-1 K blocks of the next item are in flight while the
@@ -1043,6 +1173,14 @@ bool launch_gemm1(int variant, const uint8_t* hidden, const float* hs_scale, int
         case 13:
             hipLaunchKernelGGL(gemm1_prefill8_kernel, dim3(prefill_grid), dim3(512), 0, stream,
                                hidden, hs_scale, T, w1, s1, tiles, num_tiles, sorted_tok, C);
+            return true;
+        case 15:   // register-staged streaming, ring of 4 K blocks
+            hipLaunchKernelGGL(gemm1_rstream_kernel<4>, dim3(grid_for(mt * G)), dim3(256), 0, stream,
+                               hidden, hs_scale, T, w1, s1, tiles, num_tiles, sorted_tok, inter);
+            return true;
+        case 16:   // register-staged streaming, ring of 6 K blocks
+            hipLaunchKernelGGL(gemm1_rstream_kernel<6>, dim3(grid_for(mt * G)), dim3(256), 0, stream,
+                               hidden, hs_scale, T, w1, s1, tiles, num_tiles, sorted_tok, inter);
             return true;
         case 14:   // persistent streaming, 16-row tiles, two workgroups per CU
             hipLaunchKernelGGL(gemm1_pstream_kernel<4>, dim3(grid_for(mt * G) < 512 ? grid_for(mt * G) : 512),
