@@ -63,7 +63,7 @@ bool variant_c_hilo(int v) { return v == 12 || v == 13; }
 
 Plan choose_plan(int32_t T) {
     Plan p;
-    if (T <= 96) p = {16, 15, 15};
+    if (T <= 96) p = {16, 15, 16};
     else if (T <= 256) p = {32, 11, 10};
     else if (T <= 2048) p = {128, 12, 12};
     else p = {256, 13, 13};
@@ -71,7 +71,7 @@ Plan choose_plan(int32_t T) {
     const char* e2 = getenv("MOE_MI355_G2");
     const int env_g1 = e1 ? atoi(e1) : -99;
     const int env_g2 = e2 ? atoi(e2) : -99;
-    if (env_g1 >= -1 && env_g1 <= 16 && env_g2 >= -1 && env_g2 <= 16 &&
+    if (env_g1 >= -1 && env_g1 <= 18 && env_g2 >= -1 && env_g2 <= 18 &&
         variant_tile_m(env_g1) == variant_tile_m(env_g2) &&
         variant_c_hilo(env_g1) == variant_c_hilo(env_g2))
         p = {variant_tile_m(env_g1), env_g1, env_g2};

@@ -436,22 +436,23 @@ __global__ __launch_bounds__(256) void gemm2_dma_kernel(
 }
 
 // Register-staged W2 streaming (decode): the work split of gemm2_dma_kernel<1, KSPLIT,
-// ., 1>, with the W2 bytes of a K block (16 rows x 128 B, two full-line loads) and the
+// ., HF>, with the W2 bytes of a K block (16 HF rows x 128 B, full-line loads) and the
 // bf16 C fragments held in a ring of D K blocks in VGPRs, and each W2 block moved to
-// the MFMA layout through a 2 KB per-wave LDS slot.  Without an LDS ring more waves
-// fit per CU, so more bytes are in flight.
-template <int D, int KSPLIT>
+// the MFMA layout through a per-wave LDS slot.  Without an LDS ring more waves fit per
+// CU, so more bytes are in flight; HF > 1 shares each C fragment load among HF groups
+// of 16 output columns.
+template <int D, int KSPLIT, int HF>
 __global__ __launch_bounds__(256) void gemm2_rstream_kernel(
     const uint16_t* __restrict__ inter, const uint8_t* __restrict__ w2,
     const float* __restrict__ s2, const int4* __restrict__ tiles,
     const int* __restrict__ num_tiles, float* __restrict__ out_rows) {
     constexpr int NGW = 4 / KSPLIT;
     constexpr int KB = kIB / KSPLIT;
-    constexpr int kItems = (kH / 16) / NGW;
-    constexpr int kVmPerKb = 2 + 4;                   // 2 W2 loads, 4 C loads
+    constexpr int kItems = (kH / 16) / (NGW * HF);
+    constexpr int kVmPerKb = 2 * HF + 4;              // W2 loads, 4 C loads
     static_assert(D >= 2 && (D - 1) * kVmPerKb < 64, "ring depth");
-    __shared__ __attribute__((aligned(1024))) uint8_t slot_lds[4][16 * kBlk];
-    __shared__ v4f red[KSPLIT > 1 ? 4 : 1][64];
+    __shared__ __attribute__((aligned(1024))) uint8_t slot_lds[4][16 * HF * kBlk];
+    __shared__ v4f red[KSPLIT > 1 ? 4 : 1][HF][64];
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -464,9 +465,9 @@ __global__ __launch_bounds__(256) void gemm2_rstream_kernel(
     const int swz = swz128(r16);
     const int rd0 = r16 * kBlk + (((2 * kq) ^ swz) << 4);
     const int rd1 = r16 * kBlk + (((2 * kq + 1) ^ swz) << 4);
-    int wr[2];
+    int wr[2 * HF];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < 2 * HF; ++i) {
         const int r = 8 * i + drow;
         wr[i] = r * kBlk + ((dchunk ^ swz128(r)) << 4);
     }
@@ -474,22 +475,24 @@ __global__ __launch_bounds__(256) void gemm2_rstream_kernel(
 
     for (int work = blockIdx.x; work < nwork; work += gridDim.x) {
         const int4 tile = tiles[work / kItems];
-        const int hg = (work % kItems) * NGW + ngl;
+        const int hg = ((work % kItems) * NGW + ngl) * HF;   // first of HF column groups
         const int le = tile.x, row0 = tile.y, nrows = tile.z;
         // C row r16: bf16 elements 32 kq + 8 j .. of each K block feed MFMA j
         const uint8_t* cp = reinterpret_cast<const uint8_t*>(inter + (size_t)(row0 + min(r16, nrows - 1)) * kI) + kq * 64;
-        const uint8_t* wsrc[2];
+        const uint8_t* wsrc[2 * HF];
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < 2 * HF; ++i)
             wsrc[i] = w2 + (size_t)(le * kH + hg * 16 + 8 * i + drow) * kI + dchunk * 16;
-        const float* sp = s2 + (size_t)(le * kHB + (hg >> 3)) * kIB;
+        const float* sp[HF];
+#pragma unroll
+        for (int hf = 0; hf < HF; ++hf) sp[hf] = s2 + (size_t)(le * kHB + ((hg + hf) >> 3)) * kIB;
 
-        v4u bw[D][2];
+        v4u bw[D][2 * HF];
         v4u bc[D][4];
         auto issue = [&](int k) {
             const int kb = kb0 + k;
 #pragma unroll
-            for (int i = 0; i < 2; ++i) bw[k % D][i] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(wsrc[i] + kb * kBlk));
+            for (int i = 0; i < 2 * HF; ++i) bw[k % D][i] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(wsrc[i] + kb * kBlk));
 #pragma unroll
             for (int j = 0; j < 4; ++j) bc[k % D][j] = *reinterpret_cast<const v4u*>(cp + kb * 2 * kBlk + 16 * j);
         };
@@ -498,7 +501,9 @@ __global__ __launch_bounds__(256) void gemm2_rstream_kernel(
             issue(k);
             __builtin_amdgcn_sched_barrier(0);
         }
-        v4f acc = zero;
+        v4f acc[HF];
+#pragma unroll
+        for (int hf = 0; hf < HF; ++hf) acc[hf] = zero;
 #pragma unroll
         for (int k = 0; k < KB; ++k) {
             if (k + D - 1 < KB) issue(k + D - 1);
@@ -516,37 +521,46 @@ __global__ __launch_bounds__(256) void gemm2_rstream_kernel(
             }
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int i = 0; i < 2; ++i) *reinterpret_cast<v4u*>(slot + wr[i]) = bw[k % D][i];
-            const v4u x0 = *reinterpret_cast<const v4u*>(slot + rd0);
-            const v4u x1 = *reinterpret_cast<const v4u*>(slot + rd1);
-            const uint32_t ww[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-            v4f t = zero;
+            for (int i = 0; i < 2 * HF; ++i) *reinterpret_cast<v4u*>(slot + wr[i]) = bw[k % D][i];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                uint32_t d0, d1, d2, d3;
-                e4m3x4_to_bf16x4(ww[2 * j], d0, d1);
-                e4m3x4_to_bf16x4(ww[2 * j + 1], d2, d3);
-                t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(d0, d1, d2, d3),
-                                                             __builtin_bit_cast(v8bf, bc[k % D][j]), t, 0, 0, 0);
+            for (int hf = 0; hf < HF; ++hf) {
+                const v4u x0 = *reinterpret_cast<const v4u*>(slot + hf * 16 * kBlk + rd0);
+                const v4u x1 = *reinterpret_cast<const v4u*>(slot + hf * 16 * kBlk + rd1);
+                const uint32_t ww[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+                v4f t = zero;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    uint32_t d0, d1, d2, d3;
+                    e4m3x4_to_bf16x4(ww[2 * j], d0, d1);
+                    e4m3x4_to_bf16x4(ww[2 * j + 1], d2, d3);
+                    t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(d0, d1, d2, d3),
+                                                                 __builtin_bit_cast(v8bf, bc[k % D][j]), t, 0, 0, 0);
+                }
+                const float sb = sp[hf][kb0 + k];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[hf][v] = __builtin_fmaf(t[v], sb, acc[hf][v]);
             }
-            const float sb = sp[kb0 + k];
-#pragma unroll
-            for (int v = 0; v < 4; ++v) acc[v] = __builtin_fmaf(t[v], sb, acc[v]);
             __builtin_amdgcn_sched_barrier(0);
         }
 
         if constexpr (KSPLIT == 1) {
-            if (r16 < nrows)
-                *reinterpret_cast<v4f*>(out_rows + (size_t)(row0 + r16) * kH + hg * 16 + kq * 4) = acc;
-        } else {
-            red[wave][lane] = acc;
-            __syncthreads();
-            if (ks == 0) {
-                v4f o = red[wave][lane];
+            if (r16 < nrows) {
 #pragma unroll
-                for (int q = 1; q < KSPLIT; ++q) o += red[wave + q][lane];
-                if (r16 < nrows)
-                    *reinterpret_cast<v4f*>(out_rows + (size_t)(row0 + r16) * kH + hg * 16 + kq * 4) = o;
+                for (int hf = 0; hf < HF; ++hf)
+                    *reinterpret_cast<v4f*>(out_rows + (size_t)(row0 + r16) * kH + (hg + hf) * 16 + kq * 4) = acc[hf];
+            }
+        } else {
+#pragma unroll
+            for (int hf = 0; hf < HF; ++hf) red[wave][hf][lane] = acc[hf];
+            __syncthreads();
+            if (ks == 0 && r16 < nrows) {
+#pragma unroll
+                for (int hf = 0; hf < HF; ++hf) {
+                    v4f o = red[wave][hf][lane];
+#pragma unroll
+                    for (int q = 1; q < KSPLIT; ++q) o += red[wave + q][hf][lane];
+                    *reinterpret_cast<v4f*>(out_rows + (size_t)(row0 + r16) * kH + (hg + hf) * 16 + kq * 4) = o;
+                }
             }
             __syncthreads();
         }
@@ -769,11 +783,19 @@ bool launch_gemm2(int variant, const Intermediate& C, const uint8_t* w2, const f
                                s2, tiles, num_tiles, out_rows);
             return true;
         case 15:   // register-staged streaming, K split 4 ways
-            hipLaunchKernelGGL((gemm2_rstream_kernel<4, 4>), dim3(grid_for2(mt * (kH / 16))), dim3(256), 0,
+            hipLaunchKernelGGL((gemm2_rstream_kernel<4, 4, 1>), dim3(grid_for2(mt * (kH / 16))), dim3(256), 0,
                                stream, inter, w2, s2, tiles, num_tiles, out_rows);
             return true;
-        case 16:   // register-staged streaming, K split 2 ways
-            hipLaunchKernelGGL((gemm2_rstream_kernel<4, 2>), dim3(grid_for2(mt * (kH / 16) / 2)), dim3(256), 0,
+        case 16:   // register-staged streaming, K split 4 ways, 32 output columns per wave
+            hipLaunchKernelGGL((gemm2_rstream_kernel<4, 4, 2>), dim3(grid_for2(mt * (kH / 32))), dim3(256), 0,
+                               stream, inter, w2, s2, tiles, num_tiles, out_rows);
+            return true;
+        case 17:   // register-staged streaming, K split 2 ways, 32 output columns per wave
+            hipLaunchKernelGGL((gemm2_rstream_kernel<4, 2, 2>), dim3(grid_for2(mt * (kH / 32) / 2)), dim3(256), 0,
+                               stream, inter, w2, s2, tiles, num_tiles, out_rows);
+            return true;
+        case 18:   // register-staged streaming, K split 4 ways, 64 output columns per wave
+            hipLaunchKernelGGL((gemm2_rstream_kernel<3, 4, 4>), dim3(grid_for2(mt * (kH / 64))), dim3(256), 0,
                                stream, inter, w2, s2, tiles, num_tiles, out_rows);
             return true;
         case -1:
