@@ -99,7 +99,7 @@ bool fill_layout(int32_t T, moe_mi355_workspace_layout* L) {
     L->tiles = take((size_t)mt * 2 * 16);   // room for a second, half-height tile list
     L->sorted_tokens = take(R * 4);
     L->sorted_weights = take(R * 4);
-    L->chunk_counts = take((size_t)((T + 1023) / 1024) * moe::kEL * 4);
+    L->chunk_counts = take((size_t)((T + 255) / 256) * moe::kEL * 4);
     L->intermediate = take(R * moe::kI * 2);
     L->intermediate_scales = take(R * moe::kIB * 4);
     L->expert_out = take(R * moe::kH * 4);

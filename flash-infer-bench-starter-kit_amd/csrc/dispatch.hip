@@ -1,5 +1,5 @@
 // dispatch.hip -- local-expert histogram, exclusive scan and the deterministic
-// (local expert asc, token asc) permutation, in one 1024-thread workgroup.
+// (local expert asc, token asc) permutation.
 //
 // Reference: solution/python/kernel.cu:503-547 (exclusive scan of the counts),
 // kernel.cu:321-351 (fill + inverse slot map; there the slot inside an expert comes
@@ -12,10 +12,10 @@
 // permutation) and the GEMMs walk a list of row tiles of <= TM rows, each inside one
 // expert: tiles[i] = (expert, first row, rows, 0).
 //
-// Placement is atomic-free: tokens are taken in chunks of 1024 (one per thread); for
-// each expert a wave ballot gives every lane its rank inside the wave and the wave's
-// count.  Up to 1024 tokens one workgroup does everything in one pass; beyond that a
-// count kernel writes per-chunk expert counts and a place kernel (one workgroup per
+// Placement is atomic-free: one token per thread; for each expert a wave ballot gives
+// every lane its rank inside the wave and the wave's count.  Up to 1024 tokens one
+// workgroup (sized to T) does everything in one pass; beyond that a count kernel
+// writes per-chunk (256 tokens) expert counts and a place kernel (one workgroup per
 // chunk) turns them into each chunk's base and writes the permutation.
 
 #include "moe_device.h"
@@ -169,49 +169,67 @@ __global__ __launch_bounds__(64 * NW) void dispatch_small_kernel(
     place(r, rank, tid, T, wbase[wave], sorted_tok, sorted_w, inv);
 }
 
-// T > 1024, pass 1: chunk c (1024 tokens) writes its per-expert counts.
-__global__ __launch_bounds__(1024) void dispatch_count_kernel(
+// T > 1024, pass 1: chunk c (kChunk tokens) writes its per-expert counts.
+constexpr int kChunk = 256;
+constexpr int kChunkWaves = kChunk / 64;
+
+__global__ __launch_bounds__(kChunk) void dispatch_count_kernel(
     const int* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int offset,
     int* __restrict__ chunk_cnt) {
-    __shared__ int wcnt[16][kEL];
+    __shared__ int wcnt[kChunkWaves][kEL];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const TokenRoutes r = load_routes(topk_ids, topk_w, blockIdx.x * 1024 + tid, T, offset);
+    const TokenRoutes r = load_routes(topk_ids, topk_w, blockIdx.x * kChunk + tid, T, offset);
     int rank[kTopK];
     wave_ranks(r, wave, lane, wcnt, rank);
     __syncthreads();
     if (tid < kEL) {
         int c = 0;
-        for (int w = 0; w < 16; ++w) c += wcnt[w][tid];
+        for (int w = 0; w < kChunkWaves; ++w) c += wcnt[w][tid];
         chunk_cnt[blockIdx.x * kEL + tid] = c;
     }
 }
 
 // T > 1024, pass 2: every chunk derives the expert offsets and its own base from the
-// chunk count table, places its tokens; chunk 0 also writes offsets and tiles.
+// chunk count table (thread t sums expert t % 32 over chunks = t / 32 mod 8, then the
+// eight partial sums are added in a fixed order), places its tokens; chunk 0 also
+// writes offsets and tiles.
 template <int TM>
-__global__ __launch_bounds__(1024) void dispatch_place_kernel(
+__global__ __launch_bounds__(kChunk) void dispatch_place_kernel(
     const int* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int offset,
     const int* __restrict__ chunk_cnt, int nchunks, int* __restrict__ exp_off,
     int* __restrict__ num_tiles, int4* __restrict__ tiles, int* __restrict__ num_tiles2,
     int4* __restrict__ tiles2, int* __restrict__ sorted_tok, float* __restrict__ sorted_w,
     int* __restrict__ inv) {
-    __shared__ int wcnt[16][kEL];
-    __shared__ int wbase[16][kEL];
+    constexpr int kGroups = kChunk / kEL;       // 8 chunk strides
+    __shared__ int wcnt[kChunkWaves][kEL];
+    __shared__ int wbase[kChunkWaves][kEL];
     __shared__ int off[kEL];
     __shared__ int cbase[kEL];
+    __shared__ int part[2][kGroups][kEL];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int chunk = blockIdx.x;
 
-    const TokenRoutes r = load_routes(topk_ids, topk_w, chunk * 1024 + tid, T, offset);
+    const TokenRoutes r = load_routes(topk_ids, topk_w, chunk * kChunk + tid, T, offset);
     int rank[kTopK];
     wave_ranks(r, wave, lane, wcnt, rank);
+    {
+        const int e = tid % kEL, g = tid / kEL;
+        int total = 0, before = 0;
+        for (int c = g; c < nchunks; c += kGroups) {
+            const int v = chunk_cnt[c * kEL + e];
+            before += (c < chunk) ? v : 0;
+            total += v;
+        }
+        part[0][g][e] = total;
+        part[1][g][e] = before;
+    }
+    __syncthreads();
     if (wave == 0) {
         int total = 0, before = 0;
         if (lane < kEL) {
-            for (int c = 0; c < nchunks; ++c) {
-                const int v = chunk_cnt[c * kEL + lane];
-                before += (c < chunk) ? v : 0;
-                total += v;
+            for (int g = 0; g < kGroups; ++g) {
+                total += part[0][g][lane];
+                before += part[1][g][lane];
             }
         }
         if (chunk == 0) {
@@ -226,13 +244,13 @@ __global__ __launch_bounds__(1024) void dispatch_place_kernel(
     __syncthreads();
     if (tid < kEL) {
         int run = off[tid] + cbase[tid];
-        for (int w = 0; w < 16; ++w) {
+        for (int w = 0; w < kChunkWaves; ++w) {
             wbase[w][tid] = run;
             run += wcnt[w][tid];
         }
     }
     __syncthreads();
-    place(r, rank, chunk * 1024 + tid, T, wbase[wave], sorted_tok, sorted_w, inv);
+    place(r, rank, chunk * kChunk + tid, T, wbase[wave], sorted_tok, sorted_w, inv);
 }
 
 int dispatch_max_tiles(int T, int tm) {
@@ -256,15 +274,15 @@ static void launch_dispatch_tm(const int* topk_ids, const float* topk_w, int T, 
 #undef DISPATCH_SMALL
         return;
     }
-    const int nchunks = (T + 1023) / 1024;
-    hipLaunchKernelGGL(dispatch_count_kernel, dim3(nchunks), dim3(1024), 0, stream, topk_ids, topk_w,
+    const int nchunks = (T + kChunk - 1) / kChunk;
+    hipLaunchKernelGGL(dispatch_count_kernel, dim3(nchunks), dim3(kChunk), 0, stream, topk_ids, topk_w,
                        T, offset, chunk_cnt);
-    hipLaunchKernelGGL(dispatch_place_kernel<TM>, dim3(nchunks), dim3(1024), 0, stream, topk_ids,
+    hipLaunchKernelGGL(dispatch_place_kernel<TM>, dim3(nchunks), dim3(kChunk), 0, stream, topk_ids,
                        topk_w, T, offset, chunk_cnt, nchunks, exp_off, num_tiles, tiles,
                        num_tiles2, tiles2, sorted_tok, sorted_w, inv);
 }
 
-// chunk_cnt: int32 [ceil(T/1024) * 32] scratch, needed when T > 1024.  tiles2 /
+// chunk_cnt: int32 [ceil(T/256) * 32] scratch, needed when T > 1024.  tiles2 /
 // num_tiles2 (may be null): a second tile list of tm/2 rows over the same rows.
 bool launch_dispatch(const int* topk_ids, const float* topk_w, int T, int offset, int tm,
                      int* exp_off, int* num_tiles, int4* tiles, int* sorted_tok,

@@ -7,7 +7,8 @@ Entry      : kernel.py::kernel
 
 Same signature, argument meaning and destination-passing contract as the
 reference's ``solution/python/kernel.py:95-120``; the work behind it is the C ABI of
-``include/moe_mi355.h`` (route -> dispatch -> FP8 GEMM1 + SwiGLU -> bf16 GEMM2 ->
+``include/moe_mi355.h`` (route -> dispatch -> FP8 GEMM1 + SwiGLU -> GEMM2 (bf16 MFMA
+for small T, FP8 MFMA over an fp8 hi/lo split of the SwiGLU rows for large T) ->
 ordered combine, all on the caller's current stream, no host synchronisation).
 
 The reference JIT-compiles its extension on first use (kernel.py:57-92); this one
@@ -295,7 +296,7 @@ def dispatch(topk_ids: torch.Tensor, topk_weights: torch.Tensor, local_expert_of
         inv=torch.empty(T, TOP_K, dtype=torch.int32, device=dev),
         tiles=torch.empty(max(1, mt), 4, dtype=torch.int32, device=dev),
         num_tiles=torch.empty(1, dtype=torch.int32, device=dev),
-        chunk_counts=torch.empty(max(1, (T + 1023) // 1024) * E_LOCAL, dtype=torch.int32, device=dev),
+        chunk_counts=torch.empty(max(1, (T + 255) // 256) * E_LOCAL, dtype=torch.int32, device=dev),
     )
     with torch.cuda.device(dev):
         rc = L.moe_mi355_dispatch(ids.data_ptr(), w.data_ptr(), T, int(local_expert_offset),

@@ -117,7 +117,7 @@ MOE_MI355_API int moe_mi355_route(const float* routing_logits, const uint16_t* r
  *   tiles          int32 [moe_mi355_max_tiles(T,tile_m), 4]  (expert, first row,
  *                               rows, 0) per tile of <= tile_m rows
  *   num_tiles      int32 [1]
- *   chunk_counts   int32 [ceil(T/1024) * 32] scratch (may be NULL when T <= 1024)
+ *   chunk_counts   int32 [ceil(T/256) * 32] scratch (may be NULL when T <= 1024)
  * tile_m must be 16, 32, 64, 128 or 256. */
 MOE_MI355_API int moe_mi355_dispatch(const int32_t* topk_ids, const float* topk_weights, int32_t T,
                        int64_t local_expert_offset, int32_t tile_m,
@@ -140,7 +140,7 @@ typedef struct moe_mi355_workspace_layout {
                                plans) a second list of 128-row tiles for GEMM2 */
     size_t sorted_tokens;   /* int32 [8T] */
     size_t sorted_weights;  /* fp32  [8T] */
-    size_t chunk_counts;    /* int32 [ceil(T/1024), 32] dispatch scratch */
+    size_t chunk_counts;    /* int32 [ceil(T/256), 32] dispatch scratch */
     size_t intermediate;    /* SwiGLU output rows C, 8T x 2048 x 2 bytes, in one of two
                                forms (intermediate_format):
                                0: bf16 [8T, 2048];
