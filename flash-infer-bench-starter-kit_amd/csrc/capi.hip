@@ -40,41 +40,36 @@ namespace {
 constexpr int32_t kMaxT = 1 << 19;
 constexpr int kMinTileM = 16;           // smallest row tile; sizes the tile list
 
-// Kernel plan per token count.  Small T streams weights with the register-staged
-// kernels (T <= 96, 16-row tiles) or the LDS-landed DMA kernels (32-row tiles), C in
-// bf16; large T uses the MFMA-bound prefill kernels (128- or 256-row tiles, C in the
-// fp8 hi/lo form).
-// Variant ids are those of launch_gemm1 / launch_gemm2; MOE_MI355_G1 / MOE_MI355_G2
-// override them for tuning sweeps (ignored unless both imply the same tile height
-// and the same form of C).
+// Kernel plan per token count: the dispatch tile height and the GEMM1 / GEMM2 variants
+// (ids of launch_gemm1 / launch_gemm2).  Small T streams weights with the
+// register-staged kernels (T <= 96, 16-row tiles) or the LDS-landed DMA kernels
+// (32-row tiles), C in bf16; large T uses the MFMA-bound prefill kernels (128- or
+// 256-row tiles, C in the fp8 hi/lo form; with 256-row tiles GEMM2 walks the 128-row
+// second tile list).  MOE_MI355_G1 / MOE_MI355_G2 override the variants for tuning
+// sweeps; the override is ignored unless both imply the same tile height and the same
+// form of C.
 struct Plan {
     int tm, g1, g2;
 };
 
-int variant_tile_m(int v) {
-    if (v < 0) return 64;
-    if (v == 12) return 128;
-    if (v == 13) return 256;
-    if (v >= 14) return 16;
-    return (v % 6) < 3 ? 16 : 32;
-}
-
-bool variant_c_hilo(int v) { return v == 12 || v == 13; }
+int g1_tile_m(int v) { return v <= 2 ? 16 : v == 3 ? 32 : v == 4 ? 128 : 256; }
+int g2_tile_m(int v) { return v <= 4 ? 16 : v == 5 ? 32 : v == 6 ? 128 : 256; }
+bool g1_hilo(int v) { return v >= 4; }
+bool g2_hilo(int v) { return v >= 6; }
 
 Plan choose_plan(int32_t T) {
     Plan p;
-    if (T <= 96) p = {16, 15, 16};
-    else if (T <= 256) p = {32, 11, 10};
-    else if (T <= 2048) p = {128, 12, 12};
-    else p = {256, 13, 13};
+    if (T <= 96) p = {16, 1, 2};
+    else if (T <= 256) p = {32, 3, 5};
+    else if (T <= 2048) p = {128, 4, 6};
+    else p = {256, 5, 7};
     const char* e1 = getenv("MOE_MI355_G1");
     const char* e2 = getenv("MOE_MI355_G2");
-    const int env_g1 = e1 ? atoi(e1) : -99;
-    const int env_g2 = e2 ? atoi(e2) : -99;
-    if (env_g1 >= -1 && env_g1 <= 18 && env_g2 >= -1 && env_g2 <= 18 &&
-        variant_tile_m(env_g1) == variant_tile_m(env_g2) &&
-        variant_c_hilo(env_g1) == variant_c_hilo(env_g2))
-        p = {variant_tile_m(env_g1), env_g1, env_g2};
+    const int env_g1 = e1 ? atoi(e1) : 0;
+    const int env_g2 = e2 ? atoi(e2) : 0;
+    if (env_g1 >= 1 && env_g1 <= 5 && env_g2 >= 1 && env_g2 <= 7 &&
+        g1_tile_m(env_g1) == g2_tile_m(env_g2) && g1_hilo(env_g1) == g2_hilo(env_g2))
+        p = {g1_tile_m(env_g1), env_g1, env_g2};
     return p;
 }
 
@@ -107,7 +102,7 @@ bool fill_layout(int32_t T, moe_mi355_workspace_layout* L) {
     const Plan plan = choose_plan(T);
     L->tile_m = plan.tm;
     L->max_tiles = mt;
-    L->intermediate_format = variant_c_hilo(plan.g1) ? 1 : 0;
+    L->intermediate_format = g1_hilo(plan.g1) ? 1 : 0;
     return true;
 }
 
@@ -250,8 +245,8 @@ int moe_mi355_forward(const moe_mi355_args* a, void* stream) {
     if (prof) prof_record(slot, 1, s);
     const Plan plan = choose_plan(T);
     const int max_tiles = moe::dispatch_max_tiles(T, plan.tm);
-    // GEMM2 variant 13 walks the half-height (128-row) tiles of a 256-row dispatch
-    const bool half = plan.g2 == 13;
+    // GEMM2 variant 7 walks the half-height (128-row) tiles of a 256-row dispatch
+    const bool half = plan.g2 == 7;
     int4* tiles2 = tiles + max_tiles;
     int* num_tiles2 = meta + moe::kEL + 2;
     moe::launch_dispatch(ids, wts, T, clamp_offset(a->local_expert_offset), plan.tm, meta,

@@ -8,18 +8,16 @@
 // C is written as one row per routed assignment for GEMM2: bf16 by the decode
 // kernels, the fp8 hi/lo form (moe_device.h, Intermediate) by the prefill kernels.
 //
-// Work item = (row tile of <= 16*MAXCB rows of one expert, group of 16 gate rows
-// n..n+15 paired with the 16 up rows 2048+n..).  The 4 waves of a workgroup split
-// the 56 K blocks (14 each) and reduce through LDS in a fixed order, so results do
-// not depend on scheduling.
+// Kernels: register-staged and LDS-landed weight streaming for small T (a work item is
+// one row tile x 16 gate + 16 up rows, its 56 K blocks split over the 4 waves of a
+// workgroup and reduced through LDS in a fixed order, so results do not depend on
+// scheduling), and MFMA-bound prefill kernels for large T (128- or 256-row tiles).
 //
 // MFMA: v_mfma_f32_16x16x128_f8f6f4 (e4m3 x e4m3), one instruction per 128-wide K
 // block, so the per-block scales multiply a fresh fp32 partial before it joins the
 // accumulator.  Weight rows feed operand A (16 n rows), gathered token rows feed
 // operand B (16 tokens); lane l holds row/token l%16 and K bytes 32*(l/16)..+31 of
 // the block for both operands, and receives D[n = 4*(l/16)+v][token = l%16].
-// Weight bytes stream from HBM straight into registers (each byte is used by exactly
-// one wave); the small token rows are re-read through L1/L2.
 
 #include "moe_device.h"
 
@@ -35,116 +33,12 @@ __device__ __forceinline__ v8i load_v8i(const uint8_t* p) {
     return r;
 }
 
-__device__ __forceinline__ v8i load_v8i_stream(const uint8_t* p) {
-    const v4f* q = reinterpret_cast<const v4f*>(p);
-    const v4f a = __builtin_nontemporal_load(q);
-    const v4f b = __builtin_nontemporal_load(q + 1);
-    v8i r;
-    r[0] = __float_as_int(a[0]); r[1] = __float_as_int(a[1]);
-    r[2] = __float_as_int(a[2]); r[3] = __float_as_int(a[3]);
-    r[4] = __float_as_int(b[0]); r[5] = __float_as_int(b[1]);
-    r[6] = __float_as_int(b[2]); r[7] = __float_as_int(b[3]);
-    return r;
-}
-
 __device__ __forceinline__ v4f mfma_fp8(const v8i& a, const v8i& b, const v4f& c) {
     // scale operands 0 -> plain (unscaled) e4m3 x e4m3 MFMA
     return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
 
 __device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
-
-template <int MAXCB>
-__global__ __launch_bounds__(256) void gemm1_swiglu_kernel(
-    const uint8_t* __restrict__ hidden, const float* __restrict__ hs_scale, int T,
-    const uint8_t* __restrict__ w1, const float* __restrict__ s1,
-    const int4* __restrict__ tiles, const int* __restrict__ num_tiles,
-    const int* __restrict__ sorted_tok, uint16_t* __restrict__ inter) {
-    constexpr int kGroups = kI / 16;         // 128 gate/up row-group pairs
-    constexpr int kKbPerWave = kHB / 4;      // 14
-    __shared__ v4f red[4][2][MAXCB][64];
-
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int r16 = lane & 15, kq = lane >> 4;
-    const int nwork = (*num_tiles) * kGroups;
-
-    for (int work = blockIdx.x; work < nwork; work += gridDim.x) {
-        const int4 tile = tiles[work / kGroups];
-        const int ng = work % kGroups;
-        const int le = tile.x, row0 = tile.y, nrows = tile.z;
-        const int ncb = (nrows + 15) >> 4;
-
-        int tok[MAXCB];
-#pragma unroll
-        for (int cb = 0; cb < MAXCB; ++cb) tok[cb] = sorted_tok[row0 + min(cb * 16 + r16, nrows - 1)];
-
-        const uint8_t* wg = w1 + (size_t)(le * kN1 + ng * 16 + r16) * kH + kq * 32;
-        const uint8_t* wu = wg + (size_t)kI * kH;
-        const float* sg = s1 + (size_t)(le * kN1B + (ng >> 3)) * kHB;
-        const float* su = sg + (size_t)kIB * kHB;
-
-        v4f ag[MAXCB], au[MAXCB];
-#pragma unroll
-        for (int cb = 0; cb < MAXCB; ++cb) {
-            ag[cb] = v4f{0.f, 0.f, 0.f, 0.f};
-            au[cb] = v4f{0.f, 0.f, 0.f, 0.f};
-        }
-        const v4f zero = {0.f, 0.f, 0.f, 0.f};
-        const int kb0 = wave * kKbPerWave;
-#pragma unroll 2
-        for (int kk = 0; kk < kKbPerWave; ++kk) {
-            const int kb = kb0 + kk;
-            const v8i bwg = load_v8i_stream(wg + kb * kBlk);
-            const v8i bwu = load_v8i_stream(wu + kb * kBlk);
-            const float sbg = sg[kb];
-            const float sbu = su[kb];
-#pragma unroll
-            for (int cb = 0; cb < MAXCB; ++cb) {
-                if (cb < ncb) {
-                    const v8i a = load_v8i(hidden + (size_t)tok[cb] * kH + kb * kBlk + kq * 32);
-                    const float sa = hs_scale[(size_t)kb * T + tok[cb]];
-                    const v4f tg = mfma_fp8(bwg, a, zero);
-                    const v4f tu = mfma_fp8(bwu, a, zero);
-                    const float fg = sa * sbg, fu = sa * sbu;
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        ag[cb][v] = __builtin_fmaf(tg[v], fg, ag[cb][v]);
-                        au[cb][v] = __builtin_fmaf(tu[v], fu, au[cb][v]);
-                    }
-                }
-            }
-        }
-
-#pragma unroll
-        for (int cb = 0; cb < MAXCB; ++cb) {
-            if (cb < ncb) {
-                red[wave][0][cb][lane] = ag[cb];
-                red[wave][1][cb][lane] = au[cb];
-            }
-        }
-        __syncthreads();
-        for (int cb = wave; cb < ncb; cb += 4) {
-            v4f g = red[0][0][cb][lane];
-            v4f u = red[0][1][cb][lane];
-#pragma unroll
-            for (int w = 1; w < 4; ++w) {
-                g += red[w][0][cb][lane];
-                u += red[w][1][cb][lane];
-            }
-            const int r = cb * 16 + r16;
-            if (r < nrows) {
-                uint32_t h[4];
-#pragma unroll
-                for (int v = 0; v < 4; ++v) h[v] = f32_to_bf16_bits(silu_f32(u[v]) * g[v]);
-                uint2 pk;
-                pk.x = h[0] | (h[1] << 16);
-                pk.y = h[2] | (h[3] << 16);
-                *reinterpret_cast<uint2*>(inter + (size_t)(row0 + r) * kI + ng * 16 + kq * 4) = pk;
-            }
-        }
-        __syncthreads();
-    }
-}
 
 __device__ __forceinline__ void store_swiglu4(uint16_t* __restrict__ inter, int row, int n0,
                                               const v4f& g, const v4f& u) {
@@ -155,132 +49,6 @@ __device__ __forceinline__ void store_swiglu4(uint16_t* __restrict__ inter, int 
     pk.x = h[0] | (h[1] << 16);
     pk.y = h[2] | (h[3] << 16);
     *reinterpret_cast<uint2*>(inter + (size_t)row * kI + n0) = pk;
-}
-
-// Weight-streaming GEMM1 for small token counts (decode).  Same arithmetic as
-// gemm1_swiglu_kernel; the difference is how the weight bytes move:
-//   - a work item is (row tile of <= 16*CB rows, 16 gate + 16 up rows); a workgroup
-//     runs 4/KSPLIT items side by side and KSPLIT waves split each item's 56 K blocks;
-//   - every wave keeps a ring of D K blocks of weights, token rows and token scales
-//     in registers, refilled as soon as a stage is consumed, so each wave always has
-//     D blocks (D * 4 KB of weights) in flight; weights use non-temporal loads.
-template <int CB, int KSPLIT, int D>
-__global__ __launch_bounds__(256) void gemm1_stream_kernel(
-    const uint8_t* __restrict__ hidden, const float* __restrict__ hs_scale, int T,
-    const uint8_t* __restrict__ w1, const float* __restrict__ s1,
-    const int4* __restrict__ tiles, const int* __restrict__ num_tiles,
-    const int* __restrict__ sorted_tok, uint16_t* __restrict__ inter) {
-    constexpr int NGW = 4 / KSPLIT;           // items per workgroup
-    constexpr int KB = kHB / KSPLIT;          // K blocks per wave
-    constexpr int kItems = (kI / 16) / NGW;   // workgroup work units per tile
-    __shared__ v4f red[KSPLIT > 1 ? 4 : 1][2][CB][64];
-
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int r16 = lane & 15, kq = lane >> 4;
-    const int ngl = wave / KSPLIT, ks = wave % KSPLIT;
-    const int nwork = (*num_tiles) * kItems;
-    const v4f zero = {0.f, 0.f, 0.f, 0.f};
-
-    for (int work = blockIdx.x; work < nwork; work += gridDim.x) {
-        const int4 tile = tiles[work / kItems];
-        const int ng = (work % kItems) * NGW + ngl;
-        const int le = tile.x, row0 = tile.y, nrows = tile.z;
-        const int ncb = (nrows + 15) >> 4;
-
-        const uint8_t* ap[CB];
-        const float* sp[CB];
-#pragma unroll
-        for (int cb = 0; cb < CB; ++cb) {
-            const int tok = sorted_tok[row0 + min(cb * 16 + r16, nrows - 1)];
-            ap[cb] = hidden + (size_t)tok * kH + kq * 32;
-            sp[cb] = hs_scale + tok;
-        }
-        const uint8_t* wg = w1 + (size_t)(le * kN1 + ng * 16 + r16) * kH + kq * 32;
-        const uint8_t* wu = wg + (size_t)kI * kH;
-        const float* sg = s1 + (size_t)(le * kN1B + (ng >> 3)) * kHB;
-        const float* su = sg + (size_t)kIB * kHB;
-        const int kb0 = ks * KB;
-
-        v8i bg[D], bu[D], ba[D][CB];
-        float bs[D][CB];
-#pragma unroll
-        for (int d = 0; d < D; ++d) {
-            const int kb = kb0 + d;
-            bg[d] = load_v8i_stream(wg + kb * kBlk);
-            bu[d] = load_v8i_stream(wu + kb * kBlk);
-#pragma unroll
-            for (int cb = 0; cb < CB; ++cb) {
-                ba[d][cb] = load_v8i(ap[cb] + kb * kBlk);
-                bs[d][cb] = sp[cb][(size_t)kb * T];
-            }
-        }
-        v4f ag[CB], au[CB];
-#pragma unroll
-        for (int cb = 0; cb < CB; ++cb) { ag[cb] = zero; au[cb] = zero; }
-
-#pragma unroll
-        for (int k = 0; k < KB; ++k) {
-            const int d = k % D;
-            const int kb = kb0 + k;
-            const float fsg = sg[kb], fsu = su[kb];
-#pragma unroll
-            for (int cb = 0; cb < CB; ++cb) {
-                if (cb < ncb) {
-                    const v4f tg = mfma_fp8(bg[d], ba[d][cb], zero);
-                    const v4f tu = mfma_fp8(bu[d], ba[d][cb], zero);
-                    const float fg = bs[d][cb] * fsg, fu = bs[d][cb] * fsu;
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        ag[cb][v] = __builtin_fmaf(tg[v], fg, ag[cb][v]);
-                        au[cb][v] = __builtin_fmaf(tu[v], fu, au[cb][v]);
-                    }
-                }
-            }
-            if (k + D < KB) {
-                const int nkb = kb + D;
-                bg[d] = load_v8i_stream(wg + nkb * kBlk);
-                bu[d] = load_v8i_stream(wu + nkb * kBlk);
-#pragma unroll
-                for (int cb = 0; cb < CB; ++cb) {
-                    ba[d][cb] = load_v8i(ap[cb] + nkb * kBlk);
-                    bs[d][cb] = sp[cb][(size_t)nkb * T];
-                }
-            }
-        }
-
-        if constexpr (KSPLIT == 1) {
-#pragma unroll
-            for (int cb = 0; cb < CB; ++cb) {
-                const int r = cb * 16 + r16;
-                if (cb < ncb && r < nrows) store_swiglu4(inter, row0 + r, ng * 16 + kq * 4, ag[cb], au[cb]);
-            }
-        } else {
-#pragma unroll
-            for (int cb = 0; cb < CB; ++cb) {
-                if (cb < ncb) {
-                    red[wave][0][cb][lane] = ag[cb];
-                    red[wave][1][cb][lane] = au[cb];
-                }
-            }
-            __syncthreads();
-            if (ks == 0) {
-#pragma unroll
-                for (int cb = 0; cb < CB; ++cb) {
-                    const int r = cb * 16 + r16;
-                    if (cb < ncb) {
-                        v4f g = red[wave][0][cb][lane], u = red[wave][1][cb][lane];
-#pragma unroll
-                        for (int q = 1; q < KSPLIT; ++q) {
-                            g += red[wave + q][0][cb][lane];
-                            u += red[wave + q][1][cb][lane];
-                        }
-                        if (r < nrows) store_swiglu4(inter, row0 + r, ng * 16 + kq * 4, g, u);
-                    }
-                }
-            }
-            __syncthreads();
-        }
-    }
 }
 
 // ---------------------------------------------------------------------------
@@ -588,168 +356,6 @@ __global__ __launch_bounds__(256) void gemm1_rstream_kernel(
             if (r16 < nrows) store_swiglu4(inter, row0 + r16, ng * 16 + kq * 4, g, u);
         }
         __syncthreads();
-    }
-}
-
-// Persistent form of gemm1_dma_kernel<1, 4, NS> (decode): a workgroup walks the items
-// blockIdx, blockIdx + gridDim, ... and each wave's LDS ring runs on across item
-// boundaries, so the first NS-1 K blocks of the next item are in flight while the
-// current item finishes and its four K quarters are reduced.  The ring position of a
-// K block is its running index mod NS; 14 K blocks per quarter make that position
-// alternate between two phases (PH = 0 or 14 mod NS), one instantiation each.
-// ---------------------------------------------------------------------------
-template <int NS>
-__global__ __launch_bounds__(256) void gemm1_pstream_kernel(
-    const uint8_t* __restrict__ hidden, const float* __restrict__ hs_scale, int T,
-    const uint8_t* __restrict__ w1, const float* __restrict__ s1,
-    const int4* __restrict__ tiles, const int* __restrict__ num_tiles,
-    const int* __restrict__ sorted_tok, uint16_t* __restrict__ inter) {
-    constexpr int KSPLIT = 4;
-    constexpr int KB = kHB / KSPLIT;                  // 14 K blocks per wave and item
-    constexpr int kItems = kI / 16;                   // 128 column groups per tile
-    constexpr int kSlot = 32 * kBlk;
-    constexpr int kVmPerKb = 4 + 3;
-    static_assert(NS >= 2 && NS <= 7 && (NS - 1) * kVmPerKb < 64, "ring depth");
-    __shared__ __attribute__((aligned(1024))) uint8_t ring[4][NS][kSlot];
-    __shared__ v4f red[4][2][64];
-
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    const int r16 = lane & 15, kq = lane >> 4;
-    const int ks = wave;
-    const int nwork = (*num_tiles) * kItems;
-    const v4f zero = {0.f, 0.f, 0.f, 0.f};
-    uint8_t* myring = &ring[wave][0][0];
-    const int drow = lane >> 3, dchunk = lane & 7;
-    const int swz = swz128(r16);
-    const int rd_g0 = r16 * kBlk + (((2 * kq) ^ swz) << 4);
-    const int rd_g1 = r16 * kBlk + (((2 * kq + 1) ^ swz) << 4);
-    const int rd_u0 = rd_g0 + 16 * kBlk;
-    const int rd_u1 = rd_g1 + 16 * kBlk;
-    const int kb0 = ks * KB;
-
-    // where the operands of one item come from
-    struct Src {
-        const uint8_t* w[4];      // DMA rows 8i + drow (0-15 gate, 16-31 up), K block 0
-        const uint8_t* a;         // token row, this lane's 32 bytes of K block 0
-        const float* sa;          // token scale column
-        const float* sg;          // gate / up weight scales of the column group
-        const float* su;
-        int row0, nrows, ng;
-    };
-    auto make_src = [&](int work) {
-        Src s;
-        const int4 tile = tiles[work / kItems];
-        s.ng = work % kItems;
-        const int le = tile.x;
-        s.row0 = tile.y;
-        s.nrows = tile.z;
-        const int tok = sorted_tok[s.row0 + min(r16, s.nrows - 1)];
-        s.a = hidden + (size_t)tok * kH + kq * 32;
-        s.sa = hs_scale + tok;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = 8 * i + drow;
-            const int n = (r < 16) ? s.ng * 16 + r : kI + s.ng * 16 + (r - 16);
-            s.w[i] = w1 + (size_t)(le * kN1 + n) * kH + ((dchunk ^ swz128(r)) << 4);
-        }
-        s.sg = s1 + (size_t)(le * kN1B + (s.ng >> 3)) * kHB;
-        s.su = s.sg + (size_t)kIB * kHB;
-        return s;
-    };
-
-    v8i ba[NS];
-    float bs[NS];
-    // K block k (0..KB-1 of this wave's quarter) of item src into ring position p
-    auto issue = [&](const Src& s, int k, auto pc) {
-        constexpr int p = decltype(pc)::value;
-        const int kb = kb0 + k;
-        uint8_t* slot = myring + p * kSlot;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) dma16(s.w[i] + kb * kBlk, slot + i * 1024);
-        ba[p] = load_v8i(s.a + kb * kBlk);
-        bs[p] = s.sa[(size_t)kb * T];
-    };
-
-    int work = blockIdx.x;
-    if (work >= nwork) return;                        // uniform per workgroup
-    Src cur = make_src(work);
-    // prologue: the first NS-1 K blocks of the first item (phase 0)
-    [&]<int... P>(std::integer_sequence<int, P...>) {
-        (issue(cur, P, IntC<P>{}), ...);
-    }(std::make_integer_sequence<int, NS - 1>{});
-    __builtin_amdgcn_sched_barrier(0);
-
-    auto item = [&](auto phc) {
-        constexpr int PH = decltype(phc)::value;
-        const int next = work + gridDim.x;
-        const bool has_next = next < nwork;           // uniform
-        const Src nxt = make_src(has_next ? next : work);
-        v4f ag = zero, au = zero;
-        [&]<int... K>(std::integer_sequence<int, K...>) {
-            ([&] {
-                constexpr int k = K;
-                constexpr int ki = k + NS - 1;        // K block issued at this step
-                if constexpr (ki < KB) {
-                    issue(cur, ki, IntC<(PH + ki) % NS>{});
-                } else {
-                    if (has_next) issue(nxt, ki - KB, IntC<(PH + ki) % NS>{});
-                }
-                __builtin_amdgcn_sched_barrier(0);
-                // K blocks issued after k: NS-1, fewer at the end of the last item
-                const int younger = (ki < KB || has_next) ? NS - 1 : (KB - 1 - k);
-                switch (younger) {
-                    case 6: __builtin_amdgcn_s_waitcnt(vmcnt_imm(6 * kVmPerKb)); break;
-                    case 5: __builtin_amdgcn_s_waitcnt(vmcnt_imm(5 * kVmPerKb)); break;
-                    case 4: __builtin_amdgcn_s_waitcnt(vmcnt_imm(4 * kVmPerKb)); break;
-                    case 3: __builtin_amdgcn_s_waitcnt(vmcnt_imm(3 * kVmPerKb)); break;
-                    case 2: __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kVmPerKb)); break;
-                    case 1: __builtin_amdgcn_s_waitcnt(vmcnt_imm(1 * kVmPerKb)); break;
-                    default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
-                }
-                __builtin_amdgcn_sched_barrier(0);
-                constexpr int p = (PH + k) % NS;
-                const uint8_t* slot = myring + p * kSlot;
-                const v4u g0 = *reinterpret_cast<const v4u*>(slot + rd_g0);
-                const v4u g1 = *reinterpret_cast<const v4u*>(slot + rd_g1);
-                const v4u u0 = *reinterpret_cast<const v4u*>(slot + rd_u0);
-                const v4u u1 = *reinterpret_cast<const v4u*>(slot + rd_u1);
-                const v8i bg = {(int)g0[0], (int)g0[1], (int)g0[2], (int)g0[3], (int)g1[0], (int)g1[1], (int)g1[2], (int)g1[3]};
-                const v8i bu = {(int)u0[0], (int)u0[1], (int)u0[2], (int)u0[3], (int)u1[0], (int)u1[1], (int)u1[2], (int)u1[3]};
-                const int kb = kb0 + k;
-                const float fg = bs[p] * cur.sg[kb], fu = bs[p] * cur.su[kb];
-                const v4f tg = mfma_fp8(bg, ba[p], zero);
-                const v4f tu = mfma_fp8(bu, ba[p], zero);
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    ag[v] = __builtin_fmaf(tg[v], fg, ag[v]);
-                    au[v] = __builtin_fmaf(tu[v], fu, au[v]);
-                }
-                __builtin_amdgcn_sched_barrier(0);
-            }(), ...);
-        }(std::make_integer_sequence<int, KB>{});
-
-        // reduce the four K quarters (fixed order) and store the SwiGLU rows
-        red[wave][0][lane] = ag;
-        red[wave][1][lane] = au;
-        __syncthreads();
-        if (wave == 0) {
-            v4f g = red[0][0][lane], u = red[0][1][lane];
-#pragma unroll
-            for (int q = 1; q < KSPLIT; ++q) {
-                g += red[q][0][lane];
-                u += red[q][1][lane];
-            }
-            if (r16 < cur.nrows) store_swiglu4(inter, cur.row0 + r16, cur.ng * 16 + kq * 4, g, u);
-        }
-        __syncthreads();
-        cur = nxt;
-        work = next;
-        return has_next;
-    };
-    for (;;) {
-        if (!item(IntC<0>{})) break;
-        if (!item(IntC<(KB % NS)>{})) break;
     }
 }
 
@@ -1133,68 +739,42 @@ __global__ __launch_bounds__(512, 1) void gemm1_prefill8_kernel(
 
 static int grid_for(long long work) { return (int)(work < 4096 ? work : 4096); }
 
-// variant: 0..5 register-ring streaming, 6..11 LDS-landed streaming, both with
-// (CB, KSPLIT) = (1,1) (1,2) (1,4) (2,1) (2,2) (2,4) and bf16 C; 12 the 128-row and
-// 13 the 256-row prefill kernel, both writing C in the fp8 hi/lo form; -1 the
-// 64-row tile kernel (bf16 C)
+// Variants (the tile height of the dispatch they expect, and the form of C they write):
+//   1  register-staged streaming, ring of 4 K blocks     16-row tiles   bf16
+//   2  register-staged streaming, ring of 6 K blocks     16-row tiles   bf16
+//   3  LDS-landed DMA streaming, 2 row blocks per item   32-row tiles   bf16
+//   4  prefill, 4 waves, 128 x 256 workgroup tile        128-row tiles  fp8 hi/lo
+//   5  prefill, 8 waves, 256 x 256 workgroup tile        256-row tiles  fp8 hi/lo
 bool launch_gemm1(int variant, const uint8_t* hidden, const float* hs_scale, int T,
                   const uint8_t* w1, const float* s1, const int4* tiles, const int* num_tiles,
                   int max_tiles, const int* sorted_tok, const Intermediate& C, hipStream_t stream) {
     uint16_t* inter = C.bf16();
-    // one resident workgroup per CU (the prefill kernel holds 144 KB of LDS)
-    const int prefill_grid = 256;
-    constexpr int G = kI / 16;
+    const int prefill_grid = 256;   // one resident workgroup per CU (LDS-bound)
+    constexpr int G = kI / 16;      // 16-column groups
     const long long mt = max_tiles;
-#define G1_STREAM(CB, KS, D)                                                                    \
-    hipLaunchKernelGGL((gemm1_stream_kernel<CB, KS, D>), dim3(grid_for(mt * G * KS / 4)),       \
-                       dim3(256), 0, stream, hidden, hs_scale, T, w1, s1, tiles, num_tiles,     \
-                       sorted_tok, inter)
-#define G1_DMA(CB, KS, NS)                                                                      \
-    hipLaunchKernelGGL((gemm1_dma_kernel<CB, KS, NS>), dim3(grid_for(mt * G * KS / 4)),        \
-                       dim3(256), 0, stream, hidden, hs_scale, T, w1, s1, tiles, num_tiles,     \
-                       sorted_tok, inter)
     switch (variant) {
-        case 0: G1_STREAM(1, 1, 4); return true;
-        case 1: G1_STREAM(1, 2, 4); return true;
-        case 2: G1_STREAM(1, 4, 4); return true;
-        case 3: G1_STREAM(2, 1, 3); return true;
-        case 4: G1_STREAM(2, 2, 3); return true;
-        case 5: G1_STREAM(2, 4, 3); return true;
-        case 6: G1_DMA(1, 1, 4); return true;
-        case 7: G1_DMA(1, 2, 4); return true;
-        case 8: G1_DMA(1, 4, 4); return true;
-        case 9: G1_DMA(2, 1, 3); return true;
-        case 10: G1_DMA(2, 2, 3); return true;
-        case 11: G1_DMA(2, 4, 3); return true;
-        case 12:
-            hipLaunchKernelGGL(gemm1_prefill_kernel<3>, dim3(prefill_grid), dim3(256), 0, stream,
-                               hidden, hs_scale, T, w1, s1, tiles, num_tiles, sorted_tok, C);
-            return true;
-        case 13:
-            hipLaunchKernelGGL(gemm1_prefill8_kernel, dim3(prefill_grid), dim3(512), 0, stream,
-                               hidden, hs_scale, T, w1, s1, tiles, num_tiles, sorted_tok, C);
-            return true;
-        case 15:   // register-staged streaming, ring of 4 K blocks
+        case 1:
             hipLaunchKernelGGL(gemm1_rstream_kernel<4>, dim3(grid_for(mt * G)), dim3(256), 0, stream,
                                hidden, hs_scale, T, w1, s1, tiles, num_tiles, sorted_tok, inter);
             return true;
-        case 16:   // register-staged streaming, ring of 6 K blocks
+        case 2:
             hipLaunchKernelGGL(gemm1_rstream_kernel<6>, dim3(grid_for(mt * G)), dim3(256), 0, stream,
                                hidden, hs_scale, T, w1, s1, tiles, num_tiles, sorted_tok, inter);
             return true;
-        case 14:   // persistent streaming, 16-row tiles, two workgroups per CU
-            hipLaunchKernelGGL(gemm1_pstream_kernel<4>, dim3(grid_for(mt * G) < 512 ? grid_for(mt * G) : 512),
-                               dim3(256), 0, stream, hidden, hs_scale, T, w1, s1, tiles, num_tiles,
-                               sorted_tok, inter);
+        case 3:
+            hipLaunchKernelGGL((gemm1_dma_kernel<2, 4, 3>), dim3(grid_for(mt * G)), dim3(256), 0,
+                               stream, hidden, hs_scale, T, w1, s1, tiles, num_tiles, sorted_tok, inter);
             return true;
-        case -1:
-            hipLaunchKernelGGL(gemm1_swiglu_kernel<4>, dim3(grid_for(mt * G)), dim3(256), 0, stream,
-                               hidden, hs_scale, T, w1, s1, tiles, num_tiles, sorted_tok, inter);
+        case 4:
+            hipLaunchKernelGGL(gemm1_prefill_kernel<3>, dim3(prefill_grid), dim3(256), 0, stream,
+                               hidden, hs_scale, T, w1, s1, tiles, num_tiles, sorted_tok, C);
+            return true;
+        case 5:
+            hipLaunchKernelGGL(gemm1_prefill8_kernel, dim3(prefill_grid), dim3(512), 0, stream,
+                               hidden, hs_scale, T, w1, s1, tiles, num_tiles, sorted_tok, C);
             return true;
         default: return false;
     }
-#undef G1_STREAM
-#undef G1_DMA
 }
 
 }  // namespace moe

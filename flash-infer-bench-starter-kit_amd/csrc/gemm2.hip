@@ -6,18 +6,17 @@
 // (the reference's CUTLASS path applies them in its mainloop,
 // moe_grouped_gemm_fp8.cu:274-322):
 //   O[r, h] = sum_kb sb2[e, h/128, kb] * sum_{i in kb} C[r, i] * W2[e, h, i]
-// C is the bf16 SwiGLU output of GEMM1; W2 e4m3 bytes are widened to bf16 in
-// registers (exact: every e4m3 value is a bf16 value).  Expert rows O stay fp32
-// for the combine: rounding them to bf16 first breaks the 1e-2 tolerance where two
-// large expert rows cancel.  The reference re-quantises
-// C to fp8 per (row, 128) (kernel.cu:1086-1145); keeping C in bf16 keeps GEMM2 within
-// atol = rtol = 1e-2 of the fp32 restatement.
-//
-// Work item = (row tile of <= 16*MAXCB rows of one expert, 16 output columns h).
-// The 4 waves split the 16 K blocks and reduce through LDS in a fixed order.
-// MFMA v_mfma_f32_16x16x32_bf16: operand A = 16 W2 rows, operand B = 16 C rows;
-// lane l supplies row l%16 and K elements 32*(l/16) + 8j..8j+7 of the block for MFMA
-// j = 0..3 on both operands, and receives D[h = 4*(l/16)+v][row = l%16].
+// Decode kernels: C is the bf16 SwiGLU output of GEMM1; W2 e4m3 bytes are widened to
+// bf16 in registers (exact: every e4m3 value is a bf16 value) for
+// v_mfma_f32_16x16x32_bf16, operand A = 16 W2 rows, operand B = 16 C rows; lane l
+// supplies row l%16 and K elements 32*(l/16) + 8j..8j+7 of the block for MFMA j = 0..3
+// on both operands, and receives D[h = 4*(l/16)+v][row = l%16].  A work item's K blocks
+// are split over waves and reduced through LDS in a fixed order.
+// Prefill kernel: FP8 MFMA on the hi/lo form of C (see gemm2_prefill8_kernel).
+// Expert rows O stay fp32 for the combine: rounding them to bf16 first breaks the
+// 1e-2 tolerance where two large expert rows cancel.  The reference re-quantises C to
+// one e4m3 per element (kernel.cu:1086-1145), which does not meet atol = rtol = 1e-2
+// against the fp32 restatement; both forms used here do.
 
 #include "moe_device.h"
 
@@ -39,233 +38,6 @@ __device__ __forceinline__ void e4m3x4_to_bf16x4(uint32_t w, uint32_t& d0, uint3
 __device__ __forceinline__ v8bf as_v8bf(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
     v4u t = {a, b, c, d};
     return __builtin_bit_cast(v8bf, t);
-}
-
-template <int MAXCB>
-__global__ __launch_bounds__(256) void gemm2_kernel(
-    const uint16_t* __restrict__ inter, const uint8_t* __restrict__ w2,
-    const float* __restrict__ s2, const int4* __restrict__ tiles,
-    const int* __restrict__ num_tiles, float* __restrict__ out_rows) {
-    constexpr int kGroups = kH / 16;      // 448
-    constexpr int kKbPerWave = kIB / 4;   // 4
-    __shared__ v4f red[4][MAXCB][64];
-
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int r16 = lane & 15, kq = lane >> 4;
-    const int nwork = (*num_tiles) * kGroups;
-
-    for (int work = blockIdx.x; work < nwork; work += gridDim.x) {
-        const int4 tile = tiles[work / kGroups];
-        const int hg = work % kGroups;
-        const int le = tile.x, row0 = tile.y, nrows = tile.z;
-        const int ncb = (nrows + 15) >> 4;
-
-        int crow[MAXCB];
-#pragma unroll
-        for (int cb = 0; cb < MAXCB; ++cb) crow[cb] = row0 + min(cb * 16 + r16, nrows - 1);
-
-        const uint8_t* wp = w2 + (size_t)(le * kH + hg * 16 + r16) * kI + kq * 32;
-        const float* sp = s2 + (size_t)(le * kHB + (hg >> 3)) * kIB;
-
-        v4f acc[MAXCB];
-#pragma unroll
-        for (int cb = 0; cb < MAXCB; ++cb) acc[cb] = v4f{0.f, 0.f, 0.f, 0.f};
-        const v4f zero = {0.f, 0.f, 0.f, 0.f};
-
-#pragma unroll
-        for (int kk = 0; kk < kKbPerWave; ++kk) {
-            const int kb = wave * kKbPerWave + kk;
-            const v4u* wq = reinterpret_cast<const v4u*>(wp + kb * kBlk);
-            const v4u wa = __builtin_nontemporal_load(wq);
-            const v4u wb = __builtin_nontemporal_load(wq + 1);
-            const uint32_t ww[8] = {wa[0], wa[1], wa[2], wa[3], wb[0], wb[1], wb[2], wb[3]};
-            v8bf bw[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                uint32_t d0, d1, d2, d3;
-                e4m3x4_to_bf16x4(ww[2 * j], d0, d1);
-                e4m3x4_to_bf16x4(ww[2 * j + 1], d2, d3);
-                bw[j] = as_v8bf(d0, d1, d2, d3);
-            }
-            const float sb = sp[kb];
-#pragma unroll
-            for (int cb = 0; cb < MAXCB; ++cb) {
-                if (cb < ncb) {
-                    const uint4* cp = reinterpret_cast<const uint4*>(
-                        inter + (size_t)crow[cb] * kI + kb * kBlk + kq * 32);
-                    v4f t = zero;
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const uint4 c4 = cp[j];
-                        t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bw[j], as_v8bf(c4.x, c4.y, c4.z, c4.w), t, 0, 0, 0);
-                    }
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) acc[cb][v] = __builtin_fmaf(t[v], sb, acc[cb][v]);
-                }
-            }
-        }
-
-#pragma unroll
-        for (int cb = 0; cb < MAXCB; ++cb)
-            if (cb < ncb) red[wave][cb][lane] = acc[cb];
-        __syncthreads();
-        for (int cb = wave; cb < ncb; cb += 4) {
-            v4f o = red[0][cb][lane];
-#pragma unroll
-            for (int w = 1; w < 4; ++w) o += red[w][cb][lane];
-            const int r = cb * 16 + r16;
-            if (r < nrows)
-                *reinterpret_cast<v4f*>(out_rows + (size_t)(row0 + r) * kH + hg * 16 + kq * 4) = o;
-        }
-        __syncthreads();
-    }
-}
-
-// Weight-streaming GEMM2 for small token counts (decode).  Same arithmetic as
-// gemm2_kernel; a work item is (row tile of <= 16*CB rows, HF groups of 16 output
-// columns), a workgroup runs 4/KSPLIT items side by side and KSPLIT waves split the
-// 16 K blocks.  Each wave keeps a ring of D K blocks of W2 bytes and C rows in
-// registers (non-temporal weight loads), refilled as soon as a stage is consumed;
-// the HF weight groups share every C-row load.
-template <int CB, int KSPLIT, int D, int HF>
-__global__ __launch_bounds__(256) void gemm2_stream_kernel(
-    const uint16_t* __restrict__ inter, const uint8_t* __restrict__ w2,
-    const float* __restrict__ s2, const int4* __restrict__ tiles,
-    const int* __restrict__ num_tiles, float* __restrict__ out_rows) {
-    constexpr int NGW = 4 / KSPLIT;
-    constexpr int KB = kIB / KSPLIT;
-    constexpr int kItems = (kH / 16) / (HF * NGW);
-    __shared__ v4f red[KSPLIT > 1 ? 4 : 1][HF][CB][64];
-
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int r16 = lane & 15, kq = lane >> 4;
-    const int ngl = wave / KSPLIT, ks = wave % KSPLIT;
-    const int nwork = (*num_tiles) * kItems;
-    const v4f zero = {0.f, 0.f, 0.f, 0.f};
-
-    for (int work = blockIdx.x; work < nwork; work += gridDim.x) {
-        const int4 tile = tiles[work / kItems];
-        const int hg0 = ((work % kItems) * NGW + ngl) * HF;
-        const int le = tile.x, row0 = tile.y, nrows = tile.z;
-        const int ncb = (nrows + 15) >> 4;
-
-        const uint16_t* cp[CB];
-#pragma unroll
-        for (int cb = 0; cb < CB; ++cb)
-            cp[cb] = inter + (size_t)(row0 + min(cb * 16 + r16, nrows - 1)) * kI + kq * 32;
-        const uint8_t* wp[HF];
-        const float* sp[HF];
-#pragma unroll
-        for (int hf = 0; hf < HF; ++hf) {
-            wp[hf] = w2 + (size_t)(le * kH + (hg0 + hf) * 16 + r16) * kI + kq * 32;
-            sp[hf] = s2 + (size_t)(le * kHB + ((hg0 + hf) >> 3)) * kIB;
-        }
-        const int kb0 = ks * KB;
-
-        v4u bw[D][HF][2];
-        v4u bc[D][CB][4];
-#pragma unroll
-        for (int d = 0; d < D; ++d) {
-            const int kb = kb0 + d;
-#pragma unroll
-            for (int hf = 0; hf < HF; ++hf) {
-                const v4u* q = reinterpret_cast<const v4u*>(wp[hf] + kb * kBlk);
-                bw[d][hf][0] = __builtin_nontemporal_load(q);
-                bw[d][hf][1] = __builtin_nontemporal_load(q + 1);
-            }
-#pragma unroll
-            for (int cb = 0; cb < CB; ++cb) {
-                const v4u* q = reinterpret_cast<const v4u*>(cp[cb] + kb * kBlk);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) bc[d][cb][j] = q[j];
-            }
-        }
-        v4f acc[HF][CB];
-#pragma unroll
-        for (int hf = 0; hf < HF; ++hf)
-#pragma unroll
-            for (int cb = 0; cb < CB; ++cb) acc[hf][cb] = zero;
-
-#pragma unroll
-        for (int k = 0; k < KB; ++k) {
-            const int d = k % D;
-            const int kb = kb0 + k;
-#pragma unroll
-            for (int hf = 0; hf < HF; ++hf) {
-                const uint32_t ww[8] = {bw[d][hf][0][0], bw[d][hf][0][1], bw[d][hf][0][2], bw[d][hf][0][3],
-                                        bw[d][hf][1][0], bw[d][hf][1][1], bw[d][hf][1][2], bw[d][hf][1][3]};
-                v8bf wb[4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    uint32_t d0, d1, d2, d3;
-                    e4m3x4_to_bf16x4(ww[2 * j], d0, d1);
-                    e4m3x4_to_bf16x4(ww[2 * j + 1], d2, d3);
-                    wb[j] = as_v8bf(d0, d1, d2, d3);
-                }
-                const float sb = sp[hf][kb];
-#pragma unroll
-                for (int cb = 0; cb < CB; ++cb) {
-                    if (cb < ncb) {
-                        v4f t = zero;
-#pragma unroll
-                        for (int j = 0; j < 4; ++j)
-                            t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wb[j], __builtin_bit_cast(v8bf, bc[d][cb][j]), t, 0, 0, 0);
-#pragma unroll
-                        for (int v = 0; v < 4; ++v) acc[hf][cb][v] = __builtin_fmaf(t[v], sb, acc[hf][cb][v]);
-                    }
-                }
-            }
-            if (k + D < KB) {
-                const int nkb = kb + D;
-#pragma unroll
-                for (int hf = 0; hf < HF; ++hf) {
-                    const v4u* q = reinterpret_cast<const v4u*>(wp[hf] + nkb * kBlk);
-                    bw[d][hf][0] = __builtin_nontemporal_load(q);
-                    bw[d][hf][1] = __builtin_nontemporal_load(q + 1);
-                }
-#pragma unroll
-                for (int cb = 0; cb < CB; ++cb) {
-                    const v4u* q = reinterpret_cast<const v4u*>(cp[cb] + nkb * kBlk);
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) bc[d][cb][j] = q[j];
-                }
-            }
-        }
-
-        if constexpr (KSPLIT == 1) {
-#pragma unroll
-            for (int hf = 0; hf < HF; ++hf)
-#pragma unroll
-                for (int cb = 0; cb < CB; ++cb) {
-                    const int r = cb * 16 + r16;
-                    if (cb < ncb && r < nrows)
-                        *reinterpret_cast<v4f*>(out_rows + (size_t)(row0 + r) * kH + (hg0 + hf) * 16 + kq * 4) = acc[hf][cb];
-                }
-        } else {
-#pragma unroll
-            for (int hf = 0; hf < HF; ++hf)
-#pragma unroll
-                for (int cb = 0; cb < CB; ++cb)
-                    if (cb < ncb) red[wave][hf][cb][lane] = acc[hf][cb];
-            __syncthreads();
-            if (ks == 0) {
-#pragma unroll
-                for (int hf = 0; hf < HF; ++hf)
-#pragma unroll
-                    for (int cb = 0; cb < CB; ++cb) {
-                        const int r = cb * 16 + r16;
-                        if (cb < ncb) {
-                            v4f o = red[wave][hf][cb][lane];
-#pragma unroll
-                            for (int q = 1; q < KSPLIT; ++q) o += red[wave + q][hf][cb][lane];
-                            if (r < nrows)
-                                *reinterpret_cast<v4f*>(out_rows + (size_t)(row0 + r) * kH + (hg0 + hf) * 16 + kq * 4) = o;
-                        }
-                    }
-            }
-            __syncthreads();
-        }
-    }
 }
 
 // LDS-landed weight streaming GEMM2 (decode).  A wave owns HF groups of 16 output
@@ -743,69 +515,48 @@ __global__ void e4m3_to_bf16_kernel(const uint32_t* __restrict__ in, uint2* __re
 
 static int grid_for2(long long work) { return (int)(work < 4096 ? work : 4096); }
 
-// variant: 0..5 register-ring streaming, 6..11 LDS-landed streaming, both with
-// (CB, KSPLIT, HF) = (1,1,2) (1,2,2) (1,4,1) (2,1,2) (2,2,2) (2,4,1) and bf16 C; 12 the
-// prefill kernel on 128-row tiles (13: the same kernel over the 128-row second tile
-// list of a 256-row dispatch), reading C in the fp8 hi/lo form; -1 the 64-row tile
-// kernel (bf16 C)
+// Variants (the tile height of the dispatch they expect, and the form of C they read):
+//   1  register-staged streaming, K split 4, 16 output columns per wave   16-row   bf16
+//   2  register-staged streaming, K split 4, 32 output columns per wave   16-row   bf16
+//   3  register-staged streaming, K split 2, 32 output columns per wave   16-row   bf16
+//   4  register-staged streaming, K split 4, 64 output columns per wave   16-row   bf16
+//   5  LDS-landed DMA streaming, 2 row blocks x 32 columns per item        32-row   bf16
+//   6  prefill, 8 waves, 128 x 256 workgroup tile                          128-row  hi/lo
+//   7  the same kernel over the 128-row second tile list of a 256-row dispatch      hi/lo
 bool launch_gemm2(int variant, const Intermediate& C, const uint8_t* w2, const float* s2,
                   const int4* tiles, const int* num_tiles, int max_tiles, float* out_rows,
                   hipStream_t stream) {
     const uint16_t* inter = C.bf16();
     const long long mt = max_tiles;
-#define G2_STREAM(CB, KS, D, HF)                                                                  \
-    hipLaunchKernelGGL((gemm2_stream_kernel<CB, KS, D, HF>),                                      \
-                       dim3(grid_for2(mt * (kH / 16) / (HF * (4 / KS)))), dim3(256), 0, stream,   \
-                       inter, w2, s2, tiles, num_tiles, out_rows)
-#define G2_DMA(CB, KS, NS, HF)                                                                    \
-    hipLaunchKernelGGL((gemm2_dma_kernel<CB, KS, NS, HF>),                                        \
-                       dim3(grid_for2(mt * (kH / 16) / (HF * (4 / KS)))), dim3(256), 0, stream,   \
-                       inter, w2, s2, tiles, num_tiles, out_rows)
+    constexpr int G = kH / 16;      // 16-column groups
     switch (variant) {
-        case 0: G2_STREAM(1, 1, 4, 2); return true;
-        case 1: G2_STREAM(1, 2, 4, 2); return true;
-        case 2: G2_STREAM(1, 4, 4, 1); return true;
-        case 3: G2_STREAM(2, 1, 3, 2); return true;
-        case 4: G2_STREAM(2, 2, 3, 2); return true;
-        case 5: G2_STREAM(2, 4, 4, 1); return true;
-        case 6: G2_DMA(1, 1, 4, 2); return true;
-        case 7: G2_DMA(1, 2, 4, 2); return true;
-        case 8: G2_DMA(1, 4, 4, 1); return true;
-        case 9: G2_DMA(2, 1, 3, 2); return true;
-        case 10: G2_DMA(2, 2, 3, 2); return true;
-        case 11: G2_DMA(2, 4, 3, 1); return true;
-        case 12:
-            hipLaunchKernelGGL(gemm2_prefill8_kernel, dim3(256), dim3(512), 0, stream, C, w2,
-                               s2, tiles, num_tiles, out_rows);
-            return true;
-        case 13:  // the 128-row second tile list of a 256-row dispatch
-            hipLaunchKernelGGL(gemm2_prefill8_kernel, dim3(256), dim3(512), 0, stream, C, w2,
-                               s2, tiles, num_tiles, out_rows);
-            return true;
-        case 15:   // register-staged streaming, K split 4 ways
-            hipLaunchKernelGGL((gemm2_rstream_kernel<4, 4, 1>), dim3(grid_for2(mt * (kH / 16))), dim3(256), 0,
+        case 1:
+            hipLaunchKernelGGL((gemm2_rstream_kernel<4, 4, 1>), dim3(grid_for2(mt * G)), dim3(256), 0,
                                stream, inter, w2, s2, tiles, num_tiles, out_rows);
             return true;
-        case 16:   // register-staged streaming, K split 4 ways, 32 output columns per wave
-            hipLaunchKernelGGL((gemm2_rstream_kernel<4, 4, 2>), dim3(grid_for2(mt * (kH / 32))), dim3(256), 0,
+        case 2:
+            hipLaunchKernelGGL((gemm2_rstream_kernel<4, 4, 2>), dim3(grid_for2(mt * G / 2)), dim3(256), 0,
                                stream, inter, w2, s2, tiles, num_tiles, out_rows);
             return true;
-        case 17:   // register-staged streaming, K split 2 ways, 32 output columns per wave
-            hipLaunchKernelGGL((gemm2_rstream_kernel<4, 2, 2>), dim3(grid_for2(mt * (kH / 32) / 2)), dim3(256), 0,
+        case 3:
+            hipLaunchKernelGGL((gemm2_rstream_kernel<4, 2, 2>), dim3(grid_for2(mt * G / 4)), dim3(256), 0,
                                stream, inter, w2, s2, tiles, num_tiles, out_rows);
             return true;
-        case 18:   // register-staged streaming, K split 4 ways, 64 output columns per wave
-            hipLaunchKernelGGL((gemm2_rstream_kernel<3, 4, 4>), dim3(grid_for2(mt * (kH / 64))), dim3(256), 0,
+        case 4:
+            hipLaunchKernelGGL((gemm2_rstream_kernel<3, 4, 4>), dim3(grid_for2(mt * G / 4)), dim3(256), 0,
                                stream, inter, w2, s2, tiles, num_tiles, out_rows);
             return true;
-        case -1:
-            hipLaunchKernelGGL(gemm2_kernel<4>, dim3(grid_for2(mt * (kH / 16))), dim3(256), 0, stream,
-                               inter, w2, s2, tiles, num_tiles, out_rows);
+        case 5:
+            hipLaunchKernelGGL((gemm2_dma_kernel<2, 2, 3, 2>), dim3(grid_for2(mt * G / 4)), dim3(256), 0,
+                               stream, inter, w2, s2, tiles, num_tiles, out_rows);
+            return true;
+        case 6:
+        case 7:
+            hipLaunchKernelGGL(gemm2_prefill8_kernel, dim3(256), dim3(512), 0, stream, C, w2, s2, tiles,
+                               num_tiles, out_rows);
             return true;
         default: return false;
     }
-#undef G2_STREAM
-#undef G2_DMA
 }
 
 void launch_e4m3_to_bf16(const uint8_t* in, uint16_t* out, int n, hipStream_t stream) {
