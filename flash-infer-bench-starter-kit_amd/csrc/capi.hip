@@ -26,9 +26,10 @@ bool launch_dispatch(const int*, const float*, int, int, int, int*, int*, int4*,
                      int*, int*, hipStream_t, int*, int4*);
 int dispatch_max_tiles(int T, int tm);
 bool launch_gemm1(int, const uint8_t*, const float*, int, const uint8_t*, const float*,
-                  const int4*, const int*, int, const int*, const Intermediate&, hipStream_t);
+                  const int4*, const int*, const int*, int, const int*, const Intermediate&,
+                  hipStream_t);
 bool launch_gemm2(int, const Intermediate&, const uint8_t*, const float*, const int4*, const int*,
-                  int, float*, hipStream_t);
+                  const int*, int, float*, hipStream_t);
 void launch_combine(const float*, const float*, const int*, int, uint16_t*, hipStream_t);
 void launch_e4m3_to_bf16(const uint8_t*, uint16_t*, int, hipStream_t);
 }  // namespace moe
@@ -254,14 +255,14 @@ int moe_mi355_forward(const moe_mi355_args* a, void* stream) {
                          half ? tiles2 : nullptr);
     if (prof) prof_record(slot, 2, s);
     moe::launch_gemm1(plan.g1, a->hidden_states, a->hidden_states_scale, T, a->gemm1_weights,
-                      a->gemm1_weights_scale, tiles, num_tiles, max_tiles, stok, inter, s);
+                      a->gemm1_weights_scale, tiles, num_tiles, meta, max_tiles, stok, inter, s);
     if (prof) prof_record(slot, 3, s);
     if (half)
         moe::launch_gemm2(plan.g2, inter, a->gemm2_weights, a->gemm2_weights_scale, tiles2,
-                          num_tiles2, moe::dispatch_max_tiles(T, plan.tm / 2), rows, s);
+                          num_tiles2, meta, moe::dispatch_max_tiles(T, plan.tm / 2), rows, s);
     else
         moe::launch_gemm2(plan.g2, inter, a->gemm2_weights, a->gemm2_weights_scale, tiles,
-                          num_tiles, max_tiles, rows, s);
+                          num_tiles, meta, max_tiles, rows, s);
     if (prof) prof_record(slot, 4, s);
     moe::launch_combine(rows, sw, inv, T, a->output, s);
     if (prof) prof_record(slot, 5, s);

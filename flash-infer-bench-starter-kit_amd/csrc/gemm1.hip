@@ -443,18 +443,18 @@ __device__ __forceinline__ void store_c_hilo(const v4f (&acc)[4][8], float* xch,
 // one global_load_lds_dword), into NS stages of 49 KB; rows keep 16-byte chunk c
 // at c ^ swz128(r) so ds_read_b128 in the MFMA layout is conflict-free.  One workgroup barrier per K block both publishes
 // the stage every wave waited for and frees the stage about to be refilled.
-// Work items (row tile, 128-column group) are grouped 4 row tiles x all column
-// groups (column-major inside a group) and each XCD takes a contiguous run of 32
-// items of a round: 4 row tiles x 8 column groups share one L2, so each token row
-// block is fetched about twice instead of 16 times and each weight block once per
-// 4 row tiles.
+// Work items (row tile, 128-column group) are grouped up to 4 row tiles of one
+// expert x all column groups (column-major inside a group, see grouped_item) and
+// each XCD takes a contiguous run of 32 items of a round: up to 4 row tiles x 8
+// column groups share one L2, so each token row block is fetched about twice
+// instead of 16 times and each weight block once per group.
 // ---------------------------------------------------------------------------
 template <int NS>
 __global__ __launch_bounds__(256) void gemm1_prefill_kernel(
     const uint8_t* __restrict__ hidden, const float* __restrict__ hs_scale, int T,
     const uint8_t* __restrict__ w1, const float* __restrict__ s1,
     const int4* __restrict__ tiles, const int* __restrict__ num_tiles,
-    const int* __restrict__ sorted_tok, Intermediate C) {
+    const int* __restrict__ exp_off, const int* __restrict__ sorted_tok, Intermediate C) {
     constexpr int BM = 128;                     // token rows per tile
     constexpr int NG = kI / 128;                // 16 column groups
     constexpr int kA = BM * kBlk;               // 16 KB token stage
@@ -484,7 +484,7 @@ __global__ __launch_bounds__(256) void gemm1_prefill_kernel(
         const int item = round * G + xcd * per + slot;
         if (item >= nitems) continue;            // uniform per workgroup
         int tix, ng;
-        grouped_item(item, *num_tiles, NG, tix, ng);
+        grouped_item<BM>(item, NG, tiles, exp_off, tix, ng);
         const int4 tile = tiles[tix];
         const int le = tile.x, row0 = tile.y, nrows = tile.z;
 
@@ -608,7 +608,7 @@ __global__ __launch_bounds__(512, 1) void gemm1_prefill8_kernel(
     const uint8_t* __restrict__ hidden, const float* __restrict__ hs_scale, int T,
     const uint8_t* __restrict__ w1, const float* __restrict__ s1,
     const int4* __restrict__ tiles, const int* __restrict__ num_tiles,
-    const int* __restrict__ sorted_tok, Intermediate C) {
+    const int* __restrict__ exp_off, const int* __restrict__ sorted_tok, Intermediate C) {
     constexpr int NS = 2;
     constexpr int BM = 256;
     constexpr int NG = kI / 128;
@@ -637,7 +637,7 @@ __global__ __launch_bounds__(512, 1) void gemm1_prefill8_kernel(
         const int item = round * G + xcd * per + slot;
         if (item >= nitems) continue;
         int tix, ng;
-        grouped_item(item, ntl, NG, tix, ng);
+        grouped_item<BM>(item, NG, tiles, exp_off, tix, ng);
         const int4 tile = tiles[tix];
         const int le = tile.x, row0 = tile.y, nrows = tile.z;
         const __amdgpu_buffer_rsrc_t rs_w = buffer_rsrc(w1 + (size_t)le * kN1 * kH, (uint32_t)kN1 * kH);
@@ -747,7 +747,8 @@ static int grid_for(long long work) { return (int)(work < 4096 ? work : 4096); }
 //   5  prefill, 8 waves, 256 x 256 workgroup tile        256-row tiles  fp8 hi/lo
 bool launch_gemm1(int variant, const uint8_t* hidden, const float* hs_scale, int T,
                   const uint8_t* w1, const float* s1, const int4* tiles, const int* num_tiles,
-                  int max_tiles, const int* sorted_tok, const Intermediate& C, hipStream_t stream) {
+                  const int* exp_off, int max_tiles, const int* sorted_tok, const Intermediate& C,
+                  hipStream_t stream) {
     uint16_t* inter = C.bf16();
     const int prefill_grid = 256;   // one resident workgroup per CU (LDS-bound)
     constexpr int G = kI / 16;      // 16-column groups
@@ -767,11 +768,11 @@ bool launch_gemm1(int variant, const uint8_t* hidden, const float* hs_scale, int
             return true;
         case 4:
             hipLaunchKernelGGL(gemm1_prefill_kernel<3>, dim3(prefill_grid), dim3(256), 0, stream,
-                               hidden, hs_scale, T, w1, s1, tiles, num_tiles, sorted_tok, C);
+                               hidden, hs_scale, T, w1, s1, tiles, num_tiles, exp_off, sorted_tok, C);
             return true;
         case 5:
             hipLaunchKernelGGL(gemm1_prefill8_kernel, dim3(prefill_grid), dim3(512), 0, stream,
-                               hidden, hs_scale, T, w1, s1, tiles, num_tiles, sorted_tok, C);
+                               hidden, hs_scale, T, w1, s1, tiles, num_tiles, exp_off, sorted_tok, C);
             return true;
         default: return false;
     }

@@ -353,13 +353,14 @@ __global__ __launch_bounds__(256) void gemm2_rstream_kernel(
 // Stage (two, 64.5 KB each): C hi rows 16 KB | C lo rows 16 KB | W2 rows 32 KB |
 // C row scales 512 B, all by buffer_load ... lds in two bursts per K block (C after
 // the barrier, W2 after the second column block's MFMAs); rows keep 16-byte chunk c
-// at c ^ swz128(r).  Items (128-row piece, 256-column group) are grouped 4 pieces x
-// all column groups with an XCD-contiguous mapping, as in the prefill GEMM1.
+// at c ^ swz128(r).  Items (128-row piece, 256-column group) are grouped up to 4
+// pieces of one expert x all column groups with an XCD-contiguous mapping, as in
+// the prefill GEMM1.
 // Tiles hold at most 128 rows.
 __global__ __launch_bounds__(512, 1) void gemm2_prefill8_kernel(
     Intermediate C, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
     const int4* __restrict__ tiles, const int* __restrict__ num_tiles,
-    float* __restrict__ out_rows) {
+    const int* __restrict__ exp_off, float* __restrict__ out_rows) {
     constexpr int NS = 2;
     constexpr int BM = 128;
     constexpr int NG = kH / 256;                // 28 column groups
@@ -386,7 +387,7 @@ __global__ __launch_bounds__(512, 1) void gemm2_prefill8_kernel(
         const int item = round * G + xcd * per + slot;
         if (item >= nitems) continue;            // uniform per workgroup
         int vix, hg;
-        grouped_item(item, nvt, NG, vix, hg);
+        grouped_item<BM>(item, NG, tiles, exp_off, vix, hg);
         const int4 tile = tiles[vix];
         const int le = tile.x, row0 = tile.y, nrows = tile.z;
 
@@ -524,8 +525,8 @@ static int grid_for2(long long work) { return (int)(work < 4096 ? work : 4096); 
 //   6  prefill, 8 waves, 128 x 256 workgroup tile                          128-row  hi/lo
 //   7  the same kernel over the 128-row second tile list of a 256-row dispatch      hi/lo
 bool launch_gemm2(int variant, const Intermediate& C, const uint8_t* w2, const float* s2,
-                  const int4* tiles, const int* num_tiles, int max_tiles, float* out_rows,
-                  hipStream_t stream) {
+                  const int4* tiles, const int* num_tiles, const int* exp_off, int max_tiles,
+                  float* out_rows, hipStream_t stream) {
     const uint16_t* inter = C.bf16();
     const long long mt = max_tiles;
     constexpr int G = kH / 16;      // 16-column groups
@@ -553,7 +554,7 @@ bool launch_gemm2(int variant, const Intermediate& C, const uint8_t* w2, const f
         case 6:
         case 7:
             hipLaunchKernelGGL(gemm2_prefill8_kernel, dim3(256), dim3(512), 0, stream, C, w2, s2, tiles,
-                               num_tiles, out_rows);
+                               num_tiles, exp_off, out_rows);
             return true;
         default: return false;
     }
