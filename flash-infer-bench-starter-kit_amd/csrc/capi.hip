@@ -43,32 +43,35 @@ constexpr int kMinTileM = 16;           // smallest row tile; sizes the tile lis
 
 // Kernel plan per token count: the dispatch tile height and the GEMM1 / GEMM2 variants
 // (ids of launch_gemm1 / launch_gemm2).  Small T streams weights with the
-// register-staged kernels (T <= 96, 16-row tiles) or the LDS-landed DMA kernels
-// (32-row tiles), C in bf16; large T uses the MFMA-bound prefill kernels (128- or
-// 256-row tiles, C in the fp8 hi/lo form; with 256-row tiles GEMM2 walks the 128-row
-// second tile list).  MOE_MI355_G1 / MOE_MI355_G2 override the variants for tuning
-// sweeps; the override is ignored unless both imply the same tile height and the same
-// form of C.
+// register-staged kernels, C in bf16: 16-row tiles up to T = 192 (GEMM2 with 32 output
+// columns per wave up to T = 96, 64 beyond), 32-row tiles up to T = 896, where an
+// expert gets up to about 28 rows and streams its weights about once.  Large T uses
+// the MFMA-bound prefill kernels (128- or 256-row tiles, C in the fp8 hi/lo form; with
+// 256-row tiles GEMM2 walks the 128-row second tile list).  The boundaries come from
+// sweeps of every pair at T = 96 .. 1536 on MI355X.  MOE_MI355_G1 / MOE_MI355_G2
+// override the variants for tuning sweeps; the override is ignored unless both imply
+// the same tile height and the same form of C.
 struct Plan {
     int tm, g1, g2;
 };
 
-int g1_tile_m(int v) { return v <= 2 ? 16 : v == 3 ? 32 : v == 4 ? 128 : 256; }
-int g2_tile_m(int v) { return v <= 4 ? 16 : v == 5 ? 32 : v == 6 ? 128 : 256; }
-bool g1_hilo(int v) { return v >= 4; }
-bool g2_hilo(int v) { return v >= 6; }
+int g1_tile_m(int v) { return v == 1 ? 16 : v == 2 ? 32 : v == 3 ? 128 : 256; }
+int g2_tile_m(int v) { return v <= 2 ? 16 : v == 3 ? 32 : v == 4 ? 128 : 256; }
+bool g1_hilo(int v) { return v >= 3; }
+bool g2_hilo(int v) { return v >= 4; }
 
 Plan choose_plan(int32_t T) {
     Plan p;
-    if (T <= 96) p = {16, 1, 2};
-    else if (T <= 256) p = {32, 3, 5};
-    else if (T <= 2048) p = {128, 4, 6};
-    else p = {256, 5, 7};
+    if (T <= 96) p = {16, 1, 1};
+    else if (T <= 192) p = {16, 1, 2};
+    else if (T <= 896) p = {32, 2, 3};
+    else if (T <= 2048) p = {128, 3, 4};
+    else p = {256, 4, 5};
     const char* e1 = getenv("MOE_MI355_G1");
     const char* e2 = getenv("MOE_MI355_G2");
     const int env_g1 = e1 ? atoi(e1) : 0;
     const int env_g2 = e2 ? atoi(e2) : 0;
-    if (env_g1 >= 1 && env_g1 <= 5 && env_g2 >= 1 && env_g2 <= 7 &&
+    if (env_g1 >= 1 && env_g1 <= 4 && env_g2 >= 1 && env_g2 <= 5 &&
         g1_tile_m(env_g1) == g2_tile_m(env_g2) && g1_hilo(env_g1) == g2_hilo(env_g2))
         p = {g1_tile_m(env_g1), env_g1, env_g2};
     return p;
@@ -246,8 +249,8 @@ int moe_mi355_forward(const moe_mi355_args* a, void* stream) {
     if (prof) prof_record(slot, 1, s);
     const Plan plan = choose_plan(T);
     const int max_tiles = moe::dispatch_max_tiles(T, plan.tm);
-    // GEMM2 variant 7 walks the half-height (128-row) tiles of a 256-row dispatch
-    const bool half = plan.g2 == 7;
+    // GEMM2 variant 5 walks the half-height (128-row) tiles of a 256-row dispatch
+    const bool half = plan.g2 == 5;
     int4* tiles2 = tiles + max_tiles;
     int* num_tiles2 = meta + moe::kEL + 2;
     moe::launch_dispatch(ids, wts, T, clamp_offset(a->local_expert_offset), plan.tm, meta,

@@ -8,9 +8,9 @@
 // C is written as one row per routed assignment for GEMM2: bf16 by the decode
 // kernels, the fp8 hi/lo form (moe_device.h, Intermediate) by the prefill kernels.
 //
-// Kernels: register-staged and LDS-landed weight streaming for small T (a work item is
-// one row tile x 16 gate + 16 up rows, its 56 K blocks split over the 4 waves of a
-// workgroup and reduced through LDS in a fixed order, so results do not depend on
+// Kernels: register-staged weight streaming for small T (a work item is one row tile
+// of 16 or 32 rows x 16 gate + 16 up rows, its 56 K blocks split over the 4 waves of
+// a workgroup and reduced through LDS in a fixed order, so results do not depend on
 // scheduling), and MFMA-bound prefill kernels for large T (128- or 256-row tiles).
 //
 // MFMA: v_mfma_f32_16x16x128_f8f6f4 (e4m3 x e4m3), one instruction per 128-wide K
@@ -52,194 +52,21 @@ __device__ __forceinline__ void store_swiglu4(uint16_t* __restrict__ inter, int 
 }
 
 // ---------------------------------------------------------------------------
-// LDS-landed weight streaming (decode).  A wave owns a work item of 16 gate rows +
-// 16 up rows of one expert for one row tile, over KB consecutive K blocks.  Weight
-// bytes travel HBM -> LDS with global_load_lds_dwordx4, each instruction reading 8
-// rows x 128 B (full cache lines: a K block of 8 rows), into a per-wave ring of NS
-// K-block slots (4 KB each); the MFMA operands are then read with ds_read_b128 in
-// the MFMA register layout.  Inside a slot row r keeps its 16-byte chunk c at
-// position c ^ swz128(r), which keeps the ds_read_b128 operand reads free of bank
-// conflicts.  Token rows and scales come through L1/L2 into a
-// register ring of the same depth.
-//
-// The compiler does not order LDS DMA against later LDS reads, so every K block
-// issues a fixed number of vector-memory operations (4 DMA + 3 per token block),
-// fenced by sched_barrier, and the wave waits with an explicit vmcnt that leaves
-// exactly the younger K blocks in flight.
+// Register-staged weight streaming (decode and small prefill).  A work item is one row
+// tile x one group of 16 SwiGLU columns (16 gate + 16 up weight rows); the 4 waves of
+// a workgroup take 14 of its 56 K blocks each and reduce through LDS in a fixed order.
+// Weight bytes come into registers with full-line loads (global_load_dwordx4, lane l
+// reads row 8i + l/8, 16-byte chunk l%8 of the K block: 8 rows x 128 B per
+// instruction) through a ring of D K blocks held in VGPRs, and each K block is turned
+// into the MFMA layout through a 4 KB per-wave LDS slot (ds_write_b128 at the
+// swizzled position, then ds_read_b128 by the MFMA lanes).  Keeping the in-flight
+// bytes in VGPRs instead of an LDS ring lets more waves run per CU, so more bytes are
+// in flight per CU (a streaming probe of this access pattern: 7.1 TB/s against
+// 6.3 TB/s for LDS-landed DMA).
+// A tile holds CB blocks of 16 token rows: every weight fragment feeds 2 CB MFMAs, so
+// an expert with up to 16 CB routed rows streams its weights once.
 // ---------------------------------------------------------------------------
-
-template <int CB, int KSPLIT, int NS>
-__global__ __launch_bounds__(256) void gemm1_dma_kernel(
-    const uint8_t* __restrict__ hidden, const float* __restrict__ hs_scale, int T,
-    const uint8_t* __restrict__ w1, const float* __restrict__ s1,
-    const int4* __restrict__ tiles, const int* __restrict__ num_tiles,
-    const int* __restrict__ sorted_tok, uint16_t* __restrict__ inter) {
-    constexpr int NGW = 4 / KSPLIT;
-    constexpr int KB = kHB / KSPLIT;
-    constexpr int kItems = (kI / 16) / NGW;
-    constexpr int kSlot = 32 * kBlk;                  // 32 rows x 128 B
-    constexpr int kVmPerKb = 4 + 3 * CB;              // vector-memory ops per K block
-    static_assert(NS >= 2 && (NS - 1) * kVmPerKb < 64, "ring too deep for vmcnt");
-    __shared__ __attribute__((aligned(1024))) uint8_t ring[4][NS][kSlot];
-    __shared__ v4f red[KSPLIT > 1 ? 4 : 1][2][CB][64];
-
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    const int r16 = lane & 15, kq = lane >> 4;
-    const int ngl = wave / KSPLIT, ks = wave % KSPLIT;
-    const int nwork = (*num_tiles) * kItems;
-    const v4f zero = {0.f, 0.f, 0.f, 0.f};
-    uint8_t* myring = &ring[wave][0][0];
-
-    // DMA source: instruction i covers rows 8i..8i+7 of the item (0-15 gate, 16-31 up)
-    const int drow = lane >> 3;                         // row within the instruction
-    const int dchunk = (lane & 7);                      // LDS position of this lane's chunk
-    // MFMA read offsets inside a slot (gate row r16 and up row 16 + r16, halves h = 0, 1)
-    const int swz = swz128(r16);
-    const int rd_g0 = r16 * kBlk + (((2 * kq) ^ swz) << 4);
-    const int rd_g1 = r16 * kBlk + (((2 * kq + 1) ^ swz) << 4);
-    const int rd_u0 = rd_g0 + 16 * kBlk;
-    const int rd_u1 = rd_g1 + 16 * kBlk;
-
-    for (int work = blockIdx.x; work < nwork; work += gridDim.x) {
-        const int4 tile = tiles[work / kItems];
-        const int ng = (work % kItems) * NGW + ngl;
-        const int le = tile.x, row0 = tile.y, nrows = tile.z;
-        const int ncb = (nrows + 15) >> 4;
-
-        const uint8_t* ap[CB];
-        const float* sp[CB];
-#pragma unroll
-        for (int cb = 0; cb < CB; ++cb) {
-            const int tok = sorted_tok[row0 + min(cb * 16 + r16, nrows - 1)];
-            ap[cb] = hidden + (size_t)tok * kH + kq * 32;
-            sp[cb] = hs_scale + tok;
-        }
-        const uint8_t* dsrc[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = 8 * i + drow;                           // 0..31
-            const int n = (r < 16) ? ng * 16 + r : kI + ng * 16 + (r - 16);
-            const int c = dchunk ^ swz128(r);                // global chunk for this slot position
-            dsrc[i] = w1 + (size_t)(le * kN1 + n) * kH + c * 16;
-        }
-        const float* sg = s1 + (size_t)(le * kN1B + (ng >> 3)) * kHB;
-        const float* su = sg + (size_t)kIB * kHB;
-        const int kb0 = ks * KB;
-
-        v8i ba[NS][CB];
-        float bs[NS][CB];
-        auto issue = [&](int k) {
-            const int kb = kb0 + k;
-            uint8_t* slot = myring + (k % NS) * kSlot;
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                dma16(dsrc[i] + kb * kBlk, slot + i * 1024);
-#pragma unroll
-            for (int cb = 0; cb < CB; ++cb) {
-                ba[k % NS][cb] = load_v8i(ap[cb] + kb * kBlk);
-                bs[k % NS][cb] = sp[cb][(size_t)kb * T];
-            }
-        };
-
-#pragma unroll
-        for (int k = 0; k < NS - 1 && k < KB; ++k) {
-            issue(k);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        v4f ag[CB], au[CB];
-#pragma unroll
-        for (int cb = 0; cb < CB; ++cb) { ag[cb] = zero; au[cb] = zero; }
-
-#pragma unroll
-        for (int k = 0; k < KB; ++k) {
-            if (k + NS - 1 < KB) issue(k + NS - 1);
-            __builtin_amdgcn_sched_barrier(0);
-            // K blocks issued after k: min(NS - 1, KB - 1 - k)
-            constexpr int dummy = 0; (void)dummy;
-            const int younger = (KB - 1 - k) < (NS - 1) ? (KB - 1 - k) : (NS - 1);
-            switch (younger) {   // resolved at compile time after unrolling
-                case 0: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
-                case 1: __builtin_amdgcn_s_waitcnt(vmcnt_imm(1 * kVmPerKb)); break;
-                case 2: __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kVmPerKb)); break;
-                case 3: __builtin_amdgcn_s_waitcnt(vmcnt_imm(3 * kVmPerKb)); break;
-                case 4: __builtin_amdgcn_s_waitcnt(vmcnt_imm(4 * kVmPerKb)); break;
-                case 5: __builtin_amdgcn_s_waitcnt(vmcnt_imm(5 * kVmPerKb)); break;
-                case 6: __builtin_amdgcn_s_waitcnt(vmcnt_imm(6 * kVmPerKb)); break;
-                default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            const uint8_t* slot = myring + (k % NS) * kSlot;
-            const v4u g0 = *reinterpret_cast<const v4u*>(slot + rd_g0);
-            const v4u g1 = *reinterpret_cast<const v4u*>(slot + rd_g1);
-            const v4u u0 = *reinterpret_cast<const v4u*>(slot + rd_u0);
-            const v4u u1 = *reinterpret_cast<const v4u*>(slot + rd_u1);
-            const v8i bg = {(int)g0[0], (int)g0[1], (int)g0[2], (int)g0[3], (int)g1[0], (int)g1[1], (int)g1[2], (int)g1[3]};
-            const v8i bu = {(int)u0[0], (int)u0[1], (int)u0[2], (int)u0[3], (int)u1[0], (int)u1[1], (int)u1[2], (int)u1[3]};
-            const int kb = kb0 + k;
-            const float fsg = sg[kb], fsu = su[kb];
-#pragma unroll
-            for (int cb = 0; cb < CB; ++cb) {
-                if (cb < ncb) {
-                    const v4f tg = mfma_fp8(bg, ba[k % NS][cb], zero);
-                    const v4f tu = mfma_fp8(bu, ba[k % NS][cb], zero);
-                    const float fg = bs[k % NS][cb] * fsg, fu = bs[k % NS][cb] * fsu;
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        ag[cb][v] = __builtin_fmaf(tg[v], fg, ag[cb][v]);
-                        au[cb][v] = __builtin_fmaf(tu[v], fu, au[cb][v]);
-                    }
-                }
-            }
-            __builtin_amdgcn_sched_barrier(0);
-        }
-
-        if constexpr (KSPLIT == 1) {
-#pragma unroll
-            for (int cb = 0; cb < CB; ++cb) {
-                const int r = cb * 16 + r16;
-                if (cb < ncb && r < nrows) store_swiglu4(inter, row0 + r, ng * 16 + kq * 4, ag[cb], au[cb]);
-            }
-        } else {
-#pragma unroll
-            for (int cb = 0; cb < CB; ++cb) {
-                if (cb < ncb) {
-                    red[wave][0][cb][lane] = ag[cb];
-                    red[wave][1][cb][lane] = au[cb];
-                }
-            }
-            __syncthreads();
-            if (ks == 0) {
-#pragma unroll
-                for (int cb = 0; cb < CB; ++cb) {
-                    const int r = cb * 16 + r16;
-                    if (cb < ncb) {
-                        v4f g = red[wave][0][cb][lane], u = red[wave][1][cb][lane];
-#pragma unroll
-                        for (int q = 1; q < KSPLIT; ++q) {
-                            g += red[wave + q][0][cb][lane];
-                            u += red[wave + q][1][cb][lane];
-                        }
-                        if (r < nrows) store_swiglu4(inter, row0 + r, ng * 16 + kq * 4, g, u);
-                    }
-                }
-            }
-            __syncthreads();
-        }
-    }
-}
-
-// Register-staged weight streaming (decode): the same work split as
-// gemm1_dma_kernel<1, 4, NS>, but weight bytes come into registers with full-line
-// loads (global_load_dwordx4, lane l reads row 8i + l/8, 16-byte chunk l%8 of the K
-// block: 8 rows x 128 B per instruction) through a ring of D K blocks held in VGPRs,
-// and each K block is turned into the MFMA layout through a 4 KB per-wave LDS slot
-// (ds_write_b128 at the swizzled position, then ds_read_b128 by the MFMA lanes).
-// Keeping the in-flight bytes in VGPRs instead of LDS lets more waves run per CU, so
-// more bytes are in flight per CU than with LDS-landed DMA (a streaming probe of this
-// access pattern: 7.1 TB/s against 6.3 TB/s for the LDS ring).
-// ---------------------------------------------------------------------------
-template <int D>
+template <int D, int CB>
 __global__ __launch_bounds__(256) void gemm1_rstream_kernel(
     const uint8_t* __restrict__ hidden, const float* __restrict__ hs_scale, int T,
     const uint8_t* __restrict__ w1, const float* __restrict__ s1,
@@ -248,10 +75,10 @@ __global__ __launch_bounds__(256) void gemm1_rstream_kernel(
     constexpr int KSPLIT = 4;
     constexpr int KB = kHB / KSPLIT;                  // 14 K blocks per wave
     constexpr int kItems = kI / 16;
-    constexpr int kVmPerKb = 4 + 3;                   // 4 weight loads, 2 token loads, 1 scale
+    constexpr int kVmPerKb = 4 + 3 * CB;              // 4 weight loads, per row block 2 token loads + 1 scale
     static_assert(D >= 2 && D <= 8 && (D - 1) * kVmPerKb < 64, "ring depth");
     __shared__ __attribute__((aligned(1024))) uint8_t slot_lds[4][32 * kBlk];
-    __shared__ v4f red[4][2][64];
+    __shared__ v4f red[4][2][CB][64];
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -278,9 +105,14 @@ __global__ __launch_bounds__(256) void gemm1_rstream_kernel(
         const int4 tile = tiles[work / kItems];
         const int ng = work % kItems;
         const int le = tile.x, row0 = tile.y, nrows = tile.z;
-        const int tok = sorted_tok[row0 + min(r16, nrows - 1)];
-        const uint8_t* ap = hidden + (size_t)tok * kH + kq * 32;
-        const float* sp = hs_scale + tok;
+        const uint8_t* ap[CB];
+        const float* sp[CB];
+#pragma unroll
+        for (int c = 0; c < CB; ++c) {
+            const int tok = sorted_tok[row0 + min(16 * c + r16, nrows - 1)];
+            ap[c] = hidden + (size_t)tok * kH + kq * 32;
+            sp[c] = hs_scale + tok;
+        }
         const uint8_t* wsrc[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -292,21 +124,26 @@ __global__ __launch_bounds__(256) void gemm1_rstream_kernel(
         const float* su = sg + (size_t)kIB * kHB;
 
         v4u bw[D][4];
-        v8i ba[D];
-        float bs[D];
+        v8i ba[D][CB];
+        float bs[D][CB];
         auto issue = [&](int k) {
             const int kb = kb0 + k;
 #pragma unroll
             for (int i = 0; i < 4; ++i) bw[k % D][i] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(wsrc[i] + kb * kBlk));
-            ba[k % D] = load_v8i(ap + kb * kBlk);
-            bs[k % D] = sp[(size_t)kb * T];
+#pragma unroll
+            for (int c = 0; c < CB; ++c) {
+                ba[k % D][c] = load_v8i(ap[c] + kb * kBlk);
+                bs[k % D][c] = sp[c][(size_t)kb * T];
+            }
         };
 #pragma unroll
         for (int k = 0; k < D - 1; ++k) {
             issue(k);
             __builtin_amdgcn_sched_barrier(0);
         }
-        v4f ag = zero, au = zero;
+        v4f ag[CB], au[CB];
+#pragma unroll
+        for (int c = 0; c < CB; ++c) ag[c] = au[c] = zero;
 #pragma unroll
         for (int k = 0; k < KB; ++k) {
             if (k + D - 1 < KB) issue(k + D - 1);
@@ -332,28 +169,38 @@ __global__ __launch_bounds__(256) void gemm1_rstream_kernel(
             const v8i bg = {(int)g0[0], (int)g0[1], (int)g0[2], (int)g0[3], (int)g1[0], (int)g1[1], (int)g1[2], (int)g1[3]};
             const v8i bu = {(int)u0[0], (int)u0[1], (int)u0[2], (int)u0[3], (int)u1[0], (int)u1[1], (int)u1[2], (int)u1[3]};
             const int kb = kb0 + k;
-            const float fg = bs[k % D] * sg[kb], fu = bs[k % D] * su[kb];
-            const v4f tg = mfma_fp8(bg, ba[k % D], zero);
-            const v4f tu = mfma_fp8(bu, ba[k % D], zero);
+            const float wg = sg[kb], wu = su[kb];
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                ag[v] = __builtin_fmaf(tg[v], fg, ag[v]);
-                au[v] = __builtin_fmaf(tu[v], fu, au[v]);
+            for (int c = 0; c < CB; ++c) {
+                const float fg = bs[k % D][c] * wg, fu = bs[k % D][c] * wu;
+                const v4f tg = mfma_fp8(bg, ba[k % D][c], zero);
+                const v4f tu = mfma_fp8(bu, ba[k % D][c], zero);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    ag[c][v] = __builtin_fmaf(tg[v], fg, ag[c][v]);
+                    au[c][v] = __builtin_fmaf(tu[v], fu, au[c][v]);
+                }
             }
             __builtin_amdgcn_sched_barrier(0);
         }
 
-        red[wave][0][lane] = ag;
-        red[wave][1][lane] = au;
+#pragma unroll
+        for (int c = 0; c < CB; ++c) {
+            red[wave][0][c][lane] = ag[c];
+            red[wave][1][c][lane] = au[c];
+        }
         __syncthreads();
         if (wave == 0) {
-            v4f g = red[0][0][lane], u = red[0][1][lane];
 #pragma unroll
-            for (int q = 1; q < KSPLIT; ++q) {
-                g += red[q][0][lane];
-                u += red[q][1][lane];
+            for (int c = 0; c < CB; ++c) {
+                v4f g = red[0][0][c][lane], u = red[0][1][c][lane];
+#pragma unroll
+                for (int q = 1; q < KSPLIT; ++q) {
+                    g += red[q][0][c][lane];
+                    u += red[q][1][c][lane];
+                }
+                if (16 * c + r16 < nrows) store_swiglu4(inter, row0 + 16 * c + r16, ng * 16 + kq * 4, g, u);
             }
-            if (r16 < nrows) store_swiglu4(inter, row0 + r16, ng * 16 + kq * 4, g, u);
         }
         __syncthreads();
     }
@@ -740,11 +587,10 @@ __global__ __launch_bounds__(512, 1) void gemm1_prefill8_kernel(
 static int grid_for(long long work) { return (int)(work < 4096 ? work : 4096); }
 
 // Variants (the tile height of the dispatch they expect, and the form of C they write):
-//   1  register-staged streaming, ring of 4 K blocks     16-row tiles   bf16
-//   2  register-staged streaming, ring of 6 K blocks     16-row tiles   bf16
-//   3  LDS-landed DMA streaming, 2 row blocks per item   32-row tiles   bf16
-//   4  prefill, 4 waves, 128 x 256 workgroup tile        128-row tiles  fp8 hi/lo
-//   5  prefill, 8 waves, 256 x 256 workgroup tile        256-row tiles  fp8 hi/lo
+//   1  register-staged streaming, 1 row block per item    16-row tiles   bf16
+//   2  register-staged streaming, 2 row blocks per item   32-row tiles   bf16
+//   3  prefill, 4 waves, 128 x 256 workgroup tile        128-row tiles  fp8 hi/lo
+//   4  prefill, 8 waves, 256 x 256 workgroup tile        256-row tiles  fp8 hi/lo
 bool launch_gemm1(int variant, const uint8_t* hidden, const float* hs_scale, int T,
                   const uint8_t* w1, const float* s1, const int4* tiles, const int* num_tiles,
                   const int* exp_off, int max_tiles, const int* sorted_tok, const Intermediate& C,
@@ -755,22 +601,18 @@ bool launch_gemm1(int variant, const uint8_t* hidden, const float* hs_scale, int
     const long long mt = max_tiles;
     switch (variant) {
         case 1:
-            hipLaunchKernelGGL(gemm1_rstream_kernel<4>, dim3(grid_for(mt * G)), dim3(256), 0, stream,
+            hipLaunchKernelGGL((gemm1_rstream_kernel<4, 1>), dim3(grid_for(mt * G)), dim3(256), 0, stream,
                                hidden, hs_scale, T, w1, s1, tiles, num_tiles, sorted_tok, inter);
             return true;
         case 2:
-            hipLaunchKernelGGL(gemm1_rstream_kernel<6>, dim3(grid_for(mt * G)), dim3(256), 0, stream,
+            hipLaunchKernelGGL((gemm1_rstream_kernel<4, 2>), dim3(grid_for(mt * G)), dim3(256), 0, stream,
                                hidden, hs_scale, T, w1, s1, tiles, num_tiles, sorted_tok, inter);
             return true;
         case 3:
-            hipLaunchKernelGGL((gemm1_dma_kernel<2, 4, 3>), dim3(grid_for(mt * G)), dim3(256), 0,
-                               stream, hidden, hs_scale, T, w1, s1, tiles, num_tiles, sorted_tok, inter);
-            return true;
-        case 4:
             hipLaunchKernelGGL(gemm1_prefill_kernel<3>, dim3(prefill_grid), dim3(256), 0, stream,
                                hidden, hs_scale, T, w1, s1, tiles, num_tiles, exp_off, sorted_tok, C);
             return true;
-        case 5:
+        case 4:
             hipLaunchKernelGGL(gemm1_prefill8_kernel, dim3(prefill_grid), dim3(512), 0, stream,
                                hidden, hs_scale, T, w1, s1, tiles, num_tiles, exp_off, sorted_tok, C);
             return true;

@@ -1,4 +1,4 @@
-// gemm2.hip -- grouped GEMM2 (2048 -> 7168): bf16 MFMA for the decode kernels, FP8
+// gemm2.hip -- grouped GEMM2 (2048 -> 7168): bf16 MFMA for the streaming kernels, FP8
 // MFMA on the hi/lo form of C for the prefill kernel.
 //
 // Semantics: reference solution/cuda/moe.cu:231 (O = C @ W2[e]^T) with the 128x128
@@ -6,7 +6,7 @@
 // (the reference's CUTLASS path applies them in its mainloop,
 // moe_grouped_gemm_fp8.cu:274-322):
 //   O[r, h] = sum_kb sb2[e, h/128, kb] * sum_{i in kb} C[r, i] * W2[e, h, i]
-// Decode kernels: C is the bf16 SwiGLU output of GEMM1; W2 e4m3 bytes are widened to
+// Streaming kernels: C is the bf16 SwiGLU output of GEMM1; W2 e4m3 bytes are widened to
 // bf16 in registers (exact: every e4m3 value is a bf16 value) for
 // v_mfma_f32_16x16x32_bf16, operand A = 16 W2 rows, operand B = 16 C rows; lane l
 // supplies row l%16 and K elements 32*(l/16) + 8j..8j+7 of the block for MFMA j = 0..3
@@ -40,180 +40,16 @@ __device__ __forceinline__ v8bf as_v8bf(uint32_t a, uint32_t b, uint32_t c, uint
     return __builtin_bit_cast(v8bf, t);
 }
 
-// LDS-landed weight streaming GEMM2 (decode).  A wave owns HF groups of 16 output
-// columns (W2 rows) of one expert for one row tile, over KB consecutive K blocks.
-// W2 bytes travel HBM -> LDS with global_load_lds_dwordx4, 8 rows x 128 B (full
-// lines) per instruction, into a per-wave ring of NS slots of 16*HF rows x 128 B,
-// row r keeping its 16-byte chunk c at position c ^ swz128(r).  C rows (bf16,
-// L2-resident) come through a register ring of the same depth.  Each K block issues
-// exactly 2*HF DMA + 4*CB loads; an explicit vmcnt keeps the younger blocks in flight
-// (the compiler does not order LDS DMA against LDS reads).
-template <int CB, int KSPLIT, int NS, int HF>
-__global__ __launch_bounds__(256) void gemm2_dma_kernel(
-    const uint16_t* __restrict__ inter, const uint8_t* __restrict__ w2,
-    const float* __restrict__ s2, const int4* __restrict__ tiles,
-    const int* __restrict__ num_tiles, float* __restrict__ out_rows) {
-    constexpr int NGW = 4 / KSPLIT;
-    constexpr int KB = kIB / KSPLIT;
-    constexpr int kItems = (kH / 16) / (HF * NGW);
-    constexpr int kRows = 16 * HF;
-    constexpr int kSlot = kRows * kBlk;
-    constexpr int kVmPerKb = 2 * HF + 4 * CB;
-    static_assert(NS >= 2 && (NS - 1) * kVmPerKb < 64, "ring too deep for vmcnt");
-    __shared__ __attribute__((aligned(1024))) uint8_t ring[4][NS][kSlot];
-    __shared__ v4f red[KSPLIT > 1 ? 4 : 1][HF][CB][64];
-
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    const int r16 = lane & 15, kq = lane >> 4;
-    const int ngl = wave / KSPLIT, ks = wave % KSPLIT;
-    const int nwork = (*num_tiles) * kItems;
-    const v4f zero = {0.f, 0.f, 0.f, 0.f};
-    uint8_t* myring = &ring[wave][0][0];
-
-    const int drow = lane >> 3, dchunk = lane & 7;
-    const int swz = swz128(r16);
-    const int rd0 = r16 * kBlk + (((2 * kq) ^ swz) << 4);
-    const int rd1 = r16 * kBlk + (((2 * kq + 1) ^ swz) << 4);
-
-    for (int work = blockIdx.x; work < nwork; work += gridDim.x) {
-        const int4 tile = tiles[work / kItems];
-        const int hg0 = ((work % kItems) * NGW + ngl) * HF;
-        const int le = tile.x, row0 = tile.y, nrows = tile.z;
-        const int ncb = (nrows + 15) >> 4;
-
-        const uint16_t* cp[CB];
-#pragma unroll
-        for (int cb = 0; cb < CB; ++cb)
-            cp[cb] = inter + (size_t)(row0 + min(cb * 16 + r16, nrows - 1)) * kI + kq * 32;
-        const uint8_t* dsrc[2 * HF];
-#pragma unroll
-        for (int i = 0; i < 2 * HF; ++i) {
-            const int r = 8 * i + drow;                   // 0 .. 16*HF-1
-            const int c = dchunk ^ swz128(r);
-            dsrc[i] = w2 + (size_t)(le * kH + hg0 * 16 + r) * kI + c * 16;
-        }
-        const float* sp[HF];
-#pragma unroll
-        for (int hf = 0; hf < HF; ++hf) sp[hf] = s2 + (size_t)(le * kHB + ((hg0 + hf) >> 3)) * kIB;
-        const int kb0 = ks * KB;
-
-        v4u bc[NS][CB][4];
-        auto issue = [&](int k) {
-            const int kb = kb0 + k;
-            uint8_t* slot = myring + (k % NS) * kSlot;
-#pragma unroll
-            for (int i = 0; i < 2 * HF; ++i)
-                dma16(dsrc[i] + kb * kBlk, slot + i * 1024);
-#pragma unroll
-            for (int cb = 0; cb < CB; ++cb) {
-                const v4u* q = reinterpret_cast<const v4u*>(cp[cb] + kb * kBlk);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) bc[k % NS][cb][j] = q[j];
-            }
-        };
-
-#pragma unroll
-        for (int k = 0; k < NS - 1 && k < KB; ++k) {
-            issue(k);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        v4f acc[HF][CB];
-#pragma unroll
-        for (int hf = 0; hf < HF; ++hf)
-#pragma unroll
-            for (int cb = 0; cb < CB; ++cb) acc[hf][cb] = zero;
-
-#pragma unroll
-        for (int k = 0; k < KB; ++k) {
-            if (k + NS - 1 < KB) issue(k + NS - 1);
-            __builtin_amdgcn_sched_barrier(0);
-            const int younger = (KB - 1 - k) < (NS - 1) ? (KB - 1 - k) : (NS - 1);
-            switch (younger) {
-                case 0: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
-                case 1: __builtin_amdgcn_s_waitcnt(vmcnt_imm(1 * kVmPerKb)); break;
-                case 2: __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kVmPerKb)); break;
-                case 3: __builtin_amdgcn_s_waitcnt(vmcnt_imm(3 * kVmPerKb)); break;
-                case 4: __builtin_amdgcn_s_waitcnt(vmcnt_imm(4 * kVmPerKb)); break;
-                case 5: __builtin_amdgcn_s_waitcnt(vmcnt_imm(5 * kVmPerKb)); break;
-                case 6: __builtin_amdgcn_s_waitcnt(vmcnt_imm(6 * kVmPerKb)); break;
-                default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            const uint8_t* slot = myring + (k % NS) * kSlot;
-            const int kb = kb0 + k;
-#pragma unroll
-            for (int hf = 0; hf < HF; ++hf) {
-                const v4u x0 = *reinterpret_cast<const v4u*>(slot + hf * 16 * kBlk + rd0);
-                const v4u x1 = *reinterpret_cast<const v4u*>(slot + hf * 16 * kBlk + rd1);
-                const uint32_t ww[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-                v8bf wb[4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    uint32_t d0, d1, d2, d3;
-                    e4m3x4_to_bf16x4(ww[2 * j], d0, d1);
-                    e4m3x4_to_bf16x4(ww[2 * j + 1], d2, d3);
-                    wb[j] = as_v8bf(d0, d1, d2, d3);
-                }
-                const float sb = sp[hf][kb];
-#pragma unroll
-                for (int cb = 0; cb < CB; ++cb) {
-                    if (cb < ncb) {
-                        v4f t = zero;
-#pragma unroll
-                        for (int j = 0; j < 4; ++j)
-                            t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wb[j], __builtin_bit_cast(v8bf, bc[k % NS][cb][j]), t, 0, 0, 0);
-#pragma unroll
-                        for (int v = 0; v < 4; ++v) acc[hf][cb][v] = __builtin_fmaf(t[v], sb, acc[hf][cb][v]);
-                    }
-                }
-            }
-            __builtin_amdgcn_sched_barrier(0);
-        }
-
-        if constexpr (KSPLIT == 1) {
-#pragma unroll
-            for (int hf = 0; hf < HF; ++hf)
-#pragma unroll
-                for (int cb = 0; cb < CB; ++cb) {
-                    const int r = cb * 16 + r16;
-                    if (cb < ncb && r < nrows)
-                        *reinterpret_cast<v4f*>(out_rows + (size_t)(row0 + r) * kH + (hg0 + hf) * 16 + kq * 4) = acc[hf][cb];
-                }
-        } else {
-#pragma unroll
-            for (int hf = 0; hf < HF; ++hf)
-#pragma unroll
-                for (int cb = 0; cb < CB; ++cb)
-                    if (cb < ncb) red[wave][hf][cb][lane] = acc[hf][cb];
-            __syncthreads();
-            if (ks == 0) {
-#pragma unroll
-                for (int hf = 0; hf < HF; ++hf)
-#pragma unroll
-                    for (int cb = 0; cb < CB; ++cb) {
-                        const int r = cb * 16 + r16;
-                        if (cb < ncb) {
-                            v4f o = red[wave][hf][cb][lane];
-#pragma unroll
-                            for (int q = 1; q < KSPLIT; ++q) o += red[wave + q][hf][cb][lane];
-                            if (r < nrows)
-                                *reinterpret_cast<v4f*>(out_rows + (size_t)(row0 + r) * kH + (hg0 + hf) * 16 + kq * 4) = o;
-                        }
-                    }
-            }
-            __syncthreads();
-        }
-    }
-}
-
-// Register-staged W2 streaming (decode): the work split of gemm2_dma_kernel<1, KSPLIT,
-// ., HF>, with the W2 bytes of a K block (16 HF rows x 128 B, full-line loads) and the
-// bf16 C fragments held in a ring of D K blocks in VGPRs, and each W2 block moved to
-// the MFMA layout through a per-wave LDS slot.  Without an LDS ring more waves fit per
-// CU, so more bytes are in flight; HF > 1 shares each C fragment load among HF groups
-// of 16 output columns.
-template <int D, int KSPLIT, int HF>
+// Register-staged W2 streaming (decode and small prefill).  A wave owns HF groups of
+// 16 output columns (W2 rows) of one expert for one row tile of 16 CB rows, over
+// 16 / KSPLIT consecutive K blocks (partials of the KSPLIT waves of an item reduced
+// through LDS in a fixed order).  The W2 bytes of a K block (16 HF rows x 128 B,
+// full-line loads) and the bf16 C fragments are held in a ring of D K blocks in
+// VGPRs, and each W2 block is moved to the MFMA layout through a per-wave LDS slot.
+// Without an LDS ring more waves fit per CU, so more bytes are in flight; HF > 1
+// shares each C fragment load among HF groups of 16 output columns, and CB > 1
+// feeds each widened W2 fragment to CB blocks of 16 C rows.
+template <int D, int KSPLIT, int HF, int CB>
 __global__ __launch_bounds__(256) void gemm2_rstream_kernel(
     const uint16_t* __restrict__ inter, const uint8_t* __restrict__ w2,
     const float* __restrict__ s2, const int4* __restrict__ tiles,
@@ -221,10 +57,10 @@ __global__ __launch_bounds__(256) void gemm2_rstream_kernel(
     constexpr int NGW = 4 / KSPLIT;
     constexpr int KB = kIB / KSPLIT;
     constexpr int kItems = (kH / 16) / (NGW * HF);
-    constexpr int kVmPerKb = 2 * HF + 4;              // W2 loads, 4 C loads
+    constexpr int kVmPerKb = 2 * HF + 4 * CB;         // W2 loads, 4 C loads per row block
     static_assert(D >= 2 && (D - 1) * kVmPerKb < 64, "ring depth");
     __shared__ __attribute__((aligned(1024))) uint8_t slot_lds[4][16 * HF * kBlk];
-    __shared__ v4f red[KSPLIT > 1 ? 4 : 1][HF][64];
+    __shared__ v4f red[KSPLIT > 1 ? 4 : 1][HF][CB][64];
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -249,8 +85,11 @@ __global__ __launch_bounds__(256) void gemm2_rstream_kernel(
         const int4 tile = tiles[work / kItems];
         const int hg = ((work % kItems) * NGW + ngl) * HF;   // first of HF column groups
         const int le = tile.x, row0 = tile.y, nrows = tile.z;
-        // C row r16: bf16 elements 32 kq + 8 j .. of each K block feed MFMA j
-        const uint8_t* cp = reinterpret_cast<const uint8_t*>(inter + (size_t)(row0 + min(r16, nrows - 1)) * kI) + kq * 64;
+        // C row 16 c + r16: bf16 elements 32 kq + 8 j .. of each K block feed MFMA j
+        const uint8_t* cp[CB];
+#pragma unroll
+        for (int c = 0; c < CB; ++c)
+            cp[c] = reinterpret_cast<const uint8_t*>(inter + (size_t)(row0 + min(16 * c + r16, nrows - 1)) * kI) + kq * 64;
         const uint8_t* wsrc[2 * HF];
 #pragma unroll
         for (int i = 0; i < 2 * HF; ++i)
@@ -260,22 +99,26 @@ __global__ __launch_bounds__(256) void gemm2_rstream_kernel(
         for (int hf = 0; hf < HF; ++hf) sp[hf] = s2 + (size_t)(le * kHB + ((hg + hf) >> 3)) * kIB;
 
         v4u bw[D][2 * HF];
-        v4u bc[D][4];
+        v4u bc[D][CB][4];
         auto issue = [&](int k) {
             const int kb = kb0 + k;
 #pragma unroll
             for (int i = 0; i < 2 * HF; ++i) bw[k % D][i] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(wsrc[i] + kb * kBlk));
 #pragma unroll
-            for (int j = 0; j < 4; ++j) bc[k % D][j] = *reinterpret_cast<const v4u*>(cp + kb * 2 * kBlk + 16 * j);
+            for (int c = 0; c < CB; ++c)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) bc[k % D][c][j] = *reinterpret_cast<const v4u*>(cp[c] + kb * 2 * kBlk + 16 * j);
         };
 #pragma unroll
         for (int k = 0; k < D - 1 && k < KB; ++k) {
             issue(k);
             __builtin_amdgcn_sched_barrier(0);
         }
-        v4f acc[HF];
+        v4f acc[HF][CB];
 #pragma unroll
-        for (int hf = 0; hf < HF; ++hf) acc[hf] = zero;
+        for (int hf = 0; hf < HF; ++hf)
+#pragma unroll
+            for (int c = 0; c < CB; ++c) acc[hf][c] = zero;
 #pragma unroll
         for (int k = 0; k < KB; ++k) {
             if (k + D - 1 < KB) issue(k + D - 1);
@@ -299,39 +142,55 @@ __global__ __launch_bounds__(256) void gemm2_rstream_kernel(
                 const v4u x0 = *reinterpret_cast<const v4u*>(slot + hf * 16 * kBlk + rd0);
                 const v4u x1 = *reinterpret_cast<const v4u*>(slot + hf * 16 * kBlk + rd1);
                 const uint32_t ww[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-                v4f t = zero;
+                v4f t[CB];
+#pragma unroll
+                for (int c = 0; c < CB; ++c) t[c] = zero;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     uint32_t d0, d1, d2, d3;
                     e4m3x4_to_bf16x4(ww[2 * j], d0, d1);
                     e4m3x4_to_bf16x4(ww[2 * j + 1], d2, d3);
-                    t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(d0, d1, d2, d3),
-                                                                 __builtin_bit_cast(v8bf, bc[k % D][j]), t, 0, 0, 0);
+                    const v8bf wj = as_v8bf(d0, d1, d2, d3);
+#pragma unroll
+                    for (int c = 0; c < CB; ++c)
+                        t[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wj, __builtin_bit_cast(v8bf, bc[k % D][c][j]), t[c], 0, 0, 0);
                 }
                 const float sb = sp[hf][kb0 + k];
 #pragma unroll
-                for (int v = 0; v < 4; ++v) acc[hf][v] = __builtin_fmaf(t[v], sb, acc[hf][v]);
+                for (int c = 0; c < CB; ++c)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) acc[hf][c][v] = __builtin_fmaf(t[c][v], sb, acc[hf][c][v]);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
 
         if constexpr (KSPLIT == 1) {
-            if (r16 < nrows) {
 #pragma unroll
-                for (int hf = 0; hf < HF; ++hf)
-                    *reinterpret_cast<v4f*>(out_rows + (size_t)(row0 + r16) * kH + (hg + hf) * 16 + kq * 4) = acc[hf];
+            for (int c = 0; c < CB; ++c) {
+                if (16 * c + r16 < nrows) {
+#pragma unroll
+                    for (int hf = 0; hf < HF; ++hf)
+                        *reinterpret_cast<v4f*>(out_rows + (size_t)(row0 + 16 * c + r16) * kH + (hg + hf) * 16 + kq * 4) = acc[hf][c];
+                }
             }
         } else {
 #pragma unroll
-            for (int hf = 0; hf < HF; ++hf) red[wave][hf][lane] = acc[hf];
+            for (int hf = 0; hf < HF; ++hf)
+#pragma unroll
+                for (int c = 0; c < CB; ++c) red[wave][hf][c][lane] = acc[hf][c];
             __syncthreads();
-            if (ks == 0 && r16 < nrows) {
+            if (ks == 0) {
 #pragma unroll
-                for (int hf = 0; hf < HF; ++hf) {
-                    v4f o = red[wave][hf][lane];
+                for (int c = 0; c < CB; ++c) {
+                    if (16 * c + r16 < nrows) {
 #pragma unroll
-                    for (int q = 1; q < KSPLIT; ++q) o += red[wave + q][hf][lane];
-                    *reinterpret_cast<v4f*>(out_rows + (size_t)(row0 + r16) * kH + (hg + hf) * 16 + kq * 4) = o;
+                        for (int hf = 0; hf < HF; ++hf) {
+                            v4f o = red[wave][hf][c][lane];
+#pragma unroll
+                            for (int q = 1; q < KSPLIT; ++q) o += red[wave + q][hf][c][lane];
+                            *reinterpret_cast<v4f*>(out_rows + (size_t)(row0 + 16 * c + r16) * kH + (hg + hf) * 16 + kq * 4) = o;
+                        }
+                    }
                 }
             }
             __syncthreads();
@@ -517,13 +376,11 @@ __global__ void e4m3_to_bf16_kernel(const uint32_t* __restrict__ in, uint2* __re
 static int grid_for2(long long work) { return (int)(work < 4096 ? work : 4096); }
 
 // Variants (the tile height of the dispatch they expect, and the form of C they read):
-//   1  register-staged streaming, K split 4, 16 output columns per wave   16-row   bf16
-//   2  register-staged streaming, K split 4, 32 output columns per wave   16-row   bf16
-//   3  register-staged streaming, K split 2, 32 output columns per wave   16-row   bf16
-//   4  register-staged streaming, K split 4, 64 output columns per wave   16-row   bf16
-//   5  LDS-landed DMA streaming, 2 row blocks x 32 columns per item        32-row   bf16
-//   6  prefill, 8 waves, 128 x 256 workgroup tile                          128-row  hi/lo
-//   7  the same kernel over the 128-row second tile list of a 256-row dispatch      hi/lo
+//   1  register-staged streaming, 32 columns x 1 row block per wave      16-row   bf16
+//   2  register-staged streaming, 64 columns x 1 row block per wave      16-row   bf16
+//   3  register-staged streaming, 64 columns x 2 row blocks per wave     32-row   bf16
+//   4  prefill, 8 waves, 128 x 256 workgroup tile                        128-row  hi/lo
+//   5  the same kernel over the 128-row second tile list of a 256-row dispatch    hi/lo
 bool launch_gemm2(int variant, const Intermediate& C, const uint8_t* w2, const float* s2,
                   const int4* tiles, const int* num_tiles, const int* exp_off, int max_tiles,
                   float* out_rows, hipStream_t stream) {
@@ -532,27 +389,19 @@ bool launch_gemm2(int variant, const Intermediate& C, const uint8_t* w2, const f
     constexpr int G = kH / 16;      // 16-column groups
     switch (variant) {
         case 1:
-            hipLaunchKernelGGL((gemm2_rstream_kernel<4, 4, 1>), dim3(grid_for2(mt * G)), dim3(256), 0,
+            hipLaunchKernelGGL((gemm2_rstream_kernel<4, 4, 2, 1>), dim3(grid_for2(mt * G / 2)), dim3(256), 0,
                                stream, inter, w2, s2, tiles, num_tiles, out_rows);
             return true;
         case 2:
-            hipLaunchKernelGGL((gemm2_rstream_kernel<4, 4, 2>), dim3(grid_for2(mt * G / 2)), dim3(256), 0,
+            hipLaunchKernelGGL((gemm2_rstream_kernel<3, 4, 4, 1>), dim3(grid_for2(mt * G / 4)), dim3(256), 0,
                                stream, inter, w2, s2, tiles, num_tiles, out_rows);
             return true;
         case 3:
-            hipLaunchKernelGGL((gemm2_rstream_kernel<4, 2, 2>), dim3(grid_for2(mt * G / 4)), dim3(256), 0,
+            hipLaunchKernelGGL((gemm2_rstream_kernel<3, 4, 4, 2>), dim3(grid_for2(mt * G / 4)), dim3(256), 0,
                                stream, inter, w2, s2, tiles, num_tiles, out_rows);
             return true;
         case 4:
-            hipLaunchKernelGGL((gemm2_rstream_kernel<3, 4, 4>), dim3(grid_for2(mt * G / 4)), dim3(256), 0,
-                               stream, inter, w2, s2, tiles, num_tiles, out_rows);
-            return true;
         case 5:
-            hipLaunchKernelGGL((gemm2_dma_kernel<2, 2, 3, 2>), dim3(grid_for2(mt * G / 4)), dim3(256), 0,
-                               stream, inter, w2, s2, tiles, num_tiles, out_rows);
-            return true;
-        case 6:
-        case 7:
             hipLaunchKernelGGL(gemm2_prefill8_kernel, dim3(256), dim3(512), 0, stream, C, w2, s2, tiles,
                                num_tiles, exp_off, out_rows);
             return true;

@@ -117,10 +117,11 @@ def _first_tokens(d0: dict, T: int) -> dict:
     return d
 
 
-@pytest.mark.parametrize("T", [96, 97, 256, 257, 2048, 2049])
+@pytest.mark.parametrize("T", [96, 97, 192, 193, 896, 897, 2048, 2049])
 def test_plan_boundaries_match_oracle(T):
-    """Token counts on both sides of every change of kernel plan (16-row streaming,
-    32-row streaming, 128-row and 256-row prefill tiles)."""
+    """Token counts on both sides of every change of kernel plan (16-row streaming
+    with 32 then 64 GEMM2 columns per wave, 32-row streaming, 128-row and 256-row
+    prefill tiles)."""
     d = _first_tokens(config_inputs(3), T)
     note(f"[gpu] plan boundary T={T}")
     out = run_forward(d)
@@ -131,8 +132,8 @@ def test_plan_boundaries_match_oracle(T):
     assert st["frac_within"] == 1.0, st
 
 
-@pytest.mark.parametrize("T,g1,g2", [(64, 1, 1), (64, 1, 3), (64, 2, 4), (200, 3, 5),
-                                     (1000, 4, 6), (3000, 5, 7)])
+@pytest.mark.parametrize("T,g1,g2", [(64, 1, 1), (64, 1, 2), (150, 1, 2), (64, 2, 3),
+                                     (500, 2, 3), (1000, 3, 4), (3000, 4, 5)])
 def test_every_gemm_variant_matches_oracle(T, g1, g2, monkeypatch):
     """Each GEMM1 / GEMM2 kernel variant (forced with MOE_MI355_G1 / _G2, which the
     library reads on every call) stays within the tolerance."""
