@@ -53,6 +53,7 @@ def parse():
     ap.add_argument("--config", type=int, default=1, help="index into BASELINE.json configs")
     ap.add_argument("--rotate", type=int, default=4, help="input copies cycled over steps")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-graph", action="store_true", help="skip the HIP-graph replay timing")
     ap.add_argument("--cpu-budget-s", type=float, default=20.0)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run K device-to-device copies of MIB MiB (calibrates "
@@ -155,6 +156,33 @@ def main() -> int:
     k.profile_end()
     stages_us = {name: ms * 1e3 for name, ms in zip(k.STAGES, stage_ms)}
 
+    # HIP-graph replay: the forward only launches kernels on the caller's stream, so a
+    # caller can capture a call and replay it (one graph per input copy, replayed
+    # round-robin); reported beside the eager latency, which stays the value
+    graph_us = None
+    if not a.no_graph:
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            for al in arglists:
+                k.kernel(*al, workspace=ws)
+        stream.wait_stream(side)
+        torch.cuda.synchronize()
+        graphs = []
+        for al in arglists:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                k.kernel(*al, workspace=ws)
+            graphs.append(g)
+        for i in range(a.warmup):
+            graphs[i % len(graphs)].replay()
+        torch.cuda.synchronize()
+        g0 = time.perf_counter()
+        for i in range(a.steps):
+            graphs[i % len(graphs)].replay()
+        torch.cuda.synchronize()
+        graph_us = (time.perf_counter() - g0) * 1e6 / a.steps
+
     # roofline of the dominant kernel (algorithmic bytes / flops, never padded rows)
     dom = max(("gemm1", "gemm2", "combine", "route", "dispatch"), key=lambda s: stages_us[s])
     n_a, e_a = work["N_a"], work["E_a"]
@@ -238,7 +266,8 @@ def main() -> int:
                    "parallelism": "ep-rank (32 of 256 experts) on 1 GPU"},
         "latency_us": {"mean_wall": round(lat_us, 3), "median_event": float(np.median(ev_us)),
                        "p10_event": float(np.percentile(ev_us, 10)),
-                       "p90_event": float(np.percentile(ev_us, 90))},
+                       "p90_event": float(np.percentile(ev_us, 90)),
+                       "graph_replay_wall": None if graph_us is None else round(graph_us, 3)},
         "eff_tflops": eff_tflops,
         "work": {"N_a": n_a, "E_a": e_a, "tokens_touched": touched, "flops": work["flops"],
                  "bytes": work["bytes"]},
