@@ -183,6 +183,27 @@ def main() -> int:
         torch.cuda.synchronize()
         graph_us = (time.perf_counter() - g0) * 1e6 / a.steps
 
+    # the step before the operator: blockwise FP8 quantizer of bf16 activations
+    # [T, 7168] (algorithmic bytes: read 2 B, write 1 B per element, 4 B per scale)
+    xq = [torch.randn(T, 7168, device=dev).to(torch.bfloat16) for _ in range(2)]
+    qo = torch.empty(T, 7168, dtype=torch.float8_e4m3fn, device=dev)
+    qs = torch.empty(56, T, dtype=torch.float32, device=dev)
+    for i in range(a.warmup):
+        k.quantize_fp8_blockwise(xq[i % 2], qo, qs)
+    qe0, qe1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    qe0.record(stream)
+    for i in range(a.steps):
+        k.quantize_fp8_blockwise(xq[i % 2], qo, qs)
+    qe1.record(stream)
+    torch.cuda.synchronize()
+    q_us = qe0.elapsed_time(qe1) * 1e3 / a.steps
+    q_bytes = T * 7168 * 3 + T * 56 * 4
+    quant = dict(us=round(q_us, 3), bytes=q_bytes, gbs=q_bytes / (q_us * 1e-6) / 1e9,
+                 hbm_frac=q_bytes / (q_us * 1e-6) / (HBM_PEAK_GBS * 1e9),
+                 input="bf16 [T, 7168] -> e4m3 + fp32 [56, T]")
+    del xq
+
     # roofline of the dominant kernel (algorithmic bytes / flops, never padded rows)
     dom = max(("gemm1", "gemm2", "combine", "route", "dispatch"), key=lambda s: stages_us[s])
     n_a, e_a = work["N_a"], work["E_a"]
@@ -278,6 +299,7 @@ def main() -> int:
         "profiled_calls": n_prof,
         "roofline": roof,
         "cpu_baseline": cpu,
+        "quantizer": quant,
     }
     print(json.dumps(line))
     return 0

@@ -32,6 +32,7 @@ bool launch_gemm2(int, const Intermediate&, const uint8_t*, const float*, const 
                   const int*, int, float*, hipStream_t);
 void launch_combine(const float*, const float*, const int*, int, uint16_t*, hipStream_t);
 void launch_e4m3_to_bf16(const uint8_t*, uint16_t*, int, hipStream_t);
+void launch_quantize_fp8_blockwise(const void*, int, int, int, uint8_t*, float*, hipStream_t);
 }  // namespace moe
 
 namespace {
@@ -184,6 +185,18 @@ int moe_mi355_route(const float* routing_logits, const uint16_t* routing_bias, i
     hipStream_t s = (hipStream_t)stream;
     moe::launch_route(routing_logits, routing_bias, T, (float)routed_scaling_factor, topk_ids,
                       topk_weights, s);
+    return hip_status(hipGetLastError());
+}
+
+int moe_mi355_quantize_fp8_blockwise(const void* x, int32_t x_dtype, int32_t rows, int32_t cols,
+                                     uint8_t* q, float* scales, void* stream) {
+    if (x_dtype != MOE_MI355_DTYPE_F32 && x_dtype != MOE_MI355_DTYPE_BF16) return MOE_ERR_BAD_SIZE;
+    if (rows < 0 || cols <= 0 || cols % MOE_MI355_BLOCK != 0 || cols > MOE_MI355_QUANT_MAX_COLS)
+        return MOE_ERR_BAD_SIZE;
+    if (rows == 0) return MOE_OK;
+    if (!x || !q || !scales) return MOE_ERR_NULL_POINTER;
+    if (!aligned16(x) || ((uintptr_t)q & 7u) || ((uintptr_t)scales & 3u)) return MOE_ERR_MISALIGNED;
+    moe::launch_quantize_fp8_blockwise(x, x_dtype, rows, cols, q, scales, (hipStream_t)stream);
     return hip_status(hipGetLastError());
 }
 

@@ -206,17 +206,6 @@ __global__ __launch_bounds__(256) void gemm1_rstream_kernel(
     }
 }
 
-// Four floats -> four e4m3 bytes (v_cvt_pk_fp8_f32: round to nearest even, OCP e4m3fn,
-// the same rounding as torch's float8_e4m3fn cast; inputs are clamped to +-448
-// beforehand so nothing overflows to NaN).
-__device__ __forceinline__ uint32_t e4m3x4_from_f32(float a, float b, float c, float d) {
-    int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
-    w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
-    return (uint32_t)w;
-}
-
-__device__ __forceinline__ float clamp448(float x) { return fminf(fmaxf(x, -448.f), 448.f); }
-
 // Epilogue of the prefill GEMM1 kernels: SwiGLU, then the fp8 hi/lo form of C.
 // The wave holds 64 rows x 64 SwiGLU columns (acc[s][j]: j < 4 gate, j >= 4 up; lane
 // holds D[col 16j + 4kq + v][row 16s + r16]); its partner wave (wn ^ 1) holds the other

@@ -41,6 +41,17 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
     return __uint_as_float(h << 16);
 }
 
+// Four floats -> four e4m3 bytes (v_cvt_pk_fp8_f32: round to nearest even, OCP e4m3fn,
+// the same rounding as torch's float8_e4m3fn cast; inputs are clamped to +-448
+// beforehand so nothing overflows to NaN).
+__device__ __forceinline__ uint32_t e4m3x4_from_f32(float a, float b, float c, float d) {
+    int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+    return (uint32_t)w;
+}
+
+__device__ __forceinline__ float clamp448(float x) { return fminf(fmaxf(x, -448.f), 448.f); }
+
 // Order-preserving 32-bit image of an fp32 score; NaN maps to 0 (never preferred).
 __device__ __forceinline__ uint32_t order_bits(float f) {
     uint32_t u = __float_as_uint(f);

@@ -84,6 +84,7 @@ def _declare(L: ctypes.CDLL) -> ctypes.CDLL:
         "moe_mi355_profile_read": (ctypes.c_int, [P, I32]),
         "moe_mi355_profile_end": (ctypes.c_int, []),
         "moe_mi355_debug_e4m3_to_bf16": (ctypes.c_int, [P, P, I32, P]),
+        "moe_mi355_quantize_fp8_blockwise": (ctypes.c_int, [P, I32, I32, I32, P, P, P]),
         "moe_mi355_strerror": (ctypes.c_char_p, [ctypes.c_int]),
         "moe_mi355_last_hip_error": (ctypes.c_char_p, []),
         "moe_mi355_version": (ctypes.c_char_p, []),
@@ -307,6 +308,44 @@ def dispatch(topk_ids: torch.Tensor, topk_weights: torch.Tensor, local_expert_of
                                   ctypes.c_void_p(_stream_ptr(dev)))
     _check(rc, "moe_mi355_dispatch")
     return out
+
+
+QUANT_MAX_COLS = 32768
+
+
+def quantize_fp8_blockwise(x: torch.Tensor, out: torch.Tensor | None = None,
+                           scales: torch.Tensor | None = None):
+    """Blockwise FP8 quantizer of activations (the step before the operator; the
+    reference's quantize_fp8_blockwise_kernel, solution/python/kernel.cu:998-1062).
+
+    ``x``: bfloat16 or float32 [rows, cols] on the GPU, cols a multiple of 128.
+    Returns ``(q, scales)``: q float8_e4m3fn [rows, cols], scales float32
+    [cols / 128, rows] (the ``hidden_states_scale`` layout), with per row and
+    128-column block ``scale = absmax / 448`` (1 for an all-zero block) and
+    ``q = e4m3(clamp(x * (1 / scale), -448, 448))``, round to nearest even.
+    ``out`` / ``scales`` may be passed pre-allocated (destination-passing)."""
+    L = _build_extension()
+    if x.dtype not in (torch.bfloat16, torch.float32) or x.dim() != 2:
+        raise ValueError("x must be a 2-D bfloat16 or float32 tensor")
+    rows, cols = x.shape
+    if cols <= 0 or cols % BLK or cols > QUANT_MAX_COLS:
+        raise ValueError(f"cols must be a positive multiple of {BLK} and <= {QUANT_MAX_COLS}")
+    if not x.is_cuda:
+        raise ValueError("x must be a GPU tensor")
+    dev = x.device
+    xc = x.contiguous()
+    if out is None:
+        out = torch.empty(rows, cols, dtype=torch.float8_e4m3fn, device=dev)
+    if scales is None:
+        scales = torch.empty(cols // BLK, rows, dtype=torch.float32, device=dev)
+    _expect(out, "out", torch.float8_e4m3fn, (rows, cols))
+    _expect(scales, "scales", torch.float32, (cols // BLK, rows))
+    dt = 1 if x.dtype == torch.bfloat16 else 0
+    with torch.cuda.device(dev):
+        rc = L.moe_mi355_quantize_fp8_blockwise(xc.data_ptr(), dt, rows, cols, out.data_ptr(),
+                                                scales.data_ptr(), ctypes.c_void_p(_stream_ptr(dev)))
+    _check(rc, "moe_mi355_quantize_fp8_blockwise")
+    return out, scales
 
 
 def profile_begin(max_calls: int) -> None:

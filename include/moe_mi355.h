@@ -125,6 +125,24 @@ MOE_MI355_API int moe_mi355_dispatch(const int32_t* topk_ids, const float* topk_
                        float* sorted_weights, int32_t* inverse_rows, int32_t* tiles,
                        int32_t* num_tiles, int32_t* chunk_counts, void* stream);
 
+/* Blockwise FP8 quantizer of activations, the step before the operator (replaces the
+ * reference's quantize_fp8_blockwise_kernel, solution/python/kernel.cu:998-1062, which
+ * takes fp32 input and is not launched by the reference operator).  x [rows, cols] is
+ * fp32 (x_dtype = MOE_MI355_DTYPE_F32) or bf16 bits (MOE_MI355_DTYPE_BF16).  Per row and
+ * 128-column block: scale = absmax / 448 (1 for an all-zero block; NaN is ignored by
+ * the absmax), q = e4m3(clamp(x * (1 / scale), -448, 448)) rounded to nearest even
+ * (a NaN input gives -448, as the reference's fmaxf/fminf clamp does).
+ *   q      e4m3 [rows, cols]
+ *   scales fp32 [cols / 128, rows]  (the layout of hidden_states_scale)
+ * cols must be a positive multiple of 128, at most MOE_MI355_QUANT_MAX_COLS; x 16-byte,
+ * q 8-byte, scales 4-byte aligned. */
+#define MOE_MI355_DTYPE_F32 0
+#define MOE_MI355_DTYPE_BF16 1
+#define MOE_MI355_QUANT_MAX_COLS 32768
+MOE_MI355_API int moe_mi355_quantize_fp8_blockwise(const void* x, int32_t x_dtype, int32_t rows,
+                                                   int32_t cols, uint8_t* q, float* scales,
+                                                   void* stream);
+
 /* Upper bound on the number of row tiles for T tokens and tile height tile_m. */
 MOE_MI355_API int32_t moe_mi355_max_tiles(int32_t T, int32_t tile_m);
 

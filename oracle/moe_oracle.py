@@ -291,6 +291,63 @@ def forward(routing_logits, routing_bias, hidden_states, hidden_states_scale,
 
 
 # --------------------------------------------------------------------------- #
+# activation quantizer, the step before the operator (kernel.cu:998-1062)     #
+# --------------------------------------------------------------------------- #
+
+def e4m3_encode_rne(v, _ties: str = "even") -> np.ndarray:
+    """fp32 -> e4m3fn bytes, round to nearest, ties to even, for |v| <= 448.
+
+    Written from the OCP FP8 E4M3 definition on the decode table of moe_oracle.c (the
+    127 non-negative finite codes 0x00..0x7E have increasing magnitudes): the nearest
+    code, on a tie the one with an even mantissa (code & 1 == 0); the sign bit copied,
+    so -0.0 gives 0x80.  Values above 448 saturate to 448 (callers clamp first).
+    ``_ties="away"`` is a planted mistake for the pin tests only."""
+    v = np.asarray(v, dtype=np.float32)
+    tab = e4m3_table()[:127].astype(np.float64)
+    a = np.abs(v.astype(np.float64)).ravel()
+    hi = np.clip(np.searchsorted(tab, a, side="left"), 0, 126)
+    lo = np.clip(hi - 1, 0, 126)
+    dlo = a - tab[lo]
+    dhi = tab[hi] - a
+    if _ties == "even":
+        tie_hi = (hi % 2) == 0
+    elif _ties == "away":
+        tie_hi = np.ones_like(hi, dtype=bool)
+    else:
+        raise ValueError(_ties)
+    code = np.where((dhi < dlo) | ((dhi == dlo) & tie_hi), hi, lo).astype(np.uint8)
+    code |= (np.signbit(v).ravel().astype(np.uint8) << 7)
+    return code.reshape(v.shape)
+
+
+def quantize_fp8_blockwise(x, _block_amax: bool = True):
+    """Blockwise FP8 quantizer (solution/python/kernel.cu:998-1062) in fp32 numpy.
+
+    ``x`` [rows, cols] (float32, or bfloat16 as a torch tensor; widened exactly).  Per
+    row and 128-column block: ``absmax`` with fmaxf semantics (NaN ignored,
+    kernel.cu:1020-1024), ``scale = absmax / 448`` or 1 for an all-zero block
+    (kernel.cu:1037), ``inv = 1 / scale`` (1038), ``q = e4m3(fminf(fmaxf(x * inv,
+    -448), 448))`` round to nearest even (999-1002, 1048-1050).  Returns (q uint8
+    [rows, cols], scales fp32 [cols / 128, rows]) (column-major scales, 1041-1044).
+    ``_block_amax=False`` (one absmax per row) is a planted mistake for the pin tests."""
+    if isinstance(x, torch.Tensor):
+        x = x.detach().cpu().to(torch.float32).numpy()
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, cols = x.shape
+    nb = cols // BLK
+    b = x.reshape(rows, nb, BLK)
+    amax = np.fmax.reduce(np.abs(b), axis=2, initial=np.float32(0.0)).astype(np.float32)
+    if not _block_amax:
+        amax = np.repeat(np.fmax.reduce(amax, axis=1, initial=np.float32(0.0))[:, None], nb, axis=1)
+    scale = np.where(amax > 0, amax / np.float32(448.0), np.float32(1.0)).astype(np.float32)
+    inv = (np.float32(1.0) / scale).astype(np.float32)
+    y = (b * inv[:, :, None]).astype(np.float32)
+    y = np.fmin(np.fmax(y, np.float32(-448.0)), np.float32(448.0))
+    q = e4m3_encode_rne(y).reshape(rows, cols)
+    return q, np.ascontiguousarray(scale.T)
+
+
+# --------------------------------------------------------------------------- #
 # CPU baseline: the reference's own CPU-shaped path (moe.cu:137-240)           #
 # --------------------------------------------------------------------------- #
 
