@@ -123,7 +123,7 @@ def main() -> int:
 
     # warmup
     for i in range(a.warmup):
-        k.kernel(*arglists[i % len(arglists)], workspace=ws)
+        k.forward(*arglists[i % len(arglists)], workspace=ws)
     torch.cuda.synchronize()
 
     # timed region: exactly K steps back to back, synchronised on both sides
@@ -131,7 +131,7 @@ def main() -> int:
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(a.steps):
-        k.kernel(*arglists[i % len(arglists)], workspace=ws)
+        k.forward(*arglists[i % len(arglists)], workspace=ws)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     ms_per_step = (t1 - t0) * 1e3 / a.steps
@@ -142,7 +142,7 @@ def main() -> int:
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(a.steps)]
     for i in range(a.steps):
         starts[i].record(stream)
-        k.kernel(*arglists[i % len(arglists)], workspace=ws)
+        k.forward(*arglists[i % len(arglists)], workspace=ws)
         ends[i].record(stream)
     torch.cuda.synchronize()
     ev_us = np.array([s.elapsed_time(e) * 1e3 for s, e in zip(starts, ends)])
@@ -150,7 +150,7 @@ def main() -> int:
     # per-kernel durations: HIP events recorded by the library on its launch stream
     k.profile_begin(a.steps)
     for i in range(a.steps):
-        k.kernel(*arglists[i % len(arglists)], workspace=ws, flags=k.FLAG_PROFILE)
+        k.forward(*arglists[i % len(arglists)], workspace=ws, flags=k.FLAG_PROFILE)
     torch.cuda.synchronize()
     n_prof, stage_ms = k.profile_read()
     k.profile_end()
@@ -165,14 +165,14 @@ def main() -> int:
         side.wait_stream(stream)
         with torch.cuda.stream(side):
             for al in arglists:
-                k.kernel(*al, workspace=ws)
+                k.forward(*al, workspace=ws)
         stream.wait_stream(side)
         torch.cuda.synchronize()
         graphs = []
         for al in arglists:
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
-                k.kernel(*al, workspace=ws)
+                k.forward(*al, workspace=ws)
             graphs.append(g)
         for i in range(a.warmup):
             graphs[i % len(graphs)].replay()

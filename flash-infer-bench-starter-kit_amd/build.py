@@ -19,7 +19,9 @@ REPO = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libmoe_mi355.so")
-INCLUDE = os.path.join(REPO, "include")
+# the C-ABI header: include/ next to this file in a packed solution, else the repo's
+INCLUDE = os.path.join(HERE, "include") if os.path.isdir(os.path.join(HERE, "include")) \
+    else os.path.join(REPO, "include")
 
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 ARCH = "gfx950"

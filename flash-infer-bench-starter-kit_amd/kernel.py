@@ -211,15 +211,25 @@ def kernel(
     local_expert_offset,   # int
     routed_scaling_factor, # float
     output,                # [T, 7168]         bfloat16 (DPS, pre-allocated)
-    *,
-    workspace: torch.Tensor | None = None,
-    flags: int = 0,
 ):
     """MoE forward pass on gfx950 HIP kernels; writes ``output`` in place, returns None.
 
-    ``workspace`` (keyword-only, optional) lets a caller supply and later inspect
-    the uint8 scratch buffer (>= workspace_bytes(T), 256-byte aligned); by default
-    one is taken from the caching allocator on the current stream."""
+    The harness's destination-passing entry point: exactly the reference's 10 inputs
+    and 1 output (solution/python/kernel.py:95-107), no variadic or extra parameters.
+    The scratch workspace comes from the caching allocator on the current stream;
+    ``forward`` takes it (and the profiling flags) explicitly."""
+    forward(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+            gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset,
+            routed_scaling_factor, output)
+
+
+def forward(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+            gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset,
+            routed_scaling_factor, output, *, workspace: torch.Tensor | None = None,
+            flags: int = 0):
+    """``kernel`` with a caller-supplied uint8 workspace (>= workspace_bytes(T),
+    256-byte aligned; it can be inspected afterwards with workspace_layout) and call
+    flags (FLAG_PROFILE records the stage profiler's events)."""
     L = _build_extension()
     T, logits, hs_scale = validate(routing_logits, routing_bias, hidden_states,
                                    hidden_states_scale, gemm1_weights, gemm1_weights_scale,

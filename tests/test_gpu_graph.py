@@ -18,7 +18,7 @@ pytestmark = pytest.mark.gpu
 
 def _eager(k, wl, d, ws):
     out = torch.full_like(d["output"], float("nan"))
-    k.kernel(*wl.as_args({**d, "output": out}), workspace=ws)
+    k.forward(*wl.as_args({**d, "output": out}), workspace=ws)
     torch.cuda.synchronize()
     return out
 
@@ -40,12 +40,12 @@ def test_graph_replay_matches_eager(idx):
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):          # warm-up on the capture stream
-        k.kernel(*args, workspace=ws)
+        k.forward(*args, workspace=ws)
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        k.kernel(*args, workspace=ws)
+        k.forward(*args, workspace=ws)
     torch.cuda.synchronize()
 
     for rep in range(3):

@@ -139,7 +139,7 @@ def test_forward_routing_in_workspace_is_bit_exact():
     ws = torch.empty(lay.total, dtype=torch.uint8, device="cuda")
     wl = pkg("workloads")
     out = torch.empty_like(d["output"])
-    k.kernel(*wl.as_args({**d, "output": out}), workspace=ws)
+    k.forward(*wl.as_args({**d, "output": out}), workspace=ws)
     torch.cuda.synchronize()
     ids = ws[lay.topk_ids:lay.topk_ids + T * 32].view(torch.int32).view(T, 8).cpu().numpy()
     o = oracle()
@@ -166,7 +166,7 @@ def test_prefill_intermediate_hilo_rows(idx):
     ws = torch.empty(lay.total, dtype=torch.uint8, device="cuda")
     out = torch.empty_like(d["output"])
     note(f"[gpu] hi/lo intermediate config {idx}")
-    k.kernel(*wl.as_args({**d, "output": out}), workspace=ws)
+    k.forward(*wl.as_args({**d, "output": out}), workspace=ws)
     torch.cuda.synchronize()
     R = T * 8
     exp_off = ws[lay.meta:lay.meta + 33 * 4].view(torch.int32).cpu().numpy()
