@@ -38,7 +38,7 @@ __device__ __forceinline__ void load8(const float* __restrict__ p, float (&v)[8]
 // takes the block absmax with a 4-step xor shuffle inside its 16 lanes.  The 8 waves
 // of a workgroup hold 8 consecutive rows; their scales go through LDS so each block's
 // 8 scales leave as one contiguous 32-byte run of the column-major scale array.
-template <typename In>
+template <typename In, int NP>
 __global__ __launch_bounds__(64 * kQuantRows) void quantize_fp8_blockwise_kernel(
     const In* __restrict__ x, int rows, int cols, uint8_t* __restrict__ q,
     float* __restrict__ scales) {
@@ -49,36 +49,48 @@ __global__ __launch_bounds__(64 * kQuantRows) void quantize_fp8_blockwise_kernel
     const int nb = cols >> 7;
     const int g = lane >> 4;
     const int e0 = (lane & 15) * 8;
+    // one 128-column block of 16 lanes: absmax, scale, 8 codes, scale to LDS
+    auto block = [&](int b, const float (&v)[8], uint8_t* qr) {
+        float m = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
+        m = fmaxf(m, __shfl_xor(m, 1, 16));
+        m = fmaxf(m, __shfl_xor(m, 2, 16));
+        m = fmaxf(m, __shfl_xor(m, 4, 16));
+        m = fmaxf(m, __shfl_xor(m, 8, 16));
+        const float scale = (m > 0.0f) ? (m / 448.0f) : 1.0f;
+        const float inv = 1.0f / scale;
+        uint2 pk;
+        pk.x = e4m3x4_from_f32(clamp448(v[0] * inv), clamp448(v[1] * inv),
+                               clamp448(v[2] * inv), clamp448(v[3] * inv));
+        pk.y = e4m3x4_from_f32(clamp448(v[4] * inv), clamp448(v[5] * inv),
+                               clamp448(v[6] * inv), clamp448(v[7] * inv));
+        *reinterpret_cast<uint2*>(qr + b * 128 + e0) = pk;
+        if ((lane & 15) == 0) sc[b][wave] = scale;
+    };
     if (row < rows) {
         const In* xr = x + (size_t)row * cols;
         uint8_t* qr = q + (size_t)row * cols;
-        // the next pass's load is issued before this pass's conversion, so each wave
-        // keeps two 16-byte loads in flight
-        float v[8], vn[8];
-        if (g < nb) load8(xr + g * 128 + e0, v);
-        for (int b0 = 0; b0 < nb; b0 += 4) {
-            const int b = b0 + g;
-            if (b + 4 < nb) load8(xr + (b + 4) * 128 + e0, vn);
-            if (b < nb) {                       // uniform inside each 16-lane group
-                float m = 0.0f;
+        if constexpr (NP > 0) {
+            // width known at compile time (NP passes of 4 blocks): every load of the
+            // row is issued before the first conversion
+            float v[NP][8];
 #pragma unroll
-                for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
-                m = fmaxf(m, __shfl_xor(m, 1, 16));
-                m = fmaxf(m, __shfl_xor(m, 2, 16));
-                m = fmaxf(m, __shfl_xor(m, 4, 16));
-                m = fmaxf(m, __shfl_xor(m, 8, 16));
-                const float scale = (m > 0.0f) ? (m / 448.0f) : 1.0f;
-                const float inv = 1.0f / scale;
-                uint2 pk;
-                pk.x = e4m3x4_from_f32(clamp448(v[0] * inv), clamp448(v[1] * inv),
-                                       clamp448(v[2] * inv), clamp448(v[3] * inv));
-                pk.y = e4m3x4_from_f32(clamp448(v[4] * inv), clamp448(v[5] * inv),
-                                       clamp448(v[6] * inv), clamp448(v[7] * inv));
-                *reinterpret_cast<uint2*>(qr + b * 128 + e0) = pk;
-                if ((lane & 15) == 0) sc[b][wave] = scale;
+            for (int p = 0; p < NP; ++p) load8(xr + (4 * p + g) * 128 + e0, v[p]);
+#pragma unroll
+            for (int p = 0; p < NP; ++p) block(4 * p + g, v[p], qr);
+        } else {
+            // the next pass's load is issued before this pass's conversion, so each
+            // wave keeps two 16-byte loads in flight
+            float v[8], vn[8];
+            if (g < nb) load8(xr + g * 128 + e0, v);
+            for (int b0 = 0; b0 < nb; b0 += 4) {
+                const int b = b0 + g;
+                if (b + 4 < nb) load8(xr + (b + 4) * 128 + e0, vn);
+                if (b < nb) block(b, v, qr);        // uniform inside each 16-lane group
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[i] = vn[i];
             }
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = vn[i];
         }
     }
     __syncthreads();
@@ -93,13 +105,17 @@ __global__ __launch_bounds__(64 * kQuantRows) void quantize_fp8_blockwise_kernel
 void launch_quantize_fp8_blockwise(const void* x, int x_dtype, int rows, int cols, uint8_t* q,
                                    float* scales, hipStream_t stream) {
     if (rows <= 0) return;
-    const dim3 grid((unsigned)((rows + kQuantRows - 1) / kQuantRows));
-    if (x_dtype == 1)
-        hipLaunchKernelGGL(quantize_fp8_blockwise_kernel<uint16_t>, grid, dim3(64 * kQuantRows), 0,
-                           stream, static_cast<const uint16_t*>(x), rows, cols, q, scales);
-    else
-        hipLaunchKernelGGL(quantize_fp8_blockwise_kernel<float>, grid, dim3(64 * kQuantRows), 0,
-                           stream, static_cast<const float*>(x), rows, cols, q, scales);
+    const dim3 grid((unsigned)((rows + kQuantRows - 1) / kQuantRows)), block(64 * kQuantRows);
+    const bool hidden = cols == kH;       // the operator's width: 14 passes of 512 columns
+    if (x_dtype == 1) {
+        const uint16_t* xb = static_cast<const uint16_t*>(x);
+        if (hidden) hipLaunchKernelGGL((quantize_fp8_blockwise_kernel<uint16_t, kH / 512>), grid, block, 0, stream, xb, rows, cols, q, scales);
+        else hipLaunchKernelGGL((quantize_fp8_blockwise_kernel<uint16_t, 0>), grid, block, 0, stream, xb, rows, cols, q, scales);
+    } else {
+        const float* xf = static_cast<const float*>(x);
+        if (hidden) hipLaunchKernelGGL((quantize_fp8_blockwise_kernel<float, kH / 512>), grid, block, 0, stream, xf, rows, cols, q, scales);
+        else hipLaunchKernelGGL((quantize_fp8_blockwise_kernel<float, 0>), grid, block, 0, stream, xf, rows, cols, q, scales);
+    }
 }
 
 }  // namespace moe
