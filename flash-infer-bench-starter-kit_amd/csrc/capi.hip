@@ -45,11 +45,12 @@ constexpr int kMinTileM = 16;           // smallest row tile; sizes the tile lis
 // Kernel plan per token count: the dispatch tile height and the GEMM1 / GEMM2 variants
 // (ids of launch_gemm1 / launch_gemm2).  Small T streams weights with the
 // register-staged kernels, C in bf16: 16-row tiles up to T = 192 (GEMM2 with 32 output
-// columns per wave up to T = 96, 64 beyond), 32-row tiles up to T = 896, where an
-// expert gets up to about 28 rows and streams its weights about once.  Large T uses
+// columns per wave up to T = 96, 64 beyond), 32-row tiles (GEMM1 with two column
+// groups per wave) up to T = 1152, where an expert gets up to about 36 rows and
+// streams its weights about once.  Large T uses
 // the MFMA-bound prefill kernels (128- or 256-row tiles, C in the fp8 hi/lo form; with
 // 256-row tiles GEMM2 walks the 128-row second tile list).  The boundaries come from
-// sweeps of every pair at T = 96 .. 1536 on MI355X.  MOE_MI355_G1 / MOE_MI355_G2
+// sweeps of every pair at T = 96 .. 2048 on MI355X.  MOE_MI355_G1 / MOE_MI355_G2
 // override the variants for tuning sweeps; the override is ignored unless both imply
 // the same tile height and the same form of C.
 struct Plan {
@@ -65,7 +66,7 @@ Plan choose_plan(int32_t T) {
     Plan p;
     if (T <= 96) p = {16, 1, 1};
     else if (T <= 192) p = {16, 1, 2};
-    else if (T <= 896) p = {32, 2, 3};
+    else if (T <= 1152) p = {32, 2, 3};
     else if (T <= 2048) p = {128, 3, 4};
     else p = {256, 4, 5};
     const char* e1 = getenv("MOE_MI355_G1");

@@ -64,9 +64,12 @@ __device__ __forceinline__ void store_swiglu4(uint16_t* __restrict__ inter, int 
 // in flight per CU (a streaming probe of this access pattern: 7.1 TB/s against
 // 6.3 TB/s for LDS-landed DMA).
 // A tile holds CB blocks of 16 token rows: every weight fragment feeds 2 CB MFMAs, so
-// an expert with up to 16 CB routed rows streams its weights once.
+// an expert with up to 16 CB routed rows streams its weights once.  An item covers
+// NGRP groups of 16 SwiGLU columns, so each token fragment a wave loads feeds NGRP
+// weight groups: token re-reads, which hit L2 but still take the CU's outstanding
+// request slots, fall from half of the requests (NGRP = 1, CB = 2) to a third.
 // ---------------------------------------------------------------------------
-template <int D, int CB>
+template <int D, int CB, int NGRP>
 __global__ __launch_bounds__(256) void gemm1_rstream_kernel(
     const uint8_t* __restrict__ hidden, const float* __restrict__ hs_scale, int T,
     const uint8_t* __restrict__ w1, const float* __restrict__ s1,
@@ -74,11 +77,13 @@ __global__ __launch_bounds__(256) void gemm1_rstream_kernel(
     const int* __restrict__ sorted_tok, uint16_t* __restrict__ inter) {
     constexpr int KSPLIT = 4;
     constexpr int KB = kHB / KSPLIT;                  // 14 K blocks per wave
-    constexpr int kItems = kI / 16;
-    constexpr int kVmPerKb = 4 + 3 * CB;              // 4 weight loads, per row block 2 token loads + 1 scale
+    constexpr int kItems = kI / (16 * NGRP);
+    constexpr int NW = 4 * NGRP;                      // weight loads per K block (8 rows each)
+    constexpr int kVmPerKb = NW + 3 * CB;             // per row block 2 token loads + 1 scale
     static_assert(D >= 2 && D <= 8 && (D - 1) * kVmPerKb < 64, "ring depth");
-    __shared__ __attribute__((aligned(1024))) uint8_t slot_lds[4][32 * kBlk];
-    __shared__ v4f red[4][2][CB][64];
+    static_assert(NGRP == 1 || NGRP == 2, "column groups per item");
+    __shared__ __attribute__((aligned(1024))) uint8_t slot_lds[4][32 * NGRP * kBlk];
+    __shared__ v4f red[4][2][NGRP * CB][64];
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -91,11 +96,9 @@ __global__ __launch_bounds__(256) void gemm1_rstream_kernel(
     const int swz = swz128(r16);
     const int rd_g0 = r16 * kBlk + (((2 * kq) ^ swz) << 4);
     const int rd_g1 = r16 * kBlk + (((2 * kq + 1) ^ swz) << 4);
-    const int rd_u0 = rd_g0 + 16 * kBlk;
-    const int rd_u1 = rd_g1 + 16 * kBlk;
-    int wr[4];                                         // LDS position of this lane's chunk
+    int wr[NW];                                        // LDS position of this lane's chunk
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < NW; ++i) {
         const int r = 8 * i + drow;
         wr[i] = r * kBlk + ((dchunk ^ swz128(r)) << 4);
     }
@@ -103,7 +106,7 @@ __global__ __launch_bounds__(256) void gemm1_rstream_kernel(
 
     for (int work = blockIdx.x; work < nwork; work += gridDim.x) {
         const int4 tile = tiles[work / kItems];
-        const int ng = work % kItems;
+        const int ng = (work % kItems) * NGRP;         // first 16-column group
         const int le = tile.x, row0 = tile.y, nrows = tile.z;
         const uint8_t* ap[CB];
         const float* sp[CB];
@@ -113,23 +116,26 @@ __global__ __launch_bounds__(256) void gemm1_rstream_kernel(
             ap[c] = hidden + (size_t)tok * kH + kq * 32;
             sp[c] = hs_scale + tok;
         }
-        const uint8_t* wsrc[4];
+        // slot rows 32 gi + 0..15: gate rows of group ng + gi, 32 gi + 16..31: its up rows
+        const uint8_t* wsrc[NW];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < NW; ++i) {
             const int r = 8 * i + drow;
-            const int n = (r < 16) ? ng * 16 + r : kI + ng * 16 + (r - 16);
+            const int gi = r >> 5, rr = r & 31;
+            const int n = (rr < 16) ? (ng + gi) * 16 + rr : kI + (ng + gi) * 16 + (rr - 16);
             wsrc[i] = w1 + (size_t)(le * kN1 + n) * kH + dchunk * 16;
         }
+        // the NGRP groups lie in one 128-column scale block (16 NGRP divides 128)
         const float* sg = s1 + (size_t)(le * kN1B + (ng >> 3)) * kHB;
         const float* su = sg + (size_t)kIB * kHB;
 
-        v4u bw[D][4];
+        v4u bw[D][NW];
         v8i ba[D][CB];
         float bs[D][CB];
         auto issue = [&](int k) {
             const int kb = kb0 + k;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) bw[k % D][i] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(wsrc[i] + kb * kBlk));
+            for (int i = 0; i < NW; ++i) bw[k % D][i] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(wsrc[i] + kb * kBlk));
 #pragma unroll
             for (int c = 0; c < CB; ++c) {
                 ba[k % D][c] = load_v8i(ap[c] + kb * kBlk);
@@ -141,9 +147,11 @@ __global__ __launch_bounds__(256) void gemm1_rstream_kernel(
             issue(k);
             __builtin_amdgcn_sched_barrier(0);
         }
-        v4f ag[CB], au[CB];
+        v4f ag[NGRP][CB], au[NGRP][CB];
 #pragma unroll
-        for (int c = 0; c < CB; ++c) ag[c] = au[c] = zero;
+        for (int gi = 0; gi < NGRP; ++gi)
+#pragma unroll
+            for (int c = 0; c < CB; ++c) ag[gi][c] = au[gi][c] = zero;
 #pragma unroll
         for (int k = 0; k < KB; ++k) {
             if (k + D - 1 < KB) issue(k + D - 1);
@@ -161,46 +169,55 @@ __global__ __launch_bounds__(256) void gemm1_rstream_kernel(
             }
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) *reinterpret_cast<v4u*>(slot + wr[i]) = bw[k % D][i];
-            const v4u g0 = *reinterpret_cast<const v4u*>(slot + rd_g0);
-            const v4u g1 = *reinterpret_cast<const v4u*>(slot + rd_g1);
-            const v4u u0 = *reinterpret_cast<const v4u*>(slot + rd_u0);
-            const v4u u1 = *reinterpret_cast<const v4u*>(slot + rd_u1);
-            const v8i bg = {(int)g0[0], (int)g0[1], (int)g0[2], (int)g0[3], (int)g1[0], (int)g1[1], (int)g1[2], (int)g1[3]};
-            const v8i bu = {(int)u0[0], (int)u0[1], (int)u0[2], (int)u0[3], (int)u1[0], (int)u1[1], (int)u1[2], (int)u1[3]};
+            for (int i = 0; i < NW; ++i) *reinterpret_cast<v4u*>(slot + wr[i]) = bw[k % D][i];
             const int kb = kb0 + k;
             const float wg = sg[kb], wu = su[kb];
 #pragma unroll
-            for (int c = 0; c < CB; ++c) {
-                const float fg = bs[k % D][c] * wg, fu = bs[k % D][c] * wu;
-                const v4f tg = mfma_fp8(bg, ba[k % D][c], zero);
-                const v4f tu = mfma_fp8(bu, ba[k % D][c], zero);
+            for (int gi = 0; gi < NGRP; ++gi) {
+                const uint8_t* gs = slot + gi * 32 * kBlk;
+                const v4u g0 = *reinterpret_cast<const v4u*>(gs + rd_g0);
+                const v4u g1 = *reinterpret_cast<const v4u*>(gs + rd_g1);
+                const v4u u0 = *reinterpret_cast<const v4u*>(gs + 16 * kBlk + rd_g0);
+                const v4u u1 = *reinterpret_cast<const v4u*>(gs + 16 * kBlk + rd_g1);
+                const v8i bg = {(int)g0[0], (int)g0[1], (int)g0[2], (int)g0[3], (int)g1[0], (int)g1[1], (int)g1[2], (int)g1[3]};
+                const v8i bu = {(int)u0[0], (int)u0[1], (int)u0[2], (int)u0[3], (int)u1[0], (int)u1[1], (int)u1[2], (int)u1[3]};
 #pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    ag[c][v] = __builtin_fmaf(tg[v], fg, ag[c][v]);
-                    au[c][v] = __builtin_fmaf(tu[v], fu, au[c][v]);
+                for (int c = 0; c < CB; ++c) {
+                    const float fg = bs[k % D][c] * wg, fu = bs[k % D][c] * wu;
+                    const v4f tg = mfma_fp8(bg, ba[k % D][c], zero);
+                    const v4f tu = mfma_fp8(bu, ba[k % D][c], zero);
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        ag[gi][c][v] = __builtin_fmaf(tg[v], fg, ag[gi][c][v]);
+                        au[gi][c][v] = __builtin_fmaf(tu[v], fu, au[gi][c][v]);
+                    }
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
         }
 
 #pragma unroll
-        for (int c = 0; c < CB; ++c) {
-            red[wave][0][c][lane] = ag[c];
-            red[wave][1][c][lane] = au[c];
-        }
+        for (int gi = 0; gi < NGRP; ++gi)
+#pragma unroll
+            for (int c = 0; c < CB; ++c) {
+                red[wave][0][gi * CB + c][lane] = ag[gi][c];
+                red[wave][1][gi * CB + c][lane] = au[gi][c];
+            }
         __syncthreads();
         if (wave == 0) {
 #pragma unroll
-            for (int c = 0; c < CB; ++c) {
-                v4f g = red[0][0][c][lane], u = red[0][1][c][lane];
+            for (int gi = 0; gi < NGRP; ++gi)
 #pragma unroll
-                for (int q = 1; q < KSPLIT; ++q) {
-                    g += red[q][0][c][lane];
-                    u += red[q][1][c][lane];
+                for (int c = 0; c < CB; ++c) {
+                    v4f g = red[0][0][gi * CB + c][lane], u = red[0][1][gi * CB + c][lane];
+#pragma unroll
+                    for (int q = 1; q < KSPLIT; ++q) {
+                        g += red[q][0][gi * CB + c][lane];
+                        u += red[q][1][gi * CB + c][lane];
+                    }
+                    if (16 * c + r16 < nrows)
+                        store_swiglu4(inter, row0 + 16 * c + r16, (ng + gi) * 16 + kq * 4, g, u);
                 }
-                if (16 * c + r16 < nrows) store_swiglu4(inter, row0 + 16 * c + r16, ng * 16 + kq * 4, g, u);
-            }
         }
         __syncthreads();
     }
@@ -577,7 +594,7 @@ static int grid_for(long long work) { return (int)(work < 4096 ? work : 4096); }
 
 // Variants (the tile height of the dispatch they expect, and the form of C they write):
 //   1  register-staged streaming, 1 row block per item    16-row tiles   bf16
-//   2  register-staged streaming, 2 row blocks per item   32-row tiles   bf16
+//   2  register-staged, 2 row blocks x 2 column groups   32-row tiles   bf16
 //   3  prefill, 4 waves, 128 x 256 workgroup tile        128-row tiles  fp8 hi/lo
 //   4  prefill, 8 waves, 256 x 256 workgroup tile        256-row tiles  fp8 hi/lo
 bool launch_gemm1(int variant, const uint8_t* hidden, const float* hs_scale, int T,
@@ -590,11 +607,11 @@ bool launch_gemm1(int variant, const uint8_t* hidden, const float* hs_scale, int
     const long long mt = max_tiles;
     switch (variant) {
         case 1:
-            hipLaunchKernelGGL((gemm1_rstream_kernel<4, 1>), dim3(grid_for(mt * G)), dim3(256), 0, stream,
+            hipLaunchKernelGGL((gemm1_rstream_kernel<4, 1, 1>), dim3(grid_for(mt * G)), dim3(256), 0, stream,
                                hidden, hs_scale, T, w1, s1, tiles, num_tiles, sorted_tok, inter);
             return true;
         case 2:
-            hipLaunchKernelGGL((gemm1_rstream_kernel<4, 2>), dim3(grid_for(mt * G)), dim3(256), 0, stream,
+            hipLaunchKernelGGL((gemm1_rstream_kernel<3, 2, 2>), dim3(grid_for(mt * G / 2)), dim3(256), 0, stream,
                                hidden, hs_scale, T, w1, s1, tiles, num_tiles, sorted_tok, inter);
             return true;
         case 3:

@@ -28,6 +28,16 @@ def config_inputs(idx: int) -> dict:
     return d
 
 
+def first_tokens(d0: dict, T: int) -> dict:
+    """The first T tokens of a config's inputs (same weights)."""
+    d = dict(d0)
+    d["routing_logits"] = d0["routing_logits"][:T].contiguous()
+    d["hidden_states"] = d0["hidden_states"][:T].contiguous()
+    d["hidden_states_scale"] = d0["hidden_states_scale"][:, :T].contiguous()
+    d["output"] = torch.empty(T, d0["output"].shape[1], dtype=torch.bfloat16, device="cuda")
+    return d
+
+
 def run_forward(d: dict, **kw) -> torch.Tensor:
     k = pkg("kernel")
     wl = pkg("workloads")

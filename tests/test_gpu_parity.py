@@ -13,7 +13,7 @@ import pytest
 import torch
 
 from conftest import oracle, pkg
-from gpu_common import ATOL, RTOL, compare_to_oracle, config_inputs, note, run_forward
+from gpu_common import ATOL, RTOL, compare_to_oracle, config_inputs, first_tokens, note, run_forward
 
 pytestmark = pytest.mark.gpu
 
@@ -151,28 +151,27 @@ def test_forward_routing_in_workspace_is_bit_exact():
     assert np.array_equal(stok, r["sorted_tok"])
 
 
-@pytest.mark.parametrize("idx", [2, 3])
-def test_prefill_intermediate_hilo_rows(idx):
-    """The prefill GEMM1 writes C in the fp8 hi/lo form; rebuilt rows match the fp32
-    SwiGLU of the oracle to within the form's precision (2^-8 relative, plus the
-    fp32 GEMM's own rounding)."""
+@pytest.mark.parametrize("T", [1500, 8192])
+def test_prefill_intermediate_hilo_rows(T):
+    """The prefill GEMM1 kernels (128-row tiles at T=1500, 256-row tiles at T=8192)
+    write C in the fp8 hi/lo form; rebuilt rows match the fp32 SwiGLU of the oracle to
+    within the form's precision (2^-8 relative, plus the fp32 GEMM's own rounding)."""
     k = pkg("kernel")
     o = oracle()
     wl = pkg("workloads")
-    d = config_inputs(idx)
-    T = d["routing_logits"].shape[0]
+    d = first_tokens(config_inputs(3), T)
     lay = k.workspace_layout(T)
     assert lay.intermediate_format == 1
     ws = torch.empty(lay.total, dtype=torch.uint8, device="cuda")
     out = torch.empty_like(d["output"])
-    note(f"[gpu] hi/lo intermediate config {idx}")
+    note(f"[gpu] hi/lo intermediate T={T}")
     k.forward(*wl.as_args({**d, "output": out}), workspace=ws)
     torch.cuda.synchronize()
     R = T * 8
     exp_off = ws[lay.meta:lay.meta + 33 * 4].view(torch.int32).cpu().numpy()
     na = int(exp_off[32])
     stok = ws[lay.sorted_tokens:lay.sorted_tokens + na * 4].view(torch.int32).cpu().numpy()
-    rng = np.random.default_rng(7 + idx)
+    rng = np.random.default_rng(7 + T)
     rows = sorted(rng.choice(na, 24, replace=False).tolist())
     ridx = torch.as_tensor(rows, device="cuda", dtype=torch.int64)
     hi = ws[lay.intermediate:lay.intermediate + R * 2048].view(R, 2048)[ridx].cpu()

@@ -14,7 +14,7 @@ import pytest
 import torch
 
 from conftest import oracle, pkg
-from gpu_common import compare_to_oracle, config_inputs, note, run_forward
+from gpu_common import compare_to_oracle, config_inputs, first_tokens, note, run_forward
 
 pytestmark = pytest.mark.gpu
 
@@ -107,22 +107,12 @@ def test_small_odd_batches(T):
     assert st["frac_within"] == 1.0, st
 
 
-def _first_tokens(d0: dict, T: int) -> dict:
-    """The first T tokens of a config's inputs (same weights)."""
-    d = dict(d0)
-    d["routing_logits"] = d0["routing_logits"][:T].contiguous()
-    d["hidden_states"] = d0["hidden_states"][:T].contiguous()
-    d["hidden_states_scale"] = d0["hidden_states_scale"][:, :T].contiguous()
-    d["output"] = torch.empty(T, 7168, dtype=torch.bfloat16, device="cuda")
-    return d
-
-
-@pytest.mark.parametrize("T", [96, 97, 192, 193, 896, 897, 2048, 2049])
+@pytest.mark.parametrize("T", [96, 97, 192, 193, 1152, 1153, 2048, 2049])
 def test_plan_boundaries_match_oracle(T):
     """Token counts on both sides of every change of kernel plan (16-row streaming
     with 32 then 64 GEMM2 columns per wave, 32-row streaming, 128-row and 256-row
     prefill tiles)."""
-    d = _first_tokens(config_inputs(3), T)
+    d = first_tokens(config_inputs(3), T)
     note(f"[gpu] plan boundary T={T}")
     out = run_forward(d)
     rng = np.random.default_rng(T)
@@ -137,7 +127,7 @@ def test_plan_boundaries_match_oracle(T):
 def test_every_gemm_variant_matches_oracle(T, g1, g2, monkeypatch):
     """Each GEMM1 / GEMM2 kernel variant (forced with MOE_MI355_G1 / _G2, which the
     library reads on every call) stays within the tolerance."""
-    d = _first_tokens(config_inputs(3), T)
+    d = first_tokens(config_inputs(3), T)
     monkeypatch.setenv("MOE_MI355_G1", str(g1))
     monkeypatch.setenv("MOE_MI355_G2", str(g2))
     note(f"[gpu] variants g1={g1} g2={g2} T={T}")
