@@ -9,7 +9,8 @@
 //
 // Rows of one token are visited in ascending row index, which is ascending local
 // expert because the permutation is expert-major.  Tokens with no local expert get
-// +0.0.  One thread produces 8 consecutive outputs (one 16-byte store).
+// +0.0.  One thread produces 8 consecutive outputs (one 16-byte store), with the loads
+// of all the token's rows in flight together.
 
 #include "moe_device.h"
 
@@ -47,29 +48,52 @@ __global__ __launch_bounds__(128) void combine_kernel(const float* __restrict__ 
     cswap(r[2], r[4]); cswap(r[3], r[5]);
     cswap(r[3], r[4]);
 
-    float acc[8];
+    // the valid rows are a prefix r[0 .. nr); a kernel body per row count issues every
+    // row load of the token before the first add, then adds in ascending row order
+    int nr = 0;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+    for (int k = 0; k < kTopK; ++k) nr += (r[k] != 0x7fffffff) ? 1 : 0;
+    auto body = [&](auto rows) {
+        constexpr int N = decltype(rows)::value;
+        float acc[8];
 #pragma unroll
-    for (int k = 0; k < kTopK; ++k) {
-        if (r[k] != 0x7fffffff) {
-            const float w = sorted_w[r[k]];
+        for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+        float4 a[N > 0 ? N : 1], b[N > 0 ? N : 1];
+        float w[N > 0 ? N : 1];
+#pragma unroll
+        for (int k = 0; k < N; ++k) {
             const float4* p = reinterpret_cast<const float4*>(rows_out + (size_t)r[k] * kH + h0);
-            const float4 a = p[0], b = p[1];
-            const float o[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            a[k] = p[0];
+            b[k] = p[1];
+            w[k] = sorted_w[r[k]];
+        }
+#pragma unroll
+        for (int k = 0; k < N; ++k) {
+            const float o[8] = {a[k].x, a[k].y, a[k].z, a[k].w, b[k].x, b[k].y, b[k].z, b[k].w};
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float prod = o[j] * w;
+                const float prod = o[j] * w[k];
                 acc[j] = acc[j] + prod;
             }
         }
+        uint4 pk;
+        pk.x = f32_to_bf16_bits(acc[0]) | (f32_to_bf16_bits(acc[1]) << 16);
+        pk.y = f32_to_bf16_bits(acc[2]) | (f32_to_bf16_bits(acc[3]) << 16);
+        pk.z = f32_to_bf16_bits(acc[4]) | (f32_to_bf16_bits(acc[5]) << 16);
+        pk.w = f32_to_bf16_bits(acc[6]) | (f32_to_bf16_bits(acc[7]) << 16);
+        *reinterpret_cast<uint4*>(out + (size_t)t * kH + h0) = pk;
+    };
+    switch (nr) {    // uniform per workgroup (one token)
+        case 0: body(IntC<0>{}); break;
+        case 1: body(IntC<1>{}); break;
+        case 2: body(IntC<2>{}); break;
+        case 3: body(IntC<3>{}); break;
+        case 4: body(IntC<4>{}); break;
+        case 5: body(IntC<5>{}); break;
+        case 6: body(IntC<6>{}); break;
+        case 7: body(IntC<7>{}); break;
+        default: body(IntC<8>{}); break;
     }
-    uint4 pk;
-    pk.x = f32_to_bf16_bits(acc[0]) | (f32_to_bf16_bits(acc[1]) << 16);
-    pk.y = f32_to_bf16_bits(acc[2]) | (f32_to_bf16_bits(acc[3]) << 16);
-    pk.z = f32_to_bf16_bits(acc[4]) | (f32_to_bf16_bits(acc[5]) << 16);
-    pk.w = f32_to_bf16_bits(acc[6]) | (f32_to_bf16_bits(acc[7]) << 16);
-    *reinterpret_cast<uint4*>(out + (size_t)t * kH + h0) = pk;
 }
 
 void launch_combine(const float* rows_out, const float* sorted_w, const int* inv, int T,
