@@ -131,24 +131,40 @@ def test_forward_matches_oracle(idx):
     assert st["frac_within"] == 1.0, st
 
 
-def test_forward_routing_in_workspace_is_bit_exact():
+@pytest.mark.parametrize("T", [1, 8, 13, 16, 17, 1024])
+def test_forward_routing_in_workspace_is_bit_exact(T):
+    """The routing and dispatch a forward call leaves in its workspace (ids, weights,
+    expert offsets, tile list, permutation, inverse map) equal the oracle's bit for
+    bit (config 1 sliced to T, config 2 at its full 1024 tokens)."""
     k = pkg("kernel")
-    d = config_inputs(2)
-    T = d["routing_logits"].shape[0]
+    d = config_inputs(2) if T == 1024 else first_tokens(config_inputs(1), T)
     lay = k.workspace_layout(T)
     ws = torch.empty(lay.total, dtype=torch.uint8, device="cuda")
     wl = pkg("workloads")
     out = torch.empty_like(d["output"])
+    note(f"[gpu] workspace routing / dispatch T={T}")
     k.forward(*wl.as_args({**d, "output": out}), workspace=ws)
     torch.cuda.synchronize()
-    ids = ws[lay.topk_ids:lay.topk_ids + T * 32].view(torch.int32).view(T, 8).cpu().numpy()
+
+    def arr(off, n, dt):
+        return ws[off:off + n * 4].view(dt).cpu().numpy()
+
     o = oracle()
     rids, rw = o.route(d["routing_logits"], d["routing_bias"], d["routed_scaling_factor"])
-    assert np.array_equal(ids, rids)
+    assert np.array_equal(arr(lay.topk_ids, T * 8, torch.int32).reshape(T, 8), rids)
+    assert np.array_equal(arr(lay.topk_weights, T * 8, torch.float32).reshape(T, 8).view(np.uint32),
+                          np.asarray(rw, np.float32).view(np.uint32))
     r = o.dispatch(rids, rw, d["local_expert_offset"], lay.tile_m)
+    meta = arr(lay.meta, 34, torch.int32)
+    assert np.array_equal(meta[:33], r["exp_off"])
+    nt = r["tiles"].shape[0]
+    assert meta[33] == nt
+    assert np.array_equal(arr(lay.tiles, nt * 4, torch.int32).reshape(nt, 4), r["tiles"])
     na = int(r["exp_off"][-1])
-    stok = ws[lay.sorted_tokens:lay.sorted_tokens + na * 4].view(torch.int32).cpu().numpy()
-    assert np.array_equal(stok, r["sorted_tok"])
+    assert np.array_equal(arr(lay.sorted_tokens, na, torch.int32), r["sorted_tok"])
+    assert np.array_equal(arr(lay.sorted_weights, na, torch.float32).view(np.uint32),
+                          np.asarray(r["sorted_w"], np.float32).view(np.uint32))
+    assert np.array_equal(arr(lay.inverse_rows, T * 8, torch.int32).reshape(T, 8), r["inv"])
 
 
 @pytest.mark.parametrize("T", [1500, 8192])
