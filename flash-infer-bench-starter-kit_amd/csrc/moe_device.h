@@ -169,7 +169,7 @@ __device__ __forceinline__ void bdma4(__amdgpu_buffer_rsrc_t r, uint32_t voff, u
 
 // The SwiGLU rows C [rows, 2048] between GEMM1 and GEMM2 live in one workspace
 // region in one of two forms, chosen by the kernel plan:
-//   bf16: C as bf16 rows (decode kernels);
+//   bf16: C as bf16 rows (streaming kernels, 16- and 32-row tiles);
 //   fp8 hi/lo: per row and 128-column block b a scale s = amax/448 and two e4m3
 //     rows hi = e4m3(C/s), lo = e4m3((C - hi*s) * 16/s), so C ~ s*(hi + lo/16)
 //     with about 8 significant bits (prefill kernels; GEMM2 then runs two FP8
