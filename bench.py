@@ -210,8 +210,8 @@ def main() -> int:
     per_kernel = {
         "gemm1": dict(bytes=e_a * (4096 * 7168 + 32 * 56 * 4) + touched * (7168 + 56 * 4) + n_a * 2048 * 2,
                       flops=n_a * 2 * 7168 * 4096, peak_tflops=FP8_PEAK_TFLOPS),
-        # GEMM2 runs bf16 MFMA (decode) or two FP8 MFMAs per product (prefill hi/lo):
-        # either way its MFMA ceiling on the algorithmic flops is the bf16 rate
+        # GEMM2 runs fp16 MFMA (streaming) or two FP8 MFMAs per product (prefill hi/lo):
+        # either way its MFMA ceiling on the algorithmic flops is the 16-bit rate
         "gemm2": dict(bytes=e_a * (7168 * 2048 + 56 * 16 * 4) + n_a * 2048 * 2 + n_a * 7168 * 4,
                       flops=n_a * 2 * 2048 * 7168, peak_tflops=BF16_PEAK_TFLOPS),
         "combine": dict(bytes=n_a * 7168 * 4 + T * 7168 * 2 + T * 8 * 4 + n_a * 4, flops=0,
@@ -279,7 +279,7 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": ("fp8_e4m3 GEMM1 + fp8 hi/lo GEMM2 (two FP8 MFMAs per product), fp32 accumulate"
                   if k.workspace_layout(T).intermediate_format == 1 else
-                  "fp8_e4m3 GEMM1 + bf16 GEMM2, fp32 accumulate"),
+                  "fp8_e4m3 GEMM1 + fp16 GEMM2 (W2 widened exactly), fp32 accumulate"),
         "data": "synthetic (seeded N(0,1) logits/hidden, N(0,0.02) weights, block-quantised)",
         "config": {"workload": cfg.name, "T": T, "local_expert_offset": cfg.local_expert_offset,
                    "routed_scaling_factor": cfg.routed_scaling_factor,

@@ -21,7 +21,7 @@
 #include "moe_mi355.h"
 
 namespace moe {
-void launch_route(const float*, const uint16_t*, int, float, int*, float*, hipStream_t);
+void launch_route(const float*, const uint16_t*, int, float, int*, float*, int*, hipStream_t);
 bool launch_dispatch(const int*, const float*, int, int, int, int*, int*, int4*, int*, float*,
                      int*, int*, hipStream_t, int*, int4*);
 int dispatch_max_tiles(int T, int tm);
@@ -32,6 +32,7 @@ bool launch_gemm2(int, const Intermediate&, const uint8_t*, const float*, const 
                   const int*, int, float*, hipStream_t);
 void launch_combine(const float*, const float*, const int*, int, uint16_t*, hipStream_t);
 void launch_e4m3_to_bf16(const uint8_t*, uint16_t*, int, hipStream_t);
+void launch_e4m3_to_f16(const uint8_t*, uint16_t*, int, hipStream_t);
 void launch_quantize_fp8_blockwise(const void*, int, int, int, uint8_t*, float*, hipStream_t);
 }  // namespace moe
 
@@ -44,7 +45,7 @@ constexpr int kMinTileM = 16;           // smallest row tile; sizes the tile lis
 
 // Kernel plan per token count: the dispatch tile height and the GEMM1 / GEMM2 variants
 // (ids of launch_gemm1 / launch_gemm2).  Small T streams weights with the
-// register-staged kernels, C in bf16: 16-row tiles up to T = 192 (GEMM2 with 32 output
+// register-staged kernels, C in fp16: 16-row tiles up to T = 192 (GEMM2 with 32 output
 // columns per wave up to T = 96, 64 beyond), 32-row tiles (GEMM1 with two column
 // groups per wave) up to T = 1152, where an expert gets up to about 36 rows and
 // streams its weights about once.  Large T uses
@@ -101,7 +102,7 @@ bool fill_layout(int32_t T, moe_mi355_workspace_layout* L) {
     L->sorted_tokens = take(R * 4);
     L->sorted_weights = take(R * 4);
     L->chunk_counts = take((size_t)((T + 255) / 256) * moe::kEL * 4);
-    L->intermediate = take(R * moe::kI * 2);
+    L->intermediate = take(R * moe::kI * 4);
     L->intermediate_scales = take(R * moe::kIB * 4);
     L->expert_out = take(R * moe::kH * 4);
     L->total = off;
@@ -185,7 +186,7 @@ int moe_mi355_route(const float* routing_logits, const uint16_t* routing_bias, i
     if (!aligned16(routing_logits) || ((uintptr_t)routing_bias & 7u)) return MOE_ERR_MISALIGNED;
     hipStream_t s = (hipStream_t)stream;
     moe::launch_route(routing_logits, routing_bias, T, (float)routed_scaling_factor, topk_ids,
-                      topk_weights, s);
+                      topk_weights, nullptr, s);
     return hip_status(hipGetLastError());
 }
 
@@ -259,7 +260,7 @@ int moe_mi355_forward(const moe_mi355_args* a, void* stream) {
 
     if (prof) prof_record(slot, 0, s);
     moe::launch_route(a->routing_logits, a->routing_bias, T, (float)a->routed_scaling_factor, ids,
-                      wts, s);
+                      wts, meta + moe::kCWideFlag, s);
     if (prof) prof_record(slot, 1, s);
     const Plan plan = choose_plan(T);
     const int max_tiles = moe::dispatch_max_tiles(T, plan.tm);
@@ -341,6 +342,13 @@ int moe_mi355_debug_e4m3_to_bf16(const uint8_t* in, uint16_t* out, int32_t n, vo
     if (!in || !out) return MOE_ERR_NULL_POINTER;
     if (n < 0 || (n & 3)) return MOE_ERR_BAD_SIZE;
     moe::launch_e4m3_to_bf16(in, out, n, (hipStream_t)stream);
+    return hip_status(hipGetLastError());
+}
+
+int moe_mi355_debug_e4m3_to_f16(const uint8_t* in, uint16_t* out, int32_t n, void* stream) {
+    if (!in || !out) return MOE_ERR_NULL_POINTER;
+    if (n < 0 || (n & 3)) return MOE_ERR_BAD_SIZE;
+    moe::launch_e4m3_to_f16(in, out, n, (hipStream_t)stream);
     return hip_status(hipGetLastError());
 }
 

@@ -5,8 +5,9 @@
 // mainloop):
 //   G1[r, n] = sum_kb sa[kb, tok(r)] * sb[e, n/128, kb] * sum_{k in kb} A[tok(r), k] W1[e, n, k]
 //   C[r, i]  = silu(G1[r, 2048 + i]) * G1[r, i]        (kernel.cu:1104-1108 convention)
-// C is written as one row per routed assignment for GEMM2: bf16 by the decode
-// kernels, the fp8 hi/lo form (moe_device.h, Intermediate) by the prefill kernels.
+// C is written as one row per routed assignment for GEMM2: fp16 plus a bf16 copy by
+// the streaming kernels, the fp8 hi/lo form by the prefill kernels (moe_device.h,
+// Intermediate).
 //
 // Kernels: register-staged weight streaming for small T (a work item is one row tile
 // of 16 or 32 rows x 16 gate + 16 up rows, its 56 K blocks split over the 4 waves of
@@ -40,15 +41,30 @@ __device__ __forceinline__ v4f mfma_fp8(const v8i& a, const v8i& b, const v4f& c
 
 __device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
 
-__device__ __forceinline__ void store_swiglu4(uint16_t* __restrict__ inter, int row, int n0,
-                                              const v4f& g, const v4f& u) {
+// Four SwiGLU values of row `row`, columns n0..n0+3 in fp16 (round to nearest even).
+// When one of them lies beyond the fp16 range, the four also go to the bf16 region and
+// the flag word is raised; GEMM2 then takes the bf16 value wherever the fp16 one is
+// infinite.  (Writing the bf16 copy on every call costs ~10 us at T = 1024.)
+__device__ __forceinline__ void store_swiglu4(const Intermediate& C, int* __restrict__ c_wide, int row,
+                                              int n0, const v4f& g, const v4f& u) {
+    float c[4];
     uint32_t h[4];
+    bool wide = false;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) h[v] = f32_to_bf16_bits(silu_f32(u[v]) * g[v]);
-    uint2 pk;
-    pk.x = h[0] | (h[1] << 16);
-    pk.y = h[2] | (h[3] << 16);
-    *reinterpret_cast<uint2*>(inter + (size_t)row * kI + n0) = pk;
+    for (int v = 0; v < 4; ++v) {
+        c[v] = silu_f32(u[v]) * g[v];
+        h[v] = __builtin_bit_cast(uint16_t, (_Float16)c[v]);
+        wide = wide || fabsf(c[v]) > kF16Max;
+    }
+    const size_t off = (size_t)row * kI + n0;
+    *reinterpret_cast<uint2*>(C.f16() + off) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+    if (wide) {
+        uint32_t b[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) b[v] = f32_to_bf16_bits(c[v]);
+        *reinterpret_cast<uint2*>(C.bf16() + off) = make_uint2(b[0] | (b[1] << 16), b[2] | (b[3] << 16));
+        *c_wide = 1;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -74,7 +90,7 @@ __global__ __launch_bounds__(256) void gemm1_rstream_kernel(
     const uint8_t* __restrict__ hidden, const float* __restrict__ hs_scale, int T,
     const uint8_t* __restrict__ w1, const float* __restrict__ s1,
     const int4* __restrict__ tiles, const int* __restrict__ num_tiles,
-    const int* __restrict__ sorted_tok, uint16_t* __restrict__ inter) {
+    const int* __restrict__ sorted_tok, Intermediate C, int* __restrict__ c_wide) {
     constexpr int KSPLIT = 4;
     constexpr int KB = kHB / KSPLIT;                  // 14 K blocks per wave
     constexpr int kItems = kI / (16 * NGRP);
@@ -216,7 +232,7 @@ __global__ __launch_bounds__(256) void gemm1_rstream_kernel(
                         u += red[q][1][gi * CB + c][lane];
                     }
                     if (16 * c + r16 < nrows)
-                        store_swiglu4(inter, row0 + 16 * c + r16, (ng + gi) * 16 + kq * 4, g, u);
+                        store_swiglu4(C, c_wide, row0 + 16 * c + r16, (ng + gi) * 16 + kq * 4, g, u);
                 }
         }
         __syncthreads();
@@ -593,26 +609,26 @@ __global__ __launch_bounds__(512, 1) void gemm1_prefill8_kernel(
 static int grid_for(long long work) { return (int)(work < 4096 ? work : 4096); }
 
 // Variants (the tile height of the dispatch they expect, and the form of C they write):
-//   1  register-staged streaming, 1 row block per item    16-row tiles   bf16
-//   2  register-staged, 2 row blocks x 2 column groups   32-row tiles   bf16
+//   1  register-staged streaming, 1 row block per item    16-row tiles   fp16 + bf16
+//   2  register-staged, 2 row blocks x 2 column groups   32-row tiles   fp16 + bf16
 //   3  prefill, 4 waves, 128 x 256 workgroup tile        128-row tiles  fp8 hi/lo
 //   4  prefill, 8 waves, 256 x 256 workgroup tile        256-row tiles  fp8 hi/lo
 bool launch_gemm1(int variant, const uint8_t* hidden, const float* hs_scale, int T,
                   const uint8_t* w1, const float* s1, const int4* tiles, const int* num_tiles,
                   const int* exp_off, int max_tiles, const int* sorted_tok, const Intermediate& C,
                   hipStream_t stream) {
-    uint16_t* inter = C.bf16();
+    int* c_wide = const_cast<int*>(exp_off) + kCWideFlag;   // meta word, cleared by the route kernel
     const int prefill_grid = 256;   // one resident workgroup per CU (LDS-bound)
     constexpr int G = kI / 16;      // 16-column groups
     const long long mt = max_tiles;
     switch (variant) {
         case 1:
             hipLaunchKernelGGL((gemm1_rstream_kernel<4, 1, 1>), dim3(grid_for(mt * G)), dim3(256), 0, stream,
-                               hidden, hs_scale, T, w1, s1, tiles, num_tiles, sorted_tok, inter);
+                               hidden, hs_scale, T, w1, s1, tiles, num_tiles, sorted_tok, C, c_wide);
             return true;
         case 2:
             hipLaunchKernelGGL((gemm1_rstream_kernel<3, 2, 2>), dim3(grid_for(mt * G / 2)), dim3(256), 0, stream,
-                               hidden, hs_scale, T, w1, s1, tiles, num_tiles, sorted_tok, inter);
+                               hidden, hs_scale, T, w1, s1, tiles, num_tiles, sorted_tok, C, c_wide);
             return true;
         case 3:
             hipLaunchKernelGGL(gemm1_prefill_kernel<3>, dim3(prefill_grid), dim3(256), 0, stream,

@@ -1,4 +1,4 @@
-// gemm2.hip -- grouped GEMM2 (2048 -> 7168): bf16 MFMA for the streaming kernels, FP8
+// gemm2.hip -- grouped GEMM2 (2048 -> 7168): fp16 MFMA for the streaming kernels, FP8
 // MFMA on the hi/lo form of C for the prefill kernel.
 //
 // Semantics: reference solution/cuda/moe.cu:231 (O = C @ W2[e]^T) with the 128x128
@@ -6,9 +6,11 @@
 // (the reference's CUTLASS path applies them in its mainloop,
 // moe_grouped_gemm_fp8.cu:274-322):
 //   O[r, h] = sum_kb sb2[e, h/128, kb] * sum_{i in kb} C[r, i] * W2[e, h, i]
-// Streaming kernels: C is the bf16 SwiGLU output of GEMM1; W2 e4m3 bytes are widened to
-// bf16 in registers (exact: every e4m3 value is a bf16 value) for
-// v_mfma_f32_16x16x32_bf16, operand A = 16 W2 rows, operand B = 16 C rows; lane l
+// Streaming kernels: C is the fp16 SwiGLU output of GEMM1; when GEMM1 flagged a value
+// beyond the fp16 range, C runs through bf16 instead, with the bf16 copy GEMM1 wrote
+// for exactly those values.  W2 e4m3 bytes are widened in registers to the same type
+// (exact: every e4m3 value is an fp16 and a bf16 value) for
+// v_mfma_f32_16x16x32_{f16,bf16}, operand A = 16 W2 rows, operand B = 16 C rows; lane l
 // supplies row l%16 and K elements 32*(l/16) + 8j..8j+7 of the block for MFMA j = 0..3
 // on both operands, and receives D[h = 4*(l/16)+v][row = l%16].  A work item's K blocks
 // are split over waves and reduced through LDS in a fixed order.
@@ -40,27 +42,70 @@ __device__ __forceinline__ v8bf as_v8bf(uint32_t a, uint32_t b, uint32_t c, uint
     return __builtin_bit_cast(v8bf, t);
 }
 
+// 4 e4m3 bytes -> 4 fp16 (2 dwords); v_cvt_scalef32_pk_f16_fp8 with scale 1 is exact
+__device__ __forceinline__ void e4m3x4_to_f16x4(uint32_t w, uint32_t& d0, uint32_t& d1) {
+    d0 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)w, 1.0f, false));
+    d1 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)w, 1.0f, true));
+}
+
+// 8 fp16 C values as bf16: the bf16 copy where the fp16 value is infinite (GEMM1 wrote
+// the copy for every value beyond the fp16 range), else the fp16 value rounded to bf16.
+__device__ __forceinline__ v4u c_f16_or_copy_to_bf16(const v4u& h, const v4u& b) {
+    v4u r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint32_t out = 0;
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            const uint32_t hb = (h[i] >> (16 * half)) & 0xffffu;
+            const uint32_t bb = (b[i] >> (16 * half)) & 0xffffu;
+            const float f = (float)__builtin_bit_cast(_Float16, (uint16_t)hb);
+            const uint32_t v = ((hb & 0x7fffu) == 0x7c00u) ? bb : f32_to_bf16_bits(f);
+            out |= v << (16 * half);
+        }
+        r[i] = out;
+    }
+    return r;
+}
+
+// One 16x16x32 MFMA of 8 widened W2 values per lane (e4m3 words w0, w1) against 8 C
+// values (bf16 or fp16 bits, as the kernel's C form)
+template <bool F16>
+__device__ __forceinline__ v4f mfma_w2_c(uint32_t w0, uint32_t w1, const v4u& c, const v4f& acc) {
+    uint32_t d0, d1, d2, d3;
+    if constexpr (F16) {
+        e4m3x4_to_f16x4(w0, d0, d1);
+        e4m3x4_to_f16x4(w1, d2, d3);
+        const v4u t = {d0, d1, d2, d3};
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, t), __builtin_bit_cast(v8h, c), acc, 0, 0, 0);
+    } else {
+        e4m3x4_to_bf16x4(w0, d0, d1);
+        e4m3x4_to_bf16x4(w1, d2, d3);
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(d0, d1, d2, d3), __builtin_bit_cast(v8bf, c), acc, 0, 0, 0);
+    }
+}
+
 // Register-staged W2 streaming (decode and small prefill).  A wave owns HF groups of
 // 16 output columns (W2 rows) of one expert for one row tile of 16 CB rows, over
 // 16 / KSPLIT consecutive K blocks (partials of the KSPLIT waves of an item reduced
 // through LDS in a fixed order).  The W2 bytes of a K block (16 HF rows x 128 B,
-// full-line loads) and the bf16 C fragments are held in a ring of D K blocks in
+// full-line loads) and the fp16 C fragments are held in a ring of D K blocks in
 // VGPRs, and each W2 block is moved to the MFMA layout through a per-wave LDS slot.
 // Without an LDS ring more waves fit per CU, so more bytes are in flight; HF > 1
 // shares each C fragment load among HF groups of 16 output columns, and CB > 1
 // feeds each widened W2 fragment to CB blocks of 16 C rows.
+// The kernel reads GEMM1's fp16-range flag once: fp16 C (the normal case) runs here.
 template <int D, int KSPLIT, int HF, int CB>
-__global__ __launch_bounds__(256) void gemm2_rstream_kernel(
+__device__ __forceinline__ void gemm2_rstream_body(
     const uint16_t* __restrict__ inter, const uint8_t* __restrict__ w2,
     const float* __restrict__ s2, const int4* __restrict__ tiles,
-    const int* __restrict__ num_tiles, float* __restrict__ out_rows) {
+    const int* __restrict__ num_tiles, float* __restrict__ out_rows,
+    uint8_t (*slot_lds)[16 * HF * kBlk], v4f (*red)[HF][CB][64]) {
     constexpr int NGW = 4 / KSPLIT;
     constexpr int KB = kIB / KSPLIT;
     constexpr int kItems = (kH / 16) / (NGW * HF);
     constexpr int kVmPerKb = 2 * HF + 4 * CB;         // W2 loads, 4 C loads per row block
     static_assert(D >= 2 && (D - 1) * kVmPerKb < 64, "ring depth");
-    __shared__ __attribute__((aligned(1024))) uint8_t slot_lds[4][16 * HF * kBlk];
-    __shared__ v4f red[KSPLIT > 1 ? 4 : 1][HF][CB][64];
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -146,15 +191,9 @@ __global__ __launch_bounds__(256) void gemm2_rstream_kernel(
 #pragma unroll
                 for (int c = 0; c < CB; ++c) t[c] = zero;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    uint32_t d0, d1, d2, d3;
-                    e4m3x4_to_bf16x4(ww[2 * j], d0, d1);
-                    e4m3x4_to_bf16x4(ww[2 * j + 1], d2, d3);
-                    const v8bf wj = as_v8bf(d0, d1, d2, d3);
+                for (int j = 0; j < 4; ++j)
 #pragma unroll
-                    for (int c = 0; c < CB; ++c)
-                        t[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wj, __builtin_bit_cast(v8bf, bc[k % D][c][j]), t[c], 0, 0, 0);
-                }
+                    for (int c = 0; c < CB; ++c) t[c] = mfma_w2_c<true>(ww[2 * j], ww[2 * j + 1], bc[k % D][c][j], t[c]);
                 const float sb = sp[hf][kb0 + k];
 #pragma unroll
                 for (int c = 0; c < CB; ++c)
@@ -196,6 +235,101 @@ __global__ __launch_bounds__(256) void gemm2_rstream_kernel(
             __syncthreads();
         }
     }
+}
+
+// The same work items when C went beyond the fp16 range somewhere (rare): bf16 MFMAs on
+// C taken from GEMM1's bf16 copy wherever the fp16 value is infinite.  Plain loads in
+// the MFMA layout, one K block at a time: slow, but light on registers, so the normal
+// path keeps its occupancy.
+template <int KSPLIT, int HF, int CB>
+__device__ __forceinline__ void gemm2_rstream_rare(
+    const uint16_t* __restrict__ inter, const uint16_t* __restrict__ inter_bf16,
+    const uint8_t* __restrict__ w2, const float* __restrict__ s2, const int4* __restrict__ tiles,
+    const int* __restrict__ num_tiles, float* __restrict__ out_rows, v4f (*red)[HF][CB][64]) {
+    constexpr int NGW = 4 / KSPLIT;
+    constexpr int KB = kIB / KSPLIT;
+    constexpr int kItems = (kH / 16) / (NGW * HF);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int r16 = lane & 15, kq = lane >> 4;
+    const int ngl = wave / KSPLIT, ks = wave % KSPLIT;
+    const int nwork = (*num_tiles) * kItems;
+    const v4f zero = {0.f, 0.f, 0.f, 0.f};
+    for (int work = blockIdx.x; work < nwork; work += gridDim.x) {
+        const int4 tile = tiles[work / kItems];
+        const int hg = ((work % kItems) * NGW + ngl) * HF;
+        const int le = tile.x, row0 = tile.y, nrows = tile.z;
+        v4f acc[HF][CB];
+#pragma unroll
+        for (int hf = 0; hf < HF; ++hf)
+#pragma unroll
+            for (int c = 0; c < CB; ++c) acc[hf][c] = zero;
+#pragma unroll 1
+        for (int kb = ks * KB; kb < (ks + 1) * KB; ++kb) {
+            v4u cf[CB][4];
+#pragma unroll
+            for (int c = 0; c < CB; ++c) {
+                const size_t off = (size_t)(row0 + min(16 * c + r16, nrows - 1)) * kI + kb * kBlk + kq * 32;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    cf[c][j] = c_f16_or_copy_to_bf16(*reinterpret_cast<const v4u*>(inter + off + 8 * j),
+                                                     *reinterpret_cast<const v4u*>(inter_bf16 + off + 8 * j));
+            }
+#pragma unroll
+            for (int hf = 0; hf < HF; ++hf) {
+                const uint8_t* wp = w2 + (size_t)(le * kH + (hg + hf) * 16 + r16) * kI + kb * kBlk + kq * 32;
+                const v4u x0 = *reinterpret_cast<const v4u*>(wp);
+                const v4u x1 = *reinterpret_cast<const v4u*>(wp + 16);
+                const uint32_t ww[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+                v4f t[CB];
+#pragma unroll
+                for (int c = 0; c < CB; ++c) t[c] = zero;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int c = 0; c < CB; ++c) t[c] = mfma_w2_c<false>(ww[2 * j], ww[2 * j + 1], cf[c][j], t[c]);
+                const float sb = s2[(size_t)(le * kHB + ((hg + hf) >> 3)) * kIB + kb];
+#pragma unroll
+                for (int c = 0; c < CB; ++c)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) acc[hf][c][v] = __builtin_fmaf(t[c][v], sb, acc[hf][c][v]);
+            }
+        }
+#pragma unroll
+        for (int hf = 0; hf < HF; ++hf)
+#pragma unroll
+            for (int c = 0; c < CB; ++c) red[wave][hf][c][lane] = acc[hf][c];
+        __syncthreads();
+        if (ks == 0) {
+#pragma unroll
+            for (int c = 0; c < CB; ++c) {
+                if (16 * c + r16 < nrows) {
+#pragma unroll
+                    for (int hf = 0; hf < HF; ++hf) {
+                        v4f o = red[wave][hf][c][lane];
+#pragma unroll
+                        for (int q = 1; q < KSPLIT; ++q) o += red[wave + q][hf][c][lane];
+                        *reinterpret_cast<v4f*>(out_rows + (size_t)(row0 + 16 * c + r16) * kH + (hg + hf) * 16 + kq * 4) = o;
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
+template <int D, int KSPLIT, int HF, int CB>
+__global__ __launch_bounds__(256) void gemm2_rstream_kernel(
+    Intermediate C, const int* __restrict__ c_wide, const uint8_t* __restrict__ w2,
+    const float* __restrict__ s2, const int4* __restrict__ tiles,
+    const int* __restrict__ num_tiles, float* __restrict__ out_rows) {
+    static_assert(KSPLIT > 1, "the reduction through LDS assumes a K split");
+    __shared__ __attribute__((aligned(1024))) uint8_t slot_lds[4][16 * HF * kBlk];
+    __shared__ v4f red[4][HF][CB][64];
+    if (__builtin_amdgcn_readfirstlane(*c_wide) == 0)
+        gemm2_rstream_body<D, KSPLIT, HF, CB>(C.f16(), w2, s2, tiles, num_tiles, out_rows, slot_lds, red);
+    else
+        gemm2_rstream_rare<KSPLIT, HF, CB>(C.f16(), C.bf16(), w2, s2, tiles, num_tiles, out_rows, red);
 }
 
 // Prefill GEMM2 (many tokens per expert): MFMA-bound tiling on FP8 MFMA with C in
@@ -373,6 +507,15 @@ __global__ void e4m3_to_bf16_kernel(const uint32_t* __restrict__ in, uint2* __re
     out[i] = make_uint2(d0, d1);
 }
 
+// Debug: widen e4m3 bytes to fp16 with the conversion of GEMM2's fp16 form.
+__global__ void e4m3_to_f16_kernel(const uint32_t* __restrict__ in, uint2* __restrict__ out, int nwords) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nwords) return;
+    uint32_t d0, d1;
+    e4m3x4_to_f16x4(in[i], d0, d1);
+    out[i] = make_uint2(d0, d1);
+}
+
 static int grid_for2(long long work) { return (int)(work < 4096 ? work : 4096); }
 
 // Variants (the tile height of the dispatch they expect, and the form of C they read):
@@ -384,21 +527,21 @@ static int grid_for2(long long work) { return (int)(work < 4096 ? work : 4096); 
 bool launch_gemm2(int variant, const Intermediate& C, const uint8_t* w2, const float* s2,
                   const int4* tiles, const int* num_tiles, const int* exp_off, int max_tiles,
                   float* out_rows, hipStream_t stream) {
-    const uint16_t* inter = C.bf16();
+    const int* c_wide = exp_off + kCWideFlag;
     const long long mt = max_tiles;
     constexpr int G = kH / 16;      // 16-column groups
     switch (variant) {
         case 1:
             hipLaunchKernelGGL((gemm2_rstream_kernel<4, 4, 2, 1>), dim3(grid_for2(mt * G / 2)), dim3(256), 0,
-                               stream, inter, w2, s2, tiles, num_tiles, out_rows);
+                               stream, C, c_wide, w2, s2, tiles, num_tiles, out_rows);
             return true;
         case 2:
             hipLaunchKernelGGL((gemm2_rstream_kernel<3, 4, 4, 1>), dim3(grid_for2(mt * G / 4)), dim3(256), 0,
-                               stream, inter, w2, s2, tiles, num_tiles, out_rows);
+                               stream, C, c_wide, w2, s2, tiles, num_tiles, out_rows);
             return true;
         case 3:
             hipLaunchKernelGGL((gemm2_rstream_kernel<3, 4, 4, 2>), dim3(grid_for2(mt * G / 4)), dim3(256), 0,
-                               stream, inter, w2, s2, tiles, num_tiles, out_rows);
+                               stream, C, c_wide, w2, s2, tiles, num_tiles, out_rows);
             return true;
         case 4:
         case 5:
@@ -407,6 +550,13 @@ bool launch_gemm2(int variant, const Intermediate& C, const uint8_t* w2, const f
             return true;
         default: return false;
     }
+}
+
+void launch_e4m3_to_f16(const uint8_t* in, uint16_t* out, int n, hipStream_t stream) {
+    const int nwords = n / 4;
+    if (nwords <= 0) return;
+    hipLaunchKernelGGL(e4m3_to_f16_kernel, dim3((nwords + 255) / 256), dim3(256), 0, stream,
+                       reinterpret_cast<const uint32_t*>(in), reinterpret_cast<uint2*>(out), nwords);
 }
 
 void launch_e4m3_to_bf16(const uint8_t* in, uint16_t* out, int n, hipStream_t stream) {

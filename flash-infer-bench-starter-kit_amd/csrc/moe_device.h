@@ -26,6 +26,7 @@ constexpr int kN1B = kN1 / kBlk;   // 32 GEMM1 output blocks
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef short v8s __attribute__((ext_vector_type(8)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
@@ -168,19 +169,31 @@ __device__ __forceinline__ void bdma4(__amdgpu_buffer_rsrc_t r, uint32_t voff, u
 }
 
 // The SwiGLU rows C [rows, 2048] between GEMM1 and GEMM2 live in one workspace
-// region in one of two forms, chosen by the kernel plan:
-//   bf16: C as bf16 rows (streaming kernels, 16- and 32-row tiles);
-//   fp8 hi/lo: per row and 128-column block b a scale s = amax/448 and two e4m3
-//     rows hi = e4m3(C/s), lo = e4m3((C - hi*s) * 16/s), so C ~ s*(hi + lo/16)
-//     with about 8 significant bits (prefill kernels; GEMM2 then runs two FP8
-//     MFMAs per block, the second with an exact 2^-4 operand scale).
-// hi occupies the first rows_cap*2048 bytes of the region, lo the next; the scales
-// are fp32 [16, rows_cap] (block-major, so a tile's rows are contiguous).
+// region (rows_cap x 2048 x 4 bytes) in one of two forms, chosen by the kernel plan:
+//   fp16 (streaming kernels, 16- and 32-row tiles): C rounded to fp16 in the first
+//     rows_cap*2048 halves.  fp16 keeps 11 significant bits, and so GEMM2 adds no
+//     error that matters next to the bf16 output rounding (bf16 C, 8 bits, reaches
+//     the 1e-2 tolerance on tokens whose 8 experts are all local).  For a group of 4
+//     values with one beyond the fp16 range, GEMM1 also writes the group in bf16 to
+//     the next rows_cap*2048 halves and raises the flag word meta[kCWideFlag];
+//     GEMM2 then runs on bf16, taking those copies where the fp16 value is infinite;
+//   fp8 hi/lo (prefill kernels): per row and 128-column block b a scale
+//     s = amax/448 and two e4m3 rows hi = e4m3(C/s), lo = e4m3((C - hi*s) * 16/s),
+//     so C ~ s*(hi + lo/16) (GEMM2 then runs two FP8 MFMAs per block, the second
+//     with an exact 2^-4 operand scale).  hi occupies the first rows_cap*2048 bytes
+//     of the region, lo the next; the scales are fp32 [16, rows_cap] (block-major,
+//     so a tile's rows are contiguous).
+constexpr int kCWideFlag = kEL + 3;    // meta word: C exceeds the fp16 range
+constexpr float kF16Max = 65504.f;
+
 struct Intermediate {
     void* base;
     float* scales;
     int rows_cap;
-    __host__ __device__ uint16_t* bf16() const { return static_cast<uint16_t*>(base); }
+    __host__ __device__ uint16_t* f16() const { return static_cast<uint16_t*>(base); }
+    __host__ __device__ uint16_t* bf16() const {
+        return static_cast<uint16_t*>(base) + (size_t)rows_cap * kI;
+    }
     __host__ __device__ uint8_t* hi() const { return static_cast<uint8_t*>(base); }
     __host__ __device__ uint8_t* lo() const {
         return static_cast<uint8_t*>(base) + (size_t)rows_cap * kI;

@@ -91,9 +91,12 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
                                                     const uint16_t* __restrict__ bias,
                                                     int T, float factor,
                                                     int* __restrict__ topk_ids,
-                                                    float* __restrict__ topk_w) {
+                                                    float* __restrict__ topk_w,
+                                                    int* __restrict__ clear_word) {
     const int lane = threadIdx.x & 63;
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    // the forward's per-call flag word (GEMM1 sets it, GEMM2 reads it) starts at 0
+    if (clear_word != nullptr && blockIdx.x == 0 && threadIdx.x == 0) *clear_word = 0;
     if (t >= T) return;  // uniform per wave
 
     const float4 lg = reinterpret_cast<const float4*>(logits + (size_t)t * kEG)[lane];
@@ -184,11 +187,12 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
     }
 }
 
+// clear_word (may be null): an int the kernel sets to 0 for the kernels after it.
 void launch_route(const float* logits, const uint16_t* bias, int T, float factor,
-                  int* topk_ids, float* topk_w, hipStream_t stream) {
+                  int* topk_ids, float* topk_w, int* clear_word, hipStream_t stream) {
     if (T <= 0) return;
     hipLaunchKernelGGL(route_kernel, dim3((T + 3) / 4), dim3(256), 0, stream, logits, bias,
-                       T, factor, topk_ids, topk_w);
+                       T, factor, topk_ids, topk_w, clear_word);
 }
 
 }  // namespace moe

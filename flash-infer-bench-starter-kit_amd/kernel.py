@@ -7,7 +7,7 @@ Entry      : kernel.py::kernel
 
 Same signature, argument meaning and destination-passing contract as the
 reference's ``solution/python/kernel.py:95-120``; the work behind it is the C ABI of
-``include/moe_mi355.h`` (route -> dispatch -> FP8 GEMM1 + SwiGLU -> GEMM2 (bf16 MFMA
+``include/moe_mi355.h`` (route -> dispatch -> FP8 GEMM1 + SwiGLU -> GEMM2 (fp16 MFMA
 for small T, FP8 MFMA over an fp8 hi/lo split of the SwiGLU rows for large T) ->
 ordered combine, all on the caller's current stream, no host synchronisation).
 
@@ -84,6 +84,7 @@ def _declare(L: ctypes.CDLL) -> ctypes.CDLL:
         "moe_mi355_profile_read": (ctypes.c_int, [P, I32]),
         "moe_mi355_profile_end": (ctypes.c_int, []),
         "moe_mi355_debug_e4m3_to_bf16": (ctypes.c_int, [P, P, I32, P]),
+        "moe_mi355_debug_e4m3_to_f16": (ctypes.c_int, [P, P, I32, P]),
         "moe_mi355_quantize_fp8_blockwise": (ctypes.c_int, [P, I32, I32, I32, P, P, P]),
         "moe_mi355_strerror": (ctypes.c_char_p, [ctypes.c_int]),
         "moe_mi355_last_hip_error": (ctypes.c_char_p, []),

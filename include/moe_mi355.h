@@ -153,15 +153,18 @@ typedef struct moe_mi355_workspace_layout {
     size_t topk_weights;    /* fp32  [T,8] */
     size_t inverse_rows;    /* int32 [T,8] */
     size_t meta;            /* int32 [64]: [0..32] expert offsets, [33] num tiles,
-                               [34] tiles of the second list (256-row plans) */
+                               [34] tiles of the second list (256-row plans),
+                               [35] nonzero when C went beyond the fp16 range (format 0) */
     size_t tiles;           /* int32 [2*max_tiles,4]: the tile list, then (256-row
                                plans) a second list of 128-row tiles for GEMM2 */
     size_t sorted_tokens;   /* int32 [8T] */
     size_t sorted_weights;  /* fp32  [8T] */
     size_t chunk_counts;    /* int32 [ceil(T/256), 32] dispatch scratch */
-    size_t intermediate;    /* SwiGLU output rows C, 8T x 2048 x 2 bytes, in one of two
+    size_t intermediate;    /* SwiGLU output rows C, 8T x 2048 x 4 bytes, in one of two
                                forms (intermediate_format):
-                               0: bf16 [8T, 2048];
+                               0: fp16 [8T, 2048], then bf16 [8T, 2048] holding copies
+                                  of the 4-value groups with a value beyond the fp16
+                                  range (meta[35] set: GEMM2 then runs on bf16);
                                1: fp8 hi/lo: e4m3 hi [8T, 2048] then e4m3 lo [8T, 2048],
                                   C = s * (hi + lo / 16) with s from intermediate_scales */
     size_t intermediate_scales; /* fp32 [16, 8T]: s of row r, 128-column block b at [b][r] */
@@ -186,9 +189,13 @@ MOE_MI355_API int moe_mi355_profile_end(void);
 #define MOE_MI355_NUM_STAGES 5
 
 /* Debug: widen n e4m3 bytes (n % 4 == 0) to bf16 bits with the conversion the GEMM2
- * kernel uses.  No reference counterpart (the reference never widens e4m3 to bf16);
- * it lets a test pin that conversion against the OCP e4m3 table. */
+ * kernel uses on its bf16 form of C.  No reference counterpart (the reference never
+ * widens e4m3); it lets a test pin that conversion against the OCP e4m3 table. */
 MOE_MI355_API int moe_mi355_debug_e4m3_to_bf16(const uint8_t* in, uint16_t* out, int32_t n, void* stream);
+
+/* Debug: the same for fp16 bits, the conversion of GEMM2's (default) fp16 form of C.
+ * No reference counterpart; a test pins it against the OCP e4m3 table. */
+MOE_MI355_API int moe_mi355_debug_e4m3_to_f16(const uint8_t* in, uint16_t* out, int32_t n, void* stream);
 
 MOE_MI355_API const char* moe_mi355_strerror(int status);
 /* Text of the last HIP error seen by this library in the calling thread. */

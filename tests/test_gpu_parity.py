@@ -20,19 +20,23 @@ pytestmark = pytest.mark.gpu
 CFG_IDS = [0, 1, 2, 3, 4]
 
 
-def test_e4m3_widening_is_exact():
+@pytest.mark.parametrize("form", ["bf16", "f16"])
+def test_e4m3_widening_is_exact(form):
+    """GEMM2's widening of the W2 bytes (to bf16 or fp16, the two forms of C it
+    multiplies) against the OCP e4m3 table, code by code."""
     k = pkg("kernel")
     L = k._build_extension()
     codes = torch.arange(256, dtype=torch.uint8, device="cuda")
     out = torch.empty(256, dtype=torch.int16, device="cuda")
-    rc = L.moe_mi355_debug_e4m3_to_bf16(codes.data_ptr(), out.data_ptr(), 256, None)
+    rc = getattr(L, f"moe_mi355_debug_e4m3_to_{form}")(codes.data_ptr(), out.data_ptr(), 256, None)
     assert rc == 0
     torch.cuda.synchronize()
-    got = out.cpu().view(torch.bfloat16).float().numpy()
+    got = out.cpu().view(torch.bfloat16 if form == "bf16" else torch.float16).float().numpy()
     tab = oracle().e4m3_table()
     nan = np.isnan(tab)
     assert np.array_equal(np.isnan(got), nan)
     assert np.array_equal(got[~nan], tab[~nan])
+    assert np.array_equal(np.signbit(got[~nan]), np.signbit(tab[~nan]))   # -0 stays -0
 
 
 @pytest.mark.parametrize("idx", CFG_IDS)

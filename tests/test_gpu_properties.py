@@ -137,3 +137,78 @@ def test_every_gemm_variant_matches_oracle(T, g1, g2, monkeypatch):
     st = compare_to_oracle(d, out, toks)
     note(f"[gpu] T={T} g1={g1} g2={g2} stats {st}")
     assert st["frac_within"] == 1.0, st
+
+
+@pytest.mark.parametrize("T", [64, 600, 2049])
+def test_all_local_routing_matches_oracle(T):
+    """Every token routed to 8 local experts (bias +3 on all 32 local experts, so group 0
+    always wins and holds the whole top 8): N_a = 8T rows, the most the row-tile list
+    and the workspace are sized for, on a 16-row, a 32-row and a 256-row plan."""
+    k = pkg("kernel")
+    wl = pkg("workloads")
+    cfg = wl.Config("all_local", T, 0, hot_local_experts=tuple(range(32)), seed=20261111)
+    d = dict(config_inputs(4))                   # offset 0: reuse its weights
+    d.update(wl.make_activations(cfg, device="cuda"))
+    d["output"] = torch.empty(T, 7168, dtype=torch.bfloat16, device="cuda")
+    note(f"[gpu] all-local routing T={T}")
+    ids, w = k.route(d["routing_logits"], d["routing_bias"], d["routed_scaling_factor"])
+    g = k.dispatch(ids, w, 0, 16)
+    torch.cuda.synchronize()
+    assert int(g["exp_off"][-1].item()) == 8 * T
+    out = run_forward(d)
+    rng = np.random.default_rng(T + 11)
+    toks = sorted(rng.choice(T, min(T, 12), replace=False).tolist())
+    st = compare_to_oracle(d, out, toks)
+    note(f"[gpu] all-local T={T} stats {st}")
+    assert st["frac_within"] == 1.0, st
+    assert bool(torch.isfinite(out.float()).all())
+
+
+def test_c_beyond_fp16_range_uses_the_bf16_copy():
+    """The streaming plans keep C in fp16.  Hidden-state scales 2^10 times larger push
+    C far beyond the fp16 range (|C| ~ 1e6): GEMM1 must raise the workspace flag
+    (meta[35]) and GEMM2 must read the bf16 copy.  The output is then the oracle's
+    restatement with C rounded to bf16 (to 4e-3 of the largest output: fp32 order
+    and the bf16 output rounding), within 1e-2 of the largest output of the fp32
+    oracle, and finite.  (Elementwise atol 1e-2 means nothing at this scale: where
+    terms of 1e6 cancel, bf16 C leaves errors of ~1e3.)  A normal call on the same
+    workspace afterwards finds the flag cleared again."""
+    k = pkg("kernel")
+    wl = pkg("workloads")
+    d = dict(config_inputs(1))
+    T = d["routing_logits"].shape[0]
+    lay = k.workspace_layout(T)
+    assert lay.intermediate_format == 0
+    ws = torch.empty(lay.total, dtype=torch.uint8, device="cuda")
+
+    def flag():
+        return int(ws[lay.meta + 35 * 4:lay.meta + 36 * 4].view(torch.int32).item())
+
+    big = dict(d)
+    big["hidden_states_scale"] = d["hidden_states_scale"] * 1024.0
+    note("[gpu] C beyond the fp16 range (T=64, hidden scales x 2^10)")
+    out = torch.full_like(d["output"], float("nan"))
+    k.forward(*wl.as_args({**big, "output": out}), workspace=ws)
+    torch.cuda.synchronize()
+    assert flag() == 1
+    o = oracle()
+    ids, w = o.route(big["routing_logits"], big["routing_bias"], big["routed_scaling_factor"])
+    args = (big["hidden_states"], big["hidden_states_scale"], big["gemm1_weights"], big["gemm1_weights_scale"],
+            big["gemm2_weights"], big["gemm2_weights_scale"], ids, w, big["local_expert_offset"])
+    ref32 = o.expert_forward(*args)
+    refb = o.expert_forward(*args, intermediate_dtype=torch.bfloat16)
+    got = out.float().cpu()
+    scale = float(ref32.abs().max())
+    e_b = float((got - refb).abs().max())
+    e_32 = float((got - ref32).abs().max())
+    note(f"[gpu] beyond-fp16: max|ref| {scale:.4g}, max err vs bf16-C oracle {e_b:.4g}, vs fp32 oracle {e_32:.4g}")
+    assert scale > 65504.0
+    assert bool(torch.isfinite(got).all())
+    assert e_b <= 4e-3 * scale and e_32 <= 1e-2 * scale
+
+    out2 = torch.full_like(d["output"], float("nan"))
+    k.forward(*wl.as_args({**d, "output": out2}), workspace=ws)
+    torch.cuda.synchronize()
+    assert flag() == 0
+    ref = run_forward(d)
+    assert torch.equal(out2.view(torch.int16), ref.view(torch.int16))
