@@ -85,6 +85,36 @@ __device__ __forceinline__ v4f mfma_w2_c(uint32_t w0, uint32_t w1, const v4u& c,
     }
 }
 
+// End of a streaming work item: the KSPLIT waves of each column group add their K
+// partials through LDS in a fixed order (so results do not depend on scheduling), and the
+// first of them writes the fp32 expert rows that exist.
+template <int KSPLIT, int HF, int CB>
+__device__ __forceinline__ void reduce_store(const v4f (&acc)[HF][CB], v4f (*red)[HF][CB][64], int wave,
+                                             int lane, int ks, int row0, int nrows, int hg,
+                                             float* __restrict__ out_rows) {
+    const int r16 = lane & 15, kq = lane >> 4;
+#pragma unroll
+    for (int hf = 0; hf < HF; ++hf)
+#pragma unroll
+        for (int c = 0; c < CB; ++c) red[wave][hf][c][lane] = acc[hf][c];
+    __syncthreads();
+    if (ks == 0) {
+#pragma unroll
+        for (int c = 0; c < CB; ++c) {
+            if (16 * c + r16 < nrows) {
+#pragma unroll
+                for (int hf = 0; hf < HF; ++hf) {
+                    v4f o = red[wave][hf][c][lane];
+#pragma unroll
+                    for (int q = 1; q < KSPLIT; ++q) o += red[wave + q][hf][c][lane];
+                    *reinterpret_cast<v4f*>(out_rows + (size_t)(row0 + 16 * c + r16) * kH + (hg + hf) * 16 + kq * 4) = o;
+                }
+            }
+        }
+    }
+    __syncthreads();
+}
+
 // Register-staged W2 streaming (decode and small prefill).  A wave owns HF groups of
 // 16 output columns (W2 rows) of one expert for one row tile of 16 CB rows, over
 // 16 / KSPLIT consecutive K blocks (partials of the KSPLIT waves of an item reduced
@@ -106,6 +136,7 @@ __device__ __forceinline__ void gemm2_rstream_body(
     constexpr int kItems = (kH / 16) / (NGW * HF);
     constexpr int kVmPerKb = 2 * HF + 4 * CB;         // W2 loads, 4 C loads per row block
     static_assert(D >= 2 && (D - 1) * kVmPerKb < 64, "ring depth");
+    static_assert(KSPLIT > 1, "the partials are reduced through LDS");
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -203,37 +234,7 @@ __device__ __forceinline__ void gemm2_rstream_body(
             __builtin_amdgcn_sched_barrier(0);
         }
 
-        if constexpr (KSPLIT == 1) {
-#pragma unroll
-            for (int c = 0; c < CB; ++c) {
-                if (16 * c + r16 < nrows) {
-#pragma unroll
-                    for (int hf = 0; hf < HF; ++hf)
-                        *reinterpret_cast<v4f*>(out_rows + (size_t)(row0 + 16 * c + r16) * kH + (hg + hf) * 16 + kq * 4) = acc[hf][c];
-                }
-            }
-        } else {
-#pragma unroll
-            for (int hf = 0; hf < HF; ++hf)
-#pragma unroll
-                for (int c = 0; c < CB; ++c) red[wave][hf][c][lane] = acc[hf][c];
-            __syncthreads();
-            if (ks == 0) {
-#pragma unroll
-                for (int c = 0; c < CB; ++c) {
-                    if (16 * c + r16 < nrows) {
-#pragma unroll
-                        for (int hf = 0; hf < HF; ++hf) {
-                            v4f o = red[wave][hf][c][lane];
-#pragma unroll
-                            for (int q = 1; q < KSPLIT; ++q) o += red[wave + q][hf][c][lane];
-                            *reinterpret_cast<v4f*>(out_rows + (size_t)(row0 + 16 * c + r16) * kH + (hg + hf) * 16 + kq * 4) = o;
-                        }
-                    }
-                }
-            }
-            __syncthreads();
-        }
+        reduce_store<KSPLIT, HF, CB>(acc, red, wave, lane, ks, row0, nrows, hg, out_rows);
     }
 }
 
@@ -295,26 +296,7 @@ __device__ __forceinline__ void gemm2_rstream_rare(
                     for (int v = 0; v < 4; ++v) acc[hf][c][v] = __builtin_fmaf(t[c][v], sb, acc[hf][c][v]);
             }
         }
-#pragma unroll
-        for (int hf = 0; hf < HF; ++hf)
-#pragma unroll
-            for (int c = 0; c < CB; ++c) red[wave][hf][c][lane] = acc[hf][c];
-        __syncthreads();
-        if (ks == 0) {
-#pragma unroll
-            for (int c = 0; c < CB; ++c) {
-                if (16 * c + r16 < nrows) {
-#pragma unroll
-                    for (int hf = 0; hf < HF; ++hf) {
-                        v4f o = red[wave][hf][c][lane];
-#pragma unroll
-                        for (int q = 1; q < KSPLIT; ++q) o += red[wave + q][hf][c][lane];
-                        *reinterpret_cast<v4f*>(out_rows + (size_t)(row0 + 16 * c + r16) * kH + (hg + hf) * 16 + kq * 4) = o;
-                    }
-                }
-            }
-        }
-        __syncthreads();
+        reduce_store<KSPLIT, HF, CB>(acc, red, wave, lane, ks, row0, nrows, hg, out_rows);
     }
 }
 
@@ -323,7 +305,6 @@ __global__ __launch_bounds__(256) void gemm2_rstream_kernel(
     Intermediate C, const int* __restrict__ c_wide, const uint8_t* __restrict__ w2,
     const float* __restrict__ s2, const int4* __restrict__ tiles,
     const int* __restrict__ num_tiles, float* __restrict__ out_rows) {
-    static_assert(KSPLIT > 1, "the reduction through LDS assumes a K split");
     __shared__ __attribute__((aligned(1024))) uint8_t slot_lds[4][16 * HF * kBlk];
     __shared__ v4f red[4][HF][CB][64];
     if (__builtin_amdgcn_readfirstlane(*c_wide) == 0)
