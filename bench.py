@@ -214,9 +214,9 @@ def main() -> int:
                       flops=n_a * 2 * 7168 * 4096, peak_tflops=FP8_PEAK_TFLOPS),
         # GEMM2 runs fp16 MFMA (streaming) or two FP8 MFMAs per product (prefill hi/lo):
         # either way its MFMA ceiling on the algorithmic flops is the 16-bit rate
-        "gemm2": dict(bytes=e_a * (7168 * 2048 + 56 * 16 * 4) + n_a * 2048 * 2 + n_a * 7168 * 4,
+        "gemm2": dict(bytes=e_a * (7168 * 2048 + 56 * 16 * 4) + n_a * 2048 * 2 + n_a * 7168 * 2,
                       flops=n_a * 2 * 2048 * 7168, peak_tflops=BF16_PEAK_TFLOPS),
-        "combine": dict(bytes=n_a * 7168 * 4 + T * 7168 * 2 + T * 8 * 4 + n_a * 4, flops=0,
+        "combine": dict(bytes=n_a * 7168 * 2 + T * 7168 * 2 + T * 8 * 4 + n_a * 4, flops=0,
                         peak_tflops=FP8_PEAK_TFLOPS),
         "route": dict(bytes=T * 256 * 4 + 512 + T * 8 * 8, flops=0, peak_tflops=FP8_PEAK_TFLOPS),
         "dispatch": dict(bytes=T * 8 * 8 * 2 + n_a * 8, flops=0, peak_tflops=FP8_PEAK_TFLOPS),

@@ -7,8 +7,8 @@
 // allocation:
 //   route    (T/4 workgroups)      -> topk ids / weights
 //   dispatch (1 workgroup)         -> expert offsets, row tiles, permutation, inverse map
-//   gemm1    (persistent)          -> SwiGLU rows C      [N_a, 2048] (bf16 or fp8 hi/lo)
-//   gemm2    (persistent)          -> fp32 expert rows   [N_a, 7168]
+//   gemm1    (persistent)          -> SwiGLU rows C      [N_a, 2048] (fp16 or fp8 hi/lo)
+//   gemm2    (persistent)          -> fp16 expert rows   [N_a, 7168]
 //   combine  (7 T workgroups)      -> bf16 output        [T, 7168]
 // The GEMM grids are sized from the host-known bound on the tile count; each
 // workgroup reads the real count written by dispatch and exits when it runs out.
@@ -29,8 +29,8 @@ bool launch_gemm1(int, const uint8_t*, const float*, int, const uint8_t*, const 
                   const int4*, const int*, const int*, int, const int*, const Intermediate&,
                   hipStream_t);
 bool launch_gemm2(int, const Intermediate&, const uint8_t*, const float*, const int4*, const int*,
-                  const int*, int, float*, hipStream_t);
-void launch_combine(const float*, const float*, const int*, int, uint16_t*, hipStream_t);
+                  const int*, int, const ExpertRows&, hipStream_t);
+void launch_combine(const ExpertRows&, const int*, const float*, const int*, int, uint16_t*, hipStream_t);
 void launch_e4m3_to_bf16(const uint8_t*, uint16_t*, int, hipStream_t);
 void launch_e4m3_to_f16(const uint8_t*, uint16_t*, int, hipStream_t);
 void launch_quantize_fp8_blockwise(const void*, int, int, int, uint8_t*, float*, hipStream_t);
@@ -104,7 +104,8 @@ bool fill_layout(int32_t T, moe_mi355_workspace_layout* L) {
     L->chunk_counts = take((size_t)((T + 255) / 256) * moe::kEL * 4);
     L->intermediate = take(R * moe::kI * 4);
     L->intermediate_scales = take(R * moe::kIB * 4);
-    L->expert_out = take(R * moe::kH * 4);
+    L->expert_out = take(R * moe::kH * 2);
+    L->expert_out_wide = take(R * moe::kH * 4);
     L->total = off;
     const Plan plan = choose_plan(T);
     L->tile_m = plan.tm;
@@ -251,7 +252,8 @@ int moe_mi355_forward(const moe_mi355_args* a, void* stream) {
     float* sw = reinterpret_cast<float*>(ws + L.sorted_weights);
     const moe::Intermediate inter{ws + L.intermediate, reinterpret_cast<float*>(ws + L.intermediate_scales),
                                   T * moe::kTopK};
-    float* rows = reinterpret_cast<float*>(ws + L.expert_out);
+    const moe::ExpertRows rows{reinterpret_cast<uint16_t*>(ws + L.expert_out),
+                               reinterpret_cast<float*>(ws + L.expert_out_wide)};
     int* chunk_cnt = reinterpret_cast<int*>(ws + L.chunk_counts);
     int* num_tiles = meta + moe::kEL + 1;
 
@@ -282,7 +284,7 @@ int moe_mi355_forward(const moe_mi355_args* a, void* stream) {
         moe::launch_gemm2(plan.g2, inter, a->gemm2_weights, a->gemm2_weights_scale, tiles,
                           num_tiles, meta, max_tiles, rows, s);
     if (prof) prof_record(slot, 4, s);
-    moe::launch_combine(rows, sw, inv, T, a->output, s);
+    moe::launch_combine(rows, meta + moe::kRowsWideFlag, sw, inv, T, a->output, s);
     if (prof) prof_record(slot, 5, s);
     return hip_status(hipGetLastError());
 }

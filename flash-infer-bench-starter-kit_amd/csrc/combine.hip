@@ -10,7 +10,9 @@
 // Rows of one token are visited in ascending row index, which is ascending local
 // expert because the permutation is expert-major.  Tokens with no local expert get
 // +0.0.  One thread produces 8 consecutive outputs (one 16-byte store), with the loads
-// of all the token's rows in flight together.
+// of all the token's rows in flight together.  The expert rows arrive in fp16
+// (ExpertRows); on a call where GEMM2 flagged a value beyond the fp16 range, the
+// fp32 copy GEMM2 wrote replaces every infinite fp16 value.
 
 #include "moe_device.h"
 
@@ -24,7 +26,11 @@ __device__ __forceinline__ void cswap(int& a, int& b) {
     b = y;
 }
 
-__global__ __launch_bounds__(128) void combine_kernel(const float* __restrict__ rows_out,
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+__global__ __launch_bounds__(128) void combine_kernel(ExpertRows rows, const int* __restrict__ rows_wide,
                                                       const float* __restrict__ sorted_w,
                                                       const int* __restrict__ inv, int T,
                                                       uint16_t* __restrict__ out) {
@@ -53,23 +59,31 @@ __global__ __launch_bounds__(128) void combine_kernel(const float* __restrict__ 
     int nr = 0;
 #pragma unroll
     for (int k = 0; k < kTopK; ++k) nr += (r[k] != 0x7fffffff) ? 1 : 0;
-    auto body = [&](auto rows) {
-        constexpr int N = decltype(rows)::value;
+    auto body = [&](auto nrows_c, auto wide_c) {
+        constexpr int N = decltype(nrows_c)::value;
+        constexpr bool kWide = decltype(wide_c)::value != 0;
         float acc[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
-        float4 a[N > 0 ? N : 1], b[N > 0 ? N : 1];
+        uint4 a[N > 0 ? N : 1];
         float w[N > 0 ? N : 1];
 #pragma unroll
         for (int k = 0; k < N; ++k) {
-            const float4* p = reinterpret_cast<const float4*>(rows_out + (size_t)r[k] * kH + h0);
-            a[k] = p[0];
-            b[k] = p[1];
+            a[k] = *reinterpret_cast<const uint4*>(rows.f16 + (size_t)r[k] * kH + h0);
             w[k] = sorted_w[r[k]];
         }
 #pragma unroll
         for (int k = 0; k < N; ++k) {
-            const float o[8] = {a[k].x, a[k].y, a[k].z, a[k].w, b[k].x, b[k].y, b[k].z, b[k].w};
+            const uint32_t hw[4] = {a[k].x, a[k].y, a[k].z, a[k].w};
+            float o[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o[j] = f16_bits_to_f32((hw[j >> 1] >> (16 * (j & 1))) & 0xffffu);
+            if constexpr (kWide) {
+                const float* cp = rows.f32 + (size_t)r[k] * kH + h0;
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (__builtin_isinf(o[j])) o[j] = cp[j];
+            }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const float prod = o[j] * w[k];
@@ -83,25 +97,29 @@ __global__ __launch_bounds__(128) void combine_kernel(const float* __restrict__ 
         pk.w = f32_to_bf16_bits(acc[6]) | (f32_to_bf16_bits(acc[7]) << 16);
         *reinterpret_cast<uint4*>(out + (size_t)t * kH + h0) = pk;
     };
-    switch (nr) {    // uniform per workgroup (one token)
-        case 0: body(IntC<0>{}); break;
-        case 1: body(IntC<1>{}); break;
-        case 2: body(IntC<2>{}); break;
-        case 3: body(IntC<3>{}); break;
-        case 4: body(IntC<4>{}); break;
-        case 5: body(IntC<5>{}); break;
-        case 6: body(IntC<6>{}); break;
-        case 7: body(IntC<7>{}); break;
-        default: body(IntC<8>{}); break;
-    }
+    auto rows_of = [&](auto wide_c) {
+        switch (nr) {    // uniform per workgroup (one token)
+            case 0: body(IntC<0>{}, wide_c); break;
+            case 1: body(IntC<1>{}, wide_c); break;
+            case 2: body(IntC<2>{}, wide_c); break;
+            case 3: body(IntC<3>{}, wide_c); break;
+            case 4: body(IntC<4>{}, wide_c); break;
+            case 5: body(IntC<5>{}, wide_c); break;
+            case 6: body(IntC<6>{}, wide_c); break;
+            case 7: body(IntC<7>{}, wide_c); break;
+            default: body(IntC<8>{}, wide_c); break;
+        }
+    };
+    if (__builtin_amdgcn_readfirstlane(*rows_wide) == 0) rows_of(IntC<0>{});
+    else rows_of(IntC<1>{});
 }
 
-void launch_combine(const float* rows_out, const float* sorted_w, const int* inv, int T,
-                    uint16_t* out, hipStream_t stream) {
+void launch_combine(const ExpertRows& rows, const int* rows_wide, const float* sorted_w, const int* inv,
+                    int T, uint16_t* out, hipStream_t stream) {
     if (T <= 0) return;
     constexpr int kParts = kH / (128 * 8);
-    hipLaunchKernelGGL(combine_kernel, dim3((unsigned)T * kParts), dim3(128), 0, stream, rows_out,
-                       sorted_w, inv, T, out);
+    hipLaunchKernelGGL(combine_kernel, dim3((unsigned)T * kParts), dim3(128), 0, stream, rows,
+                       rows_wide, sorted_w, inv, T, out);
 }
 
 }  // namespace moe

@@ -15,8 +15,8 @@
 // on both operands, and receives D[h = 4*(l/16)+v][row = l%16].  A work item's K blocks
 // are split over waves and reduced through LDS in a fixed order.
 // Prefill kernel: FP8 MFMA on the hi/lo form of C (see gemm2_prefill8_kernel).
-// Expert rows O stay fp32 for the combine: rounding them to bf16 first breaks the
-// 1e-2 tolerance where two large expert rows cancel.  The reference re-quantises C to
+// Expert rows O go to the combine in fp16 (ExpertRows: bf16 rows break the 1e-2
+// tolerance where two large expert rows cancel, fp16 rows do not).  The reference re-quantises C to
 // one e4m3 per element (kernel.cu:1086-1145), which does not meet atol = rtol = 1e-2
 // against the fp32 restatement; both forms used here do.
 
@@ -87,11 +87,11 @@ __device__ __forceinline__ v4f mfma_w2_c(uint32_t w0, uint32_t w1, const v4u& c,
 
 // End of a streaming work item: the KSPLIT waves of each column group add their K
 // partials through LDS in a fixed order (so results do not depend on scheduling), and the
-// first of them writes the fp32 expert rows that exist.
+// first of them writes the expert rows that exist (fp16, see ExpertRows).
 template <int KSPLIT, int HF, int CB>
 __device__ __forceinline__ void reduce_store(const v4f (&acc)[HF][CB], v4f (*red)[HF][CB][64], int wave,
                                              int lane, int ks, int row0, int nrows, int hg,
-                                             float* __restrict__ out_rows) {
+                                             const ExpertRows& rows, int* __restrict__ rows_wide) {
     const int r16 = lane & 15, kq = lane >> 4;
 #pragma unroll
     for (int hf = 0; hf < HF; ++hf)
@@ -107,7 +107,7 @@ __device__ __forceinline__ void reduce_store(const v4f (&acc)[HF][CB], v4f (*red
                     v4f o = red[wave][hf][c][lane];
 #pragma unroll
                     for (int q = 1; q < KSPLIT; ++q) o += red[wave + q][hf][c][lane];
-                    *reinterpret_cast<v4f*>(out_rows + (size_t)(row0 + 16 * c + r16) * kH + (hg + hf) * 16 + kq * 4) = o;
+                    store_rows4(rows, rows_wide, (size_t)(row0 + 16 * c + r16) * kH + (hg + hf) * 16 + kq * 4, o);
                 }
             }
         }
@@ -129,7 +129,7 @@ template <int D, int KSPLIT, int HF, int CB>
 __device__ __forceinline__ void gemm2_rstream_body(
     const uint16_t* __restrict__ inter, const uint8_t* __restrict__ w2,
     const float* __restrict__ s2, const int4* __restrict__ tiles,
-    const int* __restrict__ num_tiles, float* __restrict__ out_rows,
+    const int* __restrict__ num_tiles, const ExpertRows rows, int* __restrict__ rows_wide,
     uint8_t (*slot_lds)[16 * HF * kBlk], v4f (*red)[HF][CB][64]) {
     constexpr int NGW = 4 / KSPLIT;
     constexpr int KB = kIB / KSPLIT;
@@ -234,7 +234,7 @@ __device__ __forceinline__ void gemm2_rstream_body(
             __builtin_amdgcn_sched_barrier(0);
         }
 
-        reduce_store<KSPLIT, HF, CB>(acc, red, wave, lane, ks, row0, nrows, hg, out_rows);
+        reduce_store<KSPLIT, HF, CB>(acc, red, wave, lane, ks, row0, nrows, hg, rows, rows_wide);
     }
 }
 
@@ -246,7 +246,8 @@ template <int KSPLIT, int HF, int CB>
 __device__ __forceinline__ void gemm2_rstream_rare(
     const uint16_t* __restrict__ inter, const uint16_t* __restrict__ inter_bf16,
     const uint8_t* __restrict__ w2, const float* __restrict__ s2, const int4* __restrict__ tiles,
-    const int* __restrict__ num_tiles, float* __restrict__ out_rows, v4f (*red)[HF][CB][64]) {
+    const int* __restrict__ num_tiles, const ExpertRows rows, int* __restrict__ rows_wide,
+    v4f (*red)[HF][CB][64]) {
     constexpr int NGW = 4 / KSPLIT;
     constexpr int KB = kIB / KSPLIT;
     constexpr int kItems = (kH / 16) / (NGW * HF);
@@ -296,21 +297,22 @@ __device__ __forceinline__ void gemm2_rstream_rare(
                     for (int v = 0; v < 4; ++v) acc[hf][c][v] = __builtin_fmaf(t[c][v], sb, acc[hf][c][v]);
             }
         }
-        reduce_store<KSPLIT, HF, CB>(acc, red, wave, lane, ks, row0, nrows, hg, out_rows);
+        reduce_store<KSPLIT, HF, CB>(acc, red, wave, lane, ks, row0, nrows, hg, rows, rows_wide);
     }
 }
 
 template <int D, int KSPLIT, int HF, int CB>
 __global__ __launch_bounds__(256) void gemm2_rstream_kernel(
-    Intermediate C, const int* __restrict__ c_wide, const uint8_t* __restrict__ w2,
+    Intermediate C, int* __restrict__ flags, const uint8_t* __restrict__ w2,
     const float* __restrict__ s2, const int4* __restrict__ tiles,
-    const int* __restrict__ num_tiles, float* __restrict__ out_rows) {
+    const int* __restrict__ num_tiles, ExpertRows rows) {
+    // flags[0]: C beyond the fp16 range (set by GEMM1); flags[1]: an expert row beyond it
     __shared__ __attribute__((aligned(1024))) uint8_t slot_lds[4][16 * HF * kBlk];
     __shared__ v4f red[4][HF][CB][64];
-    if (__builtin_amdgcn_readfirstlane(*c_wide) == 0)
-        gemm2_rstream_body<D, KSPLIT, HF, CB>(C.f16(), w2, s2, tiles, num_tiles, out_rows, slot_lds, red);
+    if (__builtin_amdgcn_readfirstlane(flags[0]) == 0)
+        gemm2_rstream_body<D, KSPLIT, HF, CB>(C.f16(), w2, s2, tiles, num_tiles, rows, flags + 1, slot_lds, red);
     else
-        gemm2_rstream_rare<KSPLIT, HF, CB>(C.f16(), C.bf16(), w2, s2, tiles, num_tiles, out_rows, red);
+        gemm2_rstream_rare<KSPLIT, HF, CB>(C.f16(), C.bf16(), w2, s2, tiles, num_tiles, rows, flags + 1, red);
 }
 
 // Prefill GEMM2 (many tokens per expert): MFMA-bound tiling on FP8 MFMA with C in
@@ -334,7 +336,7 @@ __global__ __launch_bounds__(256) void gemm2_rstream_kernel(
 __global__ __launch_bounds__(512, 1) void gemm2_prefill8_kernel(
     Intermediate C, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
     const int4* __restrict__ tiles, const int* __restrict__ num_tiles,
-    const int* __restrict__ exp_off, float* __restrict__ out_rows) {
+    const int* __restrict__ exp_off, ExpertRows rows, int* __restrict__ rows_wide) {
     constexpr int NS = 2;
     constexpr int BM = 128;
     constexpr int NG = kH / 256;                // 28 column groups
@@ -473,7 +475,7 @@ __global__ __launch_bounds__(512, 1) void gemm2_prefill8_kernel(
             if (r < nrows) {
 #pragma unroll
                 for (int n = 0; n < 4; ++n)
-                    *reinterpret_cast<v4f*>(out_rows + (size_t)(row0 + r) * kH + hg * 256 + 64 * wn + 16 * n + 4 * kq) = acc[s][n];
+                    store_rows4(rows, rows_wide, (size_t)(row0 + r) * kH + hg * 256 + 64 * wn + 16 * n + 4 * kq, acc[s][n]);
             }
         }
     }
@@ -507,27 +509,27 @@ static int grid_for2(long long work) { return (int)(work < 4096 ? work : 4096); 
 //   5  the same kernel over the 128-row second tile list of a 256-row dispatch    hi/lo
 bool launch_gemm2(int variant, const Intermediate& C, const uint8_t* w2, const float* s2,
                   const int4* tiles, const int* num_tiles, const int* exp_off, int max_tiles,
-                  float* out_rows, hipStream_t stream) {
-    const int* c_wide = exp_off + kCWideFlag;
+                  const ExpertRows& rows, hipStream_t stream) {
+    int* flags = const_cast<int*>(exp_off) + kCWideFlag;   // [C beyond fp16, rows beyond fp16]
     const long long mt = max_tiles;
     constexpr int G = kH / 16;      // 16-column groups
     switch (variant) {
         case 1:
             hipLaunchKernelGGL((gemm2_rstream_kernel<4, 4, 2, 1>), dim3(grid_for2(mt * G / 2)), dim3(256), 0,
-                               stream, C, c_wide, w2, s2, tiles, num_tiles, out_rows);
+                               stream, C, flags, w2, s2, tiles, num_tiles, rows);
             return true;
         case 2:
             hipLaunchKernelGGL((gemm2_rstream_kernel<3, 4, 4, 1>), dim3(grid_for2(mt * G / 4)), dim3(256), 0,
-                               stream, C, c_wide, w2, s2, tiles, num_tiles, out_rows);
+                               stream, C, flags, w2, s2, tiles, num_tiles, rows);
             return true;
         case 3:
             hipLaunchKernelGGL((gemm2_rstream_kernel<3, 4, 4, 2>), dim3(grid_for2(mt * G / 4)), dim3(256), 0,
-                               stream, C, c_wide, w2, s2, tiles, num_tiles, out_rows);
+                               stream, C, flags, w2, s2, tiles, num_tiles, rows);
             return true;
         case 4:
         case 5:
             hipLaunchKernelGGL(gemm2_prefill8_kernel, dim3(256), dim3(512), 0, stream, C, w2, s2, tiles,
-                               num_tiles, exp_off, out_rows);
+                               num_tiles, exp_off, rows, flags + 1);
             return true;
         default: return false;
     }

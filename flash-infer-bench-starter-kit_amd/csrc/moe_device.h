@@ -184,7 +184,37 @@ __device__ __forceinline__ void bdma4(__amdgpu_buffer_rsrc_t r, uint32_t voff, u
 //     of the region, lo the next; the scales are fp32 [16, rows_cap] (block-major,
 //     so a tile's rows are contiguous).
 constexpr int kCWideFlag = kEL + 3;    // meta word: C exceeds the fp16 range
+constexpr int kRowsWideFlag = kEL + 4; // meta word: an expert row exceeds the fp16 range
 constexpr float kF16Max = 65504.f;
+
+// GEMM2's output, one row of 7168 per routed assignment, read by the combine: fp16
+// rows (11 significant bits keep the combine's result as close to the fp32 sums as
+// fp32 rows do, at half the bytes; bf16 rows were tried and break the 1e-2 tolerance
+// where large rows cancel).  A group of 4 values with one beyond the fp16 range is
+// also written in fp32 to `f32` (same [rows, 7168] indexing) and raises the flag word
+// meta[kRowsWideFlag]; the combine then takes those copies where the fp16 value is
+// infinite.
+struct ExpertRows {
+    uint16_t* f16;
+    float* f32;
+};
+
+// Four consecutive values of an expert row (element offset `off`).
+__device__ __forceinline__ void store_rows4(const ExpertRows& rows, int* __restrict__ wide_flag,
+                                            size_t off, const v4f& o) {
+    uint32_t h[4];
+    bool wide = false;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        h[v] = __builtin_bit_cast(uint16_t, (_Float16)o[v]);
+        wide = wide || fabsf(o[v]) > kF16Max;
+    }
+    *reinterpret_cast<uint2*>(rows.f16 + off) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+    if (wide) {
+        *reinterpret_cast<v4f*>(rows.f32 + off) = o;
+        *wide_flag = 1;
+    }
+}
 
 struct Intermediate {
     void* base;

@@ -95,8 +95,9 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
                                                     int* __restrict__ clear_word) {
     const int lane = threadIdx.x & 63;
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-    // the forward's per-call flag word (GEMM1 sets it, GEMM2 reads it) starts at 0
-    if (clear_word != nullptr && blockIdx.x == 0 && threadIdx.x == 0) *clear_word = 0;
+    // the forward's two per-call flag words (C and expert rows beyond the fp16 range, set
+    // by GEMM1 and GEMM2, read by GEMM2 and the combine) start at 0
+    if (clear_word != nullptr && blockIdx.x == 0 && threadIdx.x < 2) clear_word[threadIdx.x] = 0;
     if (t >= T) return;  // uniform per wave
 
     const float4 lg = reinterpret_cast<const float4*>(logits + (size_t)t * kEG)[lane];
@@ -187,7 +188,7 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
     }
 }
 
-// clear_word (may be null): an int the kernel sets to 0 for the kernels after it.
+// clear_word (may be null): two ints the kernel sets to 0 for the kernels after it.
 void launch_route(const float* logits, const uint16_t* bias, int T, float factor,
                   int* topk_ids, float* topk_w, int* clear_word, hipStream_t stream) {
     if (T <= 0) return;

@@ -154,7 +154,8 @@ typedef struct moe_mi355_workspace_layout {
     size_t inverse_rows;    /* int32 [T,8] */
     size_t meta;            /* int32 [64]: [0..32] expert offsets, [33] num tiles,
                                [34] tiles of the second list (256-row plans),
-                               [35] nonzero when C went beyond the fp16 range (format 0) */
+                               [35] nonzero when C went beyond the fp16 range (format 0),
+                               [36] nonzero when an expert row did */
     size_t tiles;           /* int32 [2*max_tiles,4]: the tile list, then (256-row
                                plans) a second list of 128-row tiles for GEMM2 */
     size_t sorted_tokens;   /* int32 [8T] */
@@ -168,7 +169,9 @@ typedef struct moe_mi355_workspace_layout {
                                1: fp8 hi/lo: e4m3 hi [8T, 2048] then e4m3 lo [8T, 2048],
                                   C = s * (hi + lo / 16) with s from intermediate_scales */
     size_t intermediate_scales; /* fp32 [16, 8T]: s of row r, 128-column block b at [b][r] */
-    size_t expert_out;      /* fp32  [8T, 7168]  GEMM2 output rows */
+    size_t expert_out;      /* fp16  [8T, 7168]  GEMM2 output rows */
+    size_t expert_out_wide; /* fp32  [8T, 7168]  copies of the 4-value groups of expert rows
+                               with a value beyond the fp16 range (meta[36] set) */
     size_t total;
     int32_t tile_m;
     int32_t max_tiles;

@@ -238,14 +238,16 @@ def swiglu_rows(hidden_states, hidden_states_scale, gemm1_weights, gemm1_weights
 def expert_forward(hidden_states, hidden_states_scale, gemm1_weights, gemm1_weights_scale,
                    gemm2_weights, gemm2_weights_scale, ids, w, offset: int,
                    tokens: Optional[Sequence[int]] = None,
-                   intermediate_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+                   intermediate_dtype: torch.dtype = torch.float32,
+                   rows_dtype: torch.dtype = torch.float32) -> torch.Tensor:
     """fp32 accumulator ``acc`` [len(tokens) or T, H] before the bf16 cast.
 
     ``tokens`` restricts the computation to a subset of tokens (each output row
     depends only on its own token, so a subset is an exact restatement for those
     rows).  ``intermediate_dtype`` rounds C = silu(x2)*x1 before GEMM2 (fp32 = the
-    reference; bf16, float8 or "hilo" (``hilo_split``) study the precision of the
-    forms the GPU path keeps C in)."""
+    reference; bf16, fp16, float8 or "hilo" (``hilo_split``) study the precision of
+    the forms the GPU path keeps C in); ``rows_dtype`` likewise rounds each expert's
+    output row O before the weighted sum (fp32 = the reference)."""
     ids = torch.as_tensor(_np(ids)).to(torch.int64)
     wt = torch.as_tensor(_np(w)).to(torch.float32)
     T = ids.shape[0]
@@ -273,6 +275,8 @@ def expert_forward(hidden_states, hidden_states_scale, gemm1_weights, gemm1_weig
         elif intermediate_dtype != torch.float32:
             C = C.to(intermediate_dtype).to(torch.float32)
         O = C @ W2.t()
+        if rows_dtype != torch.float32:
+            O = O.to(rows_dtype).to(torch.float32)
         wk = (sub_w[sel] * hit[sel].to(torch.float32)).sum(dim=1, keepdim=True)
         acc.index_add_(0, sel, O * wk)
     return acc
