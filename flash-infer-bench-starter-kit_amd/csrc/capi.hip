@@ -46,12 +46,13 @@ constexpr int kMinTileM = 16;           // smallest row tile; sizes the tile lis
 // Kernel plan per token count: the dispatch tile height and the GEMM1 / GEMM2 variants
 // (ids of launch_gemm1 / launch_gemm2).  Small T streams weights with the
 // register-staged kernels, C in fp16: 16-row tiles up to T = 192 (GEMM2 with 32 output
-// columns per wave up to T = 96, 64 beyond), 32-row tiles (GEMM1 with two column
+// columns per wave up to T = 112, 64 beyond), 32-row tiles (GEMM1 with two column
 // groups per wave) up to T = 1152, where an expert gets up to about 36 rows and
-// streams its weights about once.  Large T uses
-// the MFMA-bound prefill kernels (128- or 256-row tiles, C in the fp8 hi/lo form; with
-// 256-row tiles GEMM2 walks the 128-row second tile list).  The boundaries come from
-// sweeps of every pair at T = 96 .. 2048 on MI355X.  MOE_MI355_G1 / MOE_MI355_G2
+// streams its weights about once.  Large T uses the MFMA-bound prefill kernels on
+// 256-row tiles (C in the fp8 hi/lo form; GEMM2 walks the 128-row second tile list);
+// the 128-row prefill pair (variants 3 / 4) stays available to the override.  The
+// boundaries come from wall-clock sweeps of the pairs at T = 64 .. 2560 on MI355X.
+// MOE_MI355_G1 / MOE_MI355_G2
 // override the variants for tuning sweeps; the override is ignored unless both imply
 // the same tile height and the same form of C.
 struct Plan {
@@ -65,10 +66,9 @@ bool g2_hilo(int v) { return v >= 4; }
 
 Plan choose_plan(int32_t T) {
     Plan p;
-    if (T <= 96) p = {16, 1, 1};
+    if (T <= 112) p = {16, 1, 1};
     else if (T <= 192) p = {16, 1, 2};
     else if (T <= 1152) p = {32, 2, 3};
-    else if (T <= 2048) p = {128, 3, 4};
     else p = {256, 4, 5};
     const char* e1 = getenv("MOE_MI355_G1");
     const char* e2 = getenv("MOE_MI355_G2");

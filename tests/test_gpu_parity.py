@@ -171,11 +171,14 @@ def test_forward_routing_in_workspace_is_bit_exact(T):
     assert np.array_equal(arr(lay.inverse_rows, T * 8, torch.int32).reshape(T, 8), r["inv"])
 
 
-@pytest.mark.parametrize("T", [1500, 8192])
-def test_prefill_intermediate_hilo_rows(T):
-    """The prefill GEMM1 kernels (128-row tiles at T=1500, 256-row tiles at T=8192)
-    write C in the fp8 hi/lo form; rebuilt rows match the fp32 SwiGLU of the oracle to
-    within the form's precision (2^-8 relative, plus the fp32 GEMM's own rounding)."""
+@pytest.mark.parametrize("T,g1,g2", [(1500, 3, 4), (1500, 4, 5), (8192, 4, 5)])
+def test_prefill_intermediate_hilo_rows(T, g1, g2, monkeypatch):
+    """The prefill GEMM1 kernels (128-row tiles, forced through MOE_MI355_G1 / _G2, and
+    the default 256-row tiles) write C in the fp8 hi/lo form; rebuilt rows match the fp32
+    SwiGLU of the oracle to within the form's precision (2^-8 relative, plus the fp32
+    GEMM's own rounding)."""
+    monkeypatch.setenv("MOE_MI355_G1", str(g1))
+    monkeypatch.setenv("MOE_MI355_G2", str(g2))
     k = pkg("kernel")
     o = oracle()
     wl = pkg("workloads")
