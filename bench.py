@@ -279,9 +279,10 @@ def main() -> int:
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": ("fp8_e4m3 GEMM1 + fp8 hi/lo GEMM2 (two FP8 MFMAs per product), fp32 accumulate"
-                  if k.workspace_layout(T).intermediate_format == 1 else
-                  "fp8_e4m3 GEMM1 + fp16 GEMM2 (W2 widened exactly), fp32 accumulate"),
+        "dtype": {0: "fp8_e4m3 GEMM1 + fp16 GEMM2 (W2 widened exactly), fp32 accumulate",
+                  1: "fp8_e4m3 GEMM1 + fp8 hi/lo GEMM2 (two FP8 MFMAs per product), fp32 accumulate",
+                  2: "fp8_e4m3 GEMM1 (fp16 C, converted to fp8 hi/lo) + fp8 hi/lo GEMM2, "
+                     "fp32 accumulate"}[k.workspace_layout(T).intermediate_format],
         "data": "synthetic (seeded N(0,1) logits/hidden, N(0,0.02) weights, block-quantised)",
         "config": {"workload": cfg.name, "T": T, "local_expert_offset": cfg.local_expert_offset,
                    "routed_scaling_factor": cfg.routed_scaling_factor,

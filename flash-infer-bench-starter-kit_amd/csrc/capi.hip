@@ -8,6 +8,7 @@
 //   route    (T/4 workgroups)      -> topk ids / weights
 //   dispatch (1 workgroup)         -> expert offsets, row tiles, permutation, inverse map
 //   gemm1    (persistent)          -> SwiGLU rows C      [N_a, 2048] (fp16 or fp8 hi/lo)
+//   (cform   (persistent)          -> fp16 C as hi/lo, for the plans that need it)
 //   gemm2    (persistent)          -> fp16 expert rows   [N_a, 7168]
 //   combine  (7 T workgroups)      -> bf16 output        [T, 7168]
 // The GEMM grids are sized from the host-known bound on the tile count; each
@@ -22,7 +23,7 @@
 
 namespace moe {
 void launch_route(const float*, const uint16_t*, int, float, int*, float*, int*, hipStream_t);
-bool launch_dispatch(const int*, const float*, int, int, int, int*, int*, int4*, int*, float*,
+bool launch_dispatch(const int*, const float*, int, int, int, int, int*, int*, int4*, int*, float*,
                      int*, int*, hipStream_t, int*, int4*);
 int dispatch_max_tiles(int T, int tm);
 bool launch_gemm1(int, const uint8_t*, const float*, int, const uint8_t*, const float*,
@@ -32,6 +33,7 @@ bool launch_gemm2(int, const Intermediate&, const uint8_t*, const float*, const 
                   const int*, int, const ExpertRows&, hipStream_t);
 void launch_combine(const ExpertRows&, const int*, const float*, const int*, int, uint16_t*, hipStream_t);
 void launch_e4m3_to_bf16(const uint8_t*, uint16_t*, int, hipStream_t);
+void launch_c_f16_to_hilo(const Intermediate&, const int*, hipStream_t);
 void launch_e4m3_to_f16(const uint8_t*, uint16_t*, int, hipStream_t);
 void launch_quantize_fp8_blockwise(const void*, int, int, int, uint8_t*, float*, hipStream_t);
 }  // namespace moe
@@ -43,40 +45,61 @@ namespace {
 constexpr int32_t kMaxT = 1 << 19;
 constexpr int kMinTileM = 16;           // smallest row tile; sizes the tile list
 
-// Kernel plan per token count: the dispatch tile height and the GEMM1 / GEMM2 variants
-// (ids of launch_gemm1 / launch_gemm2).  Small T streams weights with the
-// register-staged kernels, C in fp16: 16-row tiles up to T = 192 (GEMM2 with 32 output
-// columns per wave up to T = 112, 64 beyond), 32-row tiles (GEMM1 with two column
-// groups per wave) up to T = 1152, where an expert gets up to about 36 rows and
-// streams its weights about once.  Large T uses the MFMA-bound prefill kernels on
-// 256-row tiles (C in the fp8 hi/lo form; GEMM2 walks the 128-row second tile list);
-// the 128-row prefill pair (variants 3 / 4) stays available to the override.  The
-// boundaries come from wall-clock sweeps of the pairs at T = 64 .. 2560 on MI355X.
-// MOE_MI355_G1 / MOE_MI355_G2
-// override the variants for tuning sweeps; the override is ignored unless both imply
-// the same tile height and the same form of C.
+// Kernel plan per token count: the GEMM1 / GEMM2 variants (ids of launch_gemm1 /
+// launch_gemm2) and what they imply: the tile height of the dispatch's first list (the
+// GEMM1's), an optional second list of 128-row tiles (GEMM2 variant 5), and whether the
+// fp16 C of a streaming GEMM1 is converted to the hi/lo form for a prefill GEMM2.
+// Small T streams weights with the register-staged kernels, C in fp16: 16-row tiles up
+// to T = 192 (GEMM2 with 32 output columns per wave up to T = 112, 64 beyond), 32-row
+// tiles (GEMM1 with two column groups per wave) beyond, where an expert gets up to
+// about 36 rows at T = 1152 and streams its weights about once.  From T = 705 the
+// streaming GEMM1 feeds the prefill GEMM2 (128-row tiles, FP8 MFMA on the hi/lo form),
+// the faster GEMM2 there; from T = 1409 both GEMMs are the MFMA-bound prefill kernels
+// on 256-row tiles (GEMM2 on the 128-row second list).  The 128-row prefill pair
+// (variants 3 / 4) stays available to the override.  The boundaries come from
+// wall-clock sweeps of the pairs at T = 64 .. 2560 on MI355X.  MOE_MI355_G1 /
+// MOE_MI355_G2 override the variants for tuning sweeps; a pair that cannot run together
+// is ignored.
 struct Plan {
-    int tm, g1, g2;
+    int tm;        // tile height of the first list
+    int tm2;       // tile height of the second list (0: none)
+    int g1, g2;
+    bool convert;  // fp16 C converted to the hi/lo form between the GEMMs
 };
 
 int g1_tile_m(int v) { return v == 1 ? 16 : v == 2 ? 32 : v == 3 ? 128 : 256; }
-int g2_tile_m(int v) { return v <= 2 ? 16 : v == 3 ? 32 : v == 4 ? 128 : 256; }
-bool g1_hilo(int v) { return v >= 3; }
-bool g2_hilo(int v) { return v >= 4; }
+bool g1_hilo(int v) { return v >= 3; }        // GEMM1 writes the hi/lo form
+bool g2_hilo(int v) { return v >= 4; }        // GEMM2 reads the hi/lo form
+
+// The plan of a GEMM1 / GEMM2 pair, false when they cannot run together.
+bool make_plan(int g1, int g2, Plan* p) {
+    if (g1 < 1 || g1 > 4 || g2 < 1 || g2 > 5) return false;
+    const int tm = g1_tile_m(g1);
+    if (g1_hilo(g1) && !g2_hilo(g2)) return false;      // the fp16 GEMM2s need fp16 C
+    if (g2 == 5) {                                       // the second list, 128-row tiles
+        if (tm != 16 && tm != 32 && tm != 256) return false;
+        *p = {tm, 128, g1, g2, !g1_hilo(g1)};
+        return true;
+    }
+    const int tm_g2 = g2 <= 2 ? 16 : g2 == 3 ? 32 : 128;
+    if (tm_g2 != tm) return false;
+    *p = {tm, 0, g1, g2, g1_hilo(g1) != g2_hilo(g2)};
+    return true;
+}
 
 Plan choose_plan(int32_t T) {
+    int g1, g2;
+    if (T <= 112) g1 = 1, g2 = 1;
+    else if (T <= 192) g1 = 1, g2 = 2;
+    else if (T <= 704) g1 = 2, g2 = 3;
+    else if (T <= 1408) g1 = 2, g2 = 5;
+    else g1 = 4, g2 = 5;
     Plan p;
-    if (T <= 112) p = {16, 1, 1};
-    else if (T <= 192) p = {16, 1, 2};
-    else if (T <= 1152) p = {32, 2, 3};
-    else p = {256, 4, 5};
+    make_plan(g1, g2, &p);
     const char* e1 = getenv("MOE_MI355_G1");
     const char* e2 = getenv("MOE_MI355_G2");
-    const int env_g1 = e1 ? atoi(e1) : 0;
-    const int env_g2 = e2 ? atoi(e2) : 0;
-    if (env_g1 >= 1 && env_g1 <= 4 && env_g2 >= 1 && env_g2 <= 5 &&
-        g1_tile_m(env_g1) == g2_tile_m(env_g2) && g1_hilo(env_g1) == g2_hilo(env_g2))
-        p = {g1_tile_m(env_g1), env_g1, env_g2};
+    Plan q;
+    if (e1 && e2 && make_plan(atoi(e1), atoi(e2), &q)) p = q;
     return p;
 }
 
@@ -102,7 +125,7 @@ bool fill_layout(int32_t T, moe_mi355_workspace_layout* L) {
     L->sorted_tokens = take(R * 4);
     L->sorted_weights = take(R * 4);
     L->chunk_counts = take((size_t)((T + 255) / 256) * moe::kEL * 4);
-    L->intermediate = take(R * moe::kI * 4);
+    L->intermediate = take(R * moe::kI * 6);     // hi/lo, fp16, bf16 copies
     L->intermediate_scales = take(R * moe::kIB * 4);
     L->expert_out = take(R * moe::kH * 2);
     L->expert_out_wide = take(R * moe::kH * 4);
@@ -110,7 +133,7 @@ bool fill_layout(int32_t T, moe_mi355_workspace_layout* L) {
     const Plan plan = choose_plan(T);
     L->tile_m = plan.tm;
     L->max_tiles = mt;
-    L->intermediate_format = g1_hilo(plan.g1) ? 1 : 0;
+    L->intermediate_format = g1_hilo(plan.g1) ? 1 : plan.convert ? 2 : 0;
     return true;
 }
 
@@ -216,7 +239,7 @@ int moe_mi355_dispatch(const int32_t* topk_ids, const float* topk_weights, int32
     if (!aligned16(tiles) || !aligned16(topk_ids) || !aligned16(topk_weights))
         return MOE_ERR_MISALIGNED;
     hipStream_t s = (hipStream_t)stream;
-    moe::launch_dispatch(topk_ids, topk_weights, T, clamp_offset(local_expert_offset), tile_m,
+    moe::launch_dispatch(topk_ids, topk_weights, T, clamp_offset(local_expert_offset), tile_m, 0,
                          expert_offsets, num_tiles, reinterpret_cast<int4*>(tiles), sorted_tokens,
                          sorted_weights, inverse_rows, chunk_counts, s, nullptr, nullptr);
     return hip_status(hipGetLastError());
@@ -266,20 +289,20 @@ int moe_mi355_forward(const moe_mi355_args* a, void* stream) {
     if (prof) prof_record(slot, 1, s);
     const Plan plan = choose_plan(T);
     const int max_tiles = moe::dispatch_max_tiles(T, plan.tm);
-    // GEMM2 variant 5 walks the half-height (128-row) tiles of a 256-row dispatch
-    const bool half = plan.g2 == 5;
+    const bool half = plan.tm2 > 0;   // GEMM2 walks the second (128-row) tile list
     int4* tiles2 = tiles + max_tiles;
     int* num_tiles2 = meta + moe::kEL + 2;
-    moe::launch_dispatch(ids, wts, T, clamp_offset(a->local_expert_offset), plan.tm, meta,
+    moe::launch_dispatch(ids, wts, T, clamp_offset(a->local_expert_offset), plan.tm, plan.tm2, meta,
                          num_tiles, tiles, stok, sw, inv, chunk_cnt, s, half ? num_tiles2 : nullptr,
                          half ? tiles2 : nullptr);
     if (prof) prof_record(slot, 2, s);
     moe::launch_gemm1(plan.g1, a->hidden_states, a->hidden_states_scale, T, a->gemm1_weights,
                       a->gemm1_weights_scale, tiles, num_tiles, meta, max_tiles, stok, inter, s);
     if (prof) prof_record(slot, 3, s);
+    if (plan.convert) moe::launch_c_f16_to_hilo(inter, meta, s);   // counted in the GEMM2 stage
     if (half)
         moe::launch_gemm2(plan.g2, inter, a->gemm2_weights, a->gemm2_weights_scale, tiles2,
-                          num_tiles2, meta, moe::dispatch_max_tiles(T, plan.tm / 2), rows, s);
+                          num_tiles2, meta, moe::dispatch_max_tiles(T, plan.tm2), rows, s);
     else
         moe::launch_gemm2(plan.g2, inter, a->gemm2_weights, a->gemm2_weights_scale, tiles,
                           num_tiles, meta, max_tiles, rows, s);

@@ -100,18 +100,18 @@ __device__ __forceinline__ void place(const TokenRoutes& r, const int* rank, int
 }
 
 // expert offsets, tile list and tile count from the per-expert totals (wave 0).
-// With tiles2 set, also a second list of tiles of TM/2 rows (num_tiles2 = its count):
-// the prefill GEMM2 walks finer tiles than the GEMM1 over the same rows.
-template <int TM>
+// With TM2 > 0 (and tiles2 set), also a second list of tiles of TM2 rows over the same
+// rows (num_tiles2 = its count), for a GEMM2 that walks other tiles than the GEMM1.
+template <int TM, int TM2>
 __device__ __forceinline__ void write_offsets_and_tiles(int c, int lane, int* off_lds,
                                                         int* __restrict__ exp_off,
                                                         int* __restrict__ num_tiles,
                                                         int4* __restrict__ tiles,
                                                         int* __restrict__ num_tiles2,
                                                         int4* __restrict__ tiles2) {
-    constexpr int TM2 = TM / 2;
+    constexpr int TM2r = TM2 > 0 ? TM2 : TM;
     const int nt = (c + TM - 1) / TM;
-    const int nt2 = (c + TM2 - 1) / TM2;
+    const int nt2 = (c + TM2r - 1) / TM2r;
     const int ci = scan32(c, lane);
     const int ti = scan32(nt, lane);
     const int ti2 = scan32(nt2, lane);
@@ -120,22 +120,22 @@ __device__ __forceinline__ void write_offsets_and_tiles(int c, int lane, int* of
         off_lds[lane] = o;
         exp_off[lane] = o;
         for (int j = 0; j < nt; ++j) tiles[to + j] = make_int4(lane, o + j * TM, min(TM, c - j * TM), 0);
-        if (tiles2) {
+        if (TM2 > 0 && tiles2) {
             const int to2 = ti2 - nt2;
             for (int j = 0; j < nt2; ++j)
-                tiles2[to2 + j] = make_int4(lane, o + j * TM2, min(TM2, c - j * TM2), 0);
+                tiles2[to2 + j] = make_int4(lane, o + j * TM2r, min(TM2r, c - j * TM2r), 0);
         }
     }
     if (lane == kEL - 1) {
         exp_off[kEL] = ci;
         *num_tiles = ti;
-        if (tiles2) *num_tiles2 = ti2;
+        if (TM2 > 0 && tiles2) *num_tiles2 = ti2;
     }
 }
 
 // T <= 1024: one workgroup of NW waves (64 NW >= T), one token per thread, one pass
 // over the routes.
-template <int TM, int NW>
+template <int TM, int TM2, int NW>
 __global__ __launch_bounds__(64 * NW) void dispatch_small_kernel(
     const int* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int offset,
     int* __restrict__ exp_off, int* __restrict__ num_tiles, int4* __restrict__ tiles,
@@ -154,8 +154,8 @@ __global__ __launch_bounds__(64 * NW) void dispatch_small_kernel(
         int c = 0;
         if (lane < kEL)
             for (int w = 0; w < NW; ++w) c += wcnt[w][lane];
-        write_offsets_and_tiles<TM>(lane < kEL ? c : 0, lane, off, exp_off, num_tiles, tiles,
-                                    num_tiles2, tiles2);
+        write_offsets_and_tiles<TM, TM2>(lane < kEL ? c : 0, lane, off, exp_off, num_tiles, tiles,
+                                         num_tiles2, tiles2);
     }
     __syncthreads();
     if (tid < kEL) {
@@ -193,7 +193,7 @@ __global__ __launch_bounds__(kChunk) void dispatch_count_kernel(
 // chunk count table (thread t sums expert t % 32 over chunks = t / 32 mod 8, then the
 // eight partial sums are added in a fixed order), places its tokens; chunk 0 also
 // writes offsets and tiles.
-template <int TM>
+template <int TM, int TM2>
 __global__ __launch_bounds__(kChunk) void dispatch_place_kernel(
     const int* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int offset,
     const int* __restrict__ chunk_cnt, int nchunks, int* __restrict__ exp_off,
@@ -233,8 +233,8 @@ __global__ __launch_bounds__(kChunk) void dispatch_place_kernel(
             }
         }
         if (chunk == 0) {
-            write_offsets_and_tiles<TM>(lane < kEL ? total : 0, lane, off, exp_off, num_tiles, tiles,
-                                        num_tiles2, tiles2);
+            write_offsets_and_tiles<TM, TM2>(lane < kEL ? total : 0, lane, off, exp_off, num_tiles, tiles,
+                                             num_tiles2, tiles2);
         } else {
             const int ci = scan32(lane < kEL ? total : 0, lane);
             if (lane < kEL) off[lane] = ci - total;
@@ -258,14 +258,14 @@ int dispatch_max_tiles(int T, int tm) {
     return (int)((rows + tm - 1) / tm) + kEL;
 }
 
-template <int TM>
+template <int TM, int TM2>
 static void launch_dispatch_tm(const int* topk_ids, const float* topk_w, int T, int offset,
                                int* exp_off, int* num_tiles, int4* tiles, int* num_tiles2,
                                int4* tiles2, int* sorted_tok, float* sorted_w, int* inv,
                                int* chunk_cnt, hipStream_t stream) {
     if (T <= 1024) {
 #define DISPATCH_SMALL(NW)                                                                        \
-    hipLaunchKernelGGL((dispatch_small_kernel<TM, NW>), dim3(1), dim3(64 * NW), 0, stream,        \
+    hipLaunchKernelGGL((dispatch_small_kernel<TM, TM2, NW>), dim3(1), dim3(64 * NW), 0, stream,   \
                        topk_ids, topk_w, T, offset, exp_off, num_tiles, tiles, num_tiles2, tiles2, \
                        sorted_tok, sorted_w, inv)
         if (T <= 64) DISPATCH_SMALL(1);
@@ -277,27 +277,42 @@ static void launch_dispatch_tm(const int* topk_ids, const float* topk_w, int T, 
     const int nchunks = (T + kChunk - 1) / kChunk;
     hipLaunchKernelGGL(dispatch_count_kernel, dim3(nchunks), dim3(kChunk), 0, stream, topk_ids, topk_w,
                        T, offset, chunk_cnt);
-    hipLaunchKernelGGL(dispatch_place_kernel<TM>, dim3(nchunks), dim3(kChunk), 0, stream, topk_ids,
+    hipLaunchKernelGGL((dispatch_place_kernel<TM, TM2>), dim3(nchunks), dim3(kChunk), 0, stream, topk_ids,
                        topk_w, T, offset, chunk_cnt, nchunks, exp_off, num_tiles, tiles,
                        num_tiles2, tiles2, sorted_tok, sorted_w, inv);
 }
 
-// chunk_cnt: int32 [ceil(T/256) * 32] scratch, needed when T > 1024.  tiles2 /
-// num_tiles2 (may be null): a second tile list of tm/2 rows over the same rows.
-bool launch_dispatch(const int* topk_ids, const float* topk_w, int T, int offset, int tm,
+// chunk_cnt: int32 [ceil(T/256) * 32] scratch, needed when T > 1024.  tm2 > 0 (with
+// tiles2 / num_tiles2): a second tile list of tm2 rows over the same rows.  Tile
+// heights: tm in {16, 32, 64, 128, 256} alone, or the pairs (256, 128), (32, 128) and
+// (16, 128) the kernel plans use.
+bool launch_dispatch(const int* topk_ids, const float* topk_w, int T, int offset, int tm, int tm2,
                      int* exp_off, int* num_tiles, int4* tiles, int* sorted_tok,
                      float* sorted_w, int* inv, int* chunk_cnt, hipStream_t stream,
                      int* num_tiles2, int4* tiles2) {
-#define DISPATCH_TM(TM)                                                                               launch_dispatch_tm<TM>(topk_ids, topk_w, T, offset, exp_off, num_tiles, tiles, num_tiles2,                               tiles2, sorted_tok, sorted_w, inv, chunk_cnt, stream)
+    auto run = [&](auto tm_c, auto tm2_c) {
+        launch_dispatch_tm<decltype(tm_c)::value, decltype(tm2_c)::value>(
+            topk_ids, topk_w, T, offset, exp_off, num_tiles, tiles, num_tiles2, tiles2, sorted_tok,
+            sorted_w, inv, chunk_cnt, stream);
+        return true;
+    };
+    if (tm2 == 0) {
+        switch (tm) {
+            case 16: return run(IntC<16>{}, IntC<0>{});
+            case 32: return run(IntC<32>{}, IntC<0>{});
+            case 64: return run(IntC<64>{}, IntC<0>{});
+            case 128: return run(IntC<128>{}, IntC<0>{});
+            case 256: return run(IntC<256>{}, IntC<0>{});
+            default: return false;
+        }
+    }
+    if (!tiles2 || !num_tiles2 || tm2 != 128) return false;
     switch (tm) {
-        case 16: DISPATCH_TM(16); return true;
-        case 32: DISPATCH_TM(32); return true;
-        case 64: DISPATCH_TM(64); return true;
-        case 128: DISPATCH_TM(128); return true;
-        case 256: DISPATCH_TM(256); return true;
+        case 16: return run(IntC<16>{}, IntC<128>{});
+        case 32: return run(IntC<32>{}, IntC<128>{});
+        case 256: return run(IntC<256>{}, IntC<128>{});
         default: return false;
     }
-#undef DISPATCH_TM
 }
 
 }  // namespace moe

@@ -168,21 +168,23 @@ __device__ __forceinline__ void bdma4(__amdgpu_buffer_rsrc_t r, uint32_t voff, u
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)l, 4, voff, soff, 0, 0);
 }
 
-// The SwiGLU rows C [rows, 2048] between GEMM1 and GEMM2 live in one workspace
-// region (rows_cap x 2048 x 4 bytes) in one of two forms, chosen by the kernel plan:
-//   fp16 (streaming kernels, 16- and 32-row tiles): C rounded to fp16 in the first
+// The SwiGLU rows C [rows, 2048] between GEMM1 and GEMM2 live in one workspace region
+// of rows_cap x 2048 x 6 bytes, in up to two forms chosen by the kernel plan:
+//   fp8 hi/lo (bytes [0, 4 rows_cap) x 512; written by the prefill GEMM1 kernels, or
+//     converted from the fp16 form, and read by the prefill GEMM2 kernel): per row and
+//     128-column block b a scale s = amax/448 and two e4m3 rows hi = e4m3(C/s),
+//     lo = e4m3((C - hi*s) * 16/s), so C ~ s*(hi + lo/16) (GEMM2 then runs two FP8
+//     MFMAs per block, the second with an exact 2^-4 operand scale).  hi occupies the
+//     first rows_cap*2048 bytes, lo the next; the scales are fp32 [16, rows_cap]
+//     (block-major, so a tile's rows are contiguous).
+//   fp16 (written by the streaming GEMM1 kernels): C rounded to fp16 in the next
 //     rows_cap*2048 halves.  fp16 keeps 11 significant bits, and so GEMM2 adds no
 //     error that matters next to the bf16 output rounding (bf16 C, 8 bits, reaches
 //     the 1e-2 tolerance on tokens whose 8 experts are all local).  For a group of 4
 //     values with one beyond the fp16 range, GEMM1 also writes the group in bf16 to
-//     the next rows_cap*2048 halves and raises the flag word meta[kCWideFlag];
-//     GEMM2 then runs on bf16, taking those copies where the fp16 value is infinite;
-//   fp8 hi/lo (prefill kernels): per row and 128-column block b a scale
-//     s = amax/448 and two e4m3 rows hi = e4m3(C/s), lo = e4m3((C - hi*s) * 16/s),
-//     so C ~ s*(hi + lo/16) (GEMM2 then runs two FP8 MFMAs per block, the second
-//     with an exact 2^-4 operand scale).  hi occupies the first rows_cap*2048 bytes
-//     of the region, lo the next; the scales are fp32 [16, rows_cap] (block-major,
-//     so a tile's rows are contiguous).
+//     the last rows_cap*2048 halves and raises the flag word meta[kCWideFlag]; the
+//     kernels that read fp16 C then take those copies where the fp16 value is
+//     infinite.
 constexpr int kCWideFlag = kEL + 3;    // meta word: C exceeds the fp16 range
 constexpr int kRowsWideFlag = kEL + 4; // meta word: an expert row exceeds the fp16 range
 constexpr float kF16Max = 65504.f;
@@ -220,9 +222,11 @@ struct Intermediate {
     void* base;
     float* scales;
     int rows_cap;
-    __host__ __device__ uint16_t* f16() const { return static_cast<uint16_t*>(base); }
-    __host__ __device__ uint16_t* bf16() const {
+    __host__ __device__ uint16_t* f16() const {
         return static_cast<uint16_t*>(base) + (size_t)rows_cap * kI;
+    }
+    __host__ __device__ uint16_t* bf16() const {
+        return static_cast<uint16_t*>(base) + 2 * (size_t)rows_cap * kI;
     }
     __host__ __device__ uint8_t* hi() const { return static_cast<uint8_t*>(base); }
     __host__ __device__ uint8_t* lo() const {

@@ -161,13 +161,14 @@ typedef struct moe_mi355_workspace_layout {
     size_t sorted_tokens;   /* int32 [8T] */
     size_t sorted_weights;  /* fp32  [8T] */
     size_t chunk_counts;    /* int32 [ceil(T/256), 32] dispatch scratch */
-    size_t intermediate;    /* SwiGLU output rows C, 8T x 2048 x 4 bytes, in one of two
-                               forms (intermediate_format):
-                               0: fp16 [8T, 2048], then bf16 [8T, 2048] holding copies
-                                  of the 4-value groups with a value beyond the fp16
-                                  range (meta[35] set: GEMM2 then runs on bf16);
-                               1: fp8 hi/lo: e4m3 hi [8T, 2048] then e4m3 lo [8T, 2048],
-                                  C = s * (hi + lo / 16) with s from intermediate_scales */
+    size_t intermediate;    /* SwiGLU output rows C, 8T x 2048 x 6 bytes:
+                               e4m3 hi [8T, 2048], e4m3 lo [8T, 2048]  (hi/lo form:
+                                  C = s * (hi + lo / 16), s from intermediate_scales),
+                               fp16 [8T, 2048]                          (fp16 form),
+                               bf16 [8T, 2048]  copies of the 4-value groups of the fp16
+                                  form with a value beyond the fp16 range (meta[35] set).
+                               intermediate_format: 0 fp16 form, 1 hi/lo form, 2 fp16
+                               form converted to the hi/lo form before GEMM2 */
     size_t intermediate_scales; /* fp32 [16, 8T]: s of row r, 128-column block b at [b][r] */
     size_t expert_out;      /* fp16  [8T, 7168]  GEMM2 output rows */
     size_t expert_out_wide; /* fp32  [8T, 7168]  copies of the 4-value groups of expert rows

@@ -54,7 +54,7 @@ def test_workspace_bytes(lib):
             lay.sorted_tokens, lay.sorted_weights, lay.chunk_counts, lay.intermediate, lay.expert_out,
             lay.expert_out_wide]
     assert offs == sorted(offs) and all(o % 256 == 0 for o in offs)
-    assert lay.intermediate + 64 * 8 * 2048 * 4 <= lay.intermediate_scales   # fp16 C + bf16 copies
+    assert lay.intermediate + 64 * 8 * 2048 * 6 <= lay.intermediate_scales   # hi/lo, fp16, bf16 copies
     assert lay.expert_out + 64 * 8 * 7168 * 2 <= lay.expert_out_wide         # fp16 expert rows
     assert lay.expert_out_wide + 64 * 8 * 7168 * 4 <= lay.total              # their fp32 copies
     assert lay.max_tiles == (64 * 8 + 15) // 16 + 32   # sized for the smallest tile height

@@ -107,12 +107,12 @@ def test_small_odd_batches(T):
     assert st["frac_within"] == 1.0, st
 
 
-@pytest.mark.parametrize("T", [112, 113, 192, 193, 1024, 1025, 1152, 1153])
+@pytest.mark.parametrize("T", [112, 113, 192, 193, 704, 705, 1024, 1025, 1408, 1409])
 def test_plan_boundaries_match_oracle(T):
     """Token counts on both sides of every change of kernel plan (16-row streaming
-    with 32 then 64 GEMM2 columns per wave, 32-row streaming, 256-row prefill tiles)
-    and of the dispatch (one workgroup up to T = 1024, count and place kernels over
-    256-token chunks beyond)."""
+    with 32 then 64 GEMM2 columns per wave, 32-row streaming, 32-row streaming GEMM1
+    with the prefill GEMM2, 256-row prefill tiles) and of the dispatch (one workgroup
+    up to T = 1024, count and place kernels over 256-token chunks beyond)."""
     d = first_tokens(config_inputs(3), T)
     note(f"[gpu] plan boundary T={T}")
     out = run_forward(d)
@@ -124,7 +124,8 @@ def test_plan_boundaries_match_oracle(T):
 
 
 @pytest.mark.parametrize("T,g1,g2", [(64, 1, 1), (64, 1, 2), (150, 1, 2), (64, 2, 3),
-                                     (500, 2, 3), (1000, 3, 4), (3000, 4, 5)])
+                                     (500, 2, 3), (1000, 3, 4), (3000, 4, 5), (1000, 2, 5),
+                                     (150, 1, 5)])
 def test_every_gemm_variant_matches_oracle(T, g1, g2, monkeypatch):
     """Each GEMM1 / GEMM2 kernel variant (forced with MOE_MI355_G1 / _G2, which the
     library reads on every call) stays within the tolerance."""
@@ -225,6 +226,15 @@ def test_values_beyond_fp16_range_streaming_plan():
     _huge_inputs_check(d, c_flag=1)
 
 
+def test_values_beyond_fp16_range_converted_plan():
+    """T = 1024 (streaming GEMM1, fp16 C converted to the hi/lo form for the prefill
+    GEMM2): the conversion takes GEMM1's bf16 copies of the values beyond the fp16
+    range."""
+    d = first_tokens(config_inputs(3), 1024)
+    note("[gpu] values beyond the fp16 range, T=1024")
+    _huge_inputs_check(d, c_flag=1)
+
+
 def test_values_beyond_fp16_range_prefill_plan():
     """T = 1500 (prefill plan, fp8 hi/lo C, whose per-block scale covers any range):
     only the expert rows overflow fp16."""
@@ -235,7 +245,7 @@ def test_values_beyond_fp16_range_prefill_plan():
 
 def test_large_batch_matches_oracle_and_is_deterministic():
     """T = 32768 (4x the largest benchmark config; 262,144 routed rows, 256 dispatch
-    chunks, a 13 GB workspace): sampled tokens match the oracle and two calls agree
+    chunks, a 15 GB workspace): sampled tokens match the oracle and two calls agree
     bit for bit."""
     k = pkg("kernel")
     wl = pkg("workloads")
