@@ -135,13 +135,14 @@ def test_forward_matches_oracle(idx):
     assert st["frac_within"] == 1.0, st
 
 
-@pytest.mark.parametrize("T", [1, 8, 13, 16, 17, 1024])
+@pytest.mark.parametrize("T", [1, 8, 13, 16, 17, 64, 65, 1024])
 def test_forward_routing_in_workspace_is_bit_exact(T):
     """The routing and dispatch a forward call leaves in its workspace (ids, weights,
     expert offsets, tile list, permutation, inverse map) equal the oracle's bit for
-    bit (config 1 sliced to T, config 2 at its full 1024 tokens)."""
+    bit (config 1 sliced to T, config 2 sliced to 65 and at its full 1024 tokens;
+    the dispatch runs on one wave up to T = 64 and on four from 65 on)."""
     k = pkg("kernel")
-    d = config_inputs(2) if T == 1024 else first_tokens(config_inputs(1), T)
+    d = first_tokens(config_inputs(1 if T <= 64 else 2), T)
     lay = k.workspace_layout(T)
     ws = torch.empty(lay.total, dtype=torch.uint8, device="cuda")
     wl = pkg("workloads")
