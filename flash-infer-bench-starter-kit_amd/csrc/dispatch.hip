@@ -68,18 +68,31 @@ __device__ __forceinline__ TokenRoutes load_routes(const int* __restrict__ topk_
 }
 
 // For each expert e: the wave's count into wcnt[wave][e]; returns in rank[k] this
-// lane's rank among the wave's lanes holding expert lek[k].
+// lane's rank among the wave's lanes holding expert lek[k].  One ballot per expert;
+// lane e keeps expert e's ballot and writes it to the wave's table bal[kEL] in LDS,
+// from which every lane reads the ballots of its own experts.  The table is written
+// and read by the same wave only (LDS operations of a wave complete in order).
 __device__ __forceinline__ void wave_ranks(const TokenRoutes& r, int wave, int lane,
-                                           int (*wcnt)[kEL], int* rank) {
+                                           int (*wcnt)[kEL], uint64_t* bal, int* rank) {
+    uint64_t mine = 0;
 #pragma unroll
-    for (int k = 0; k < kTopK; ++k) rank[k] = 0;
     for (int e = 0; e < kEL; ++e) {
         const uint64_t b = __ballot((r.mask >> e) & 1u);
-        if (lane == 0) wcnt[wave][e] = __popcll(b);
-        const int below = __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32),
-                                                    __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+        mine = (lane == e) ? b : mine;
+    }
+    if (lane < kEL) {
+        bal[lane] = mine;
+        wcnt[wave][lane] = __popcll(mine);
+    }
+    __builtin_amdgcn_wave_barrier();
 #pragma unroll
-        for (int k = 0; k < kTopK; ++k) rank[k] = (r.lek[k] == e) ? below : rank[k];
+    for (int k = 0; k < kTopK; ++k) {
+        rank[k] = 0;
+        if (r.lek[k] >= 0) {
+            const uint64_t b = bal[r.lek[k]];
+            rank[k] = __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32),
+                                                __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+        }
     }
 }
 
@@ -144,11 +157,12 @@ __global__ __launch_bounds__(64 * NW) void dispatch_small_kernel(
     __shared__ int wcnt[NW][kEL];
     __shared__ int wbase[NW][kEL];
     __shared__ int off[kEL];
+    __shared__ uint64_t bal[NW][kEL];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
 
     const TokenRoutes r = load_routes(topk_ids, topk_w, tid, T, offset);
     int rank[kTopK];
-    wave_ranks(r, wave, lane, wcnt, rank);
+    wave_ranks(r, wave, lane, wcnt, bal[wave], rank);
     __syncthreads();
     if (wave == 0) {
         int c = 0;
@@ -177,10 +191,11 @@ __global__ __launch_bounds__(kChunk) void dispatch_count_kernel(
     const int* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int offset,
     int* __restrict__ chunk_cnt) {
     __shared__ int wcnt[kChunkWaves][kEL];
+    __shared__ uint64_t bal[kChunkWaves][kEL];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const TokenRoutes r = load_routes(topk_ids, topk_w, blockIdx.x * kChunk + tid, T, offset);
     int rank[kTopK];
-    wave_ranks(r, wave, lane, wcnt, rank);
+    wave_ranks(r, wave, lane, wcnt, bal[wave], rank);
     __syncthreads();
     if (tid < kEL) {
         int c = 0;
@@ -206,12 +221,13 @@ __global__ __launch_bounds__(kChunk) void dispatch_place_kernel(
     __shared__ int off[kEL];
     __shared__ int cbase[kEL];
     __shared__ int part[2][kGroups][kEL];
+    __shared__ uint64_t bal[kChunkWaves][kEL];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int chunk = blockIdx.x;
 
     const TokenRoutes r = load_routes(topk_ids, topk_w, chunk * kChunk + tid, T, offset);
     int rank[kTopK];
-    wave_ranks(r, wave, lane, wcnt, rank);
+    wave_ranks(r, wave, lane, wcnt, bal[wave], rank);
     {
         const int e = tid % kEL, g = tid / kEL;
         int total = 0, before = 0;
