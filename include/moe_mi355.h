@@ -153,11 +153,14 @@ typedef struct moe_mi355_workspace_layout {
     size_t topk_weights;    /* fp32  [T,8] */
     size_t inverse_rows;    /* int32 [T,8] */
     size_t meta;            /* int32 [64]: [0..32] expert offsets, [33] num tiles,
-                               [34] tiles of the second list (256-row plans),
-                               [35] nonzero when C went beyond the fp16 range (format 0),
-                               [36] nonzero when an expert row did */
-    size_t tiles;           /* int32 [2*max_tiles,4]: the tile list, then (256-row
-                               plans) a second list of 128-row tiles for GEMM2 */
+                               [34] tiles of the second list (plans whose GEMM2 runs
+                               on 128-row tiles under a GEMM1 on other tiles),
+                               [35] nonzero when C went beyond the fp16 range (formats
+                               0 and 2), [36] nonzero when an expert row did */
+    size_t tiles;           /* int32 [2*max_tiles,4]: the tile list of GEMM1 (tile_m
+                               rows), then, for those plans, a second list of 128-row
+                               tiles for GEMM2 right after the first list's
+                               moe_mi355_max_tiles(T, tile_m) entries */
     size_t sorted_tokens;   /* int32 [8T] */
     size_t sorted_weights;  /* fp32  [8T] */
     size_t chunk_counts;    /* int32 [ceil(T/256), 32] dispatch scratch */
