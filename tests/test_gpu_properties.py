@@ -141,6 +141,25 @@ def test_every_gemm_variant_matches_oracle(T, g1, g2, monkeypatch):
     assert st["frac_within"] == 1.0, st
 
 
+@pytest.mark.parametrize("T,offset", [(37, 224), (213, 32), (611, 0), (977, 64), (1311, 224),
+                                      (1777, 32), (2459, 64), (3583, 0)])
+def test_batch_sizes_between_plan_boundaries(T, offset):
+    """Token counts away from the tested boundaries, one in each plan range, each with
+    another expert offset (config 3 sliced to T): sampled tokens match the oracle and a
+    second call on the same inputs is bit-identical."""
+    d = first_tokens(config_inputs(3), T)
+    d["local_expert_offset"] = offset
+    note(f"[gpu] batch size T={T} offset={offset}")
+    a = run_forward(d)
+    b = run_forward(d)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    rng = np.random.default_rng(T)
+    toks = sorted(rng.choice(T, 12, replace=False).tolist())
+    st = compare_to_oracle(d, a, toks)
+    note(f"[gpu] T={T} offset={offset} stats {st}")
+    assert st["frac_within"] == 1.0, st
+
+
 @pytest.mark.parametrize("T", [64, 600, 2049])
 def test_all_local_routing_matches_oracle(T):
     """Every token routed to 8 local experts (bias +3 on all 32 local experts, so group 0
