@@ -26,7 +26,7 @@ void launch_route(const float*, const uint16_t*, int, float, int*, float*, int*,
 bool launch_dispatch(const int*, const float*, int, int, int, int, int*, int*, int4*, int*, float*,
                      int*, int*, hipStream_t, int*, int4*);
 int dispatch_max_tiles(int T, int tm);
-bool launch_gemm1(int, const uint8_t*, const float*, int, const uint8_t*, const float*,
+bool launch_gemm1(int, const uint8_t*, const TokenScales&, int, const uint8_t*, const float*,
                   const int4*, const int*, const int*, int, const int*, const Intermediate&,
                   hipStream_t);
 bool launch_gemm2(int, const Intermediate&, const uint8_t*, const float*, const int4*, const int*,
@@ -34,6 +34,7 @@ bool launch_gemm2(int, const Intermediate&, const uint8_t*, const float*, const 
 void launch_combine(const ExpertRows&, const int*, const float*, const int*, int, uint16_t*, hipStream_t);
 void launch_e4m3_to_bf16(const uint8_t*, uint16_t*, int, hipStream_t);
 void launch_c_f16_to_hilo(const Intermediate&, const int*, hipStream_t);
+void launch_gather_row_scales(const float*, int, const int*, const int*, float*, int, hipStream_t);
 void launch_e4m3_to_f16(const uint8_t*, uint16_t*, int, hipStream_t);
 void launch_quantize_fp8_blockwise(const void*, int, int, int, uint8_t*, float*, hipStream_t);
 }  // namespace moe
@@ -103,6 +104,16 @@ Plan choose_plan(int32_t T) {
     return p;
 }
 
+// Whether GEMM1 reads the token scales gathered into row order (see
+// gather_row_scales_kernel): from T = kRowScalesMinT on; MOE_MI355_ROW_SCALES=0 / 1
+// overrides it for tuning sweeps (read on every call, as the plan overrides are).
+constexpr int32_t kRowScalesMinT = 512;
+bool row_scales_for(int32_t T) {
+    const char* e = getenv("MOE_MI355_ROW_SCALES");
+    if (e != nullptr && (e[0] == '0' || e[0] == '1') && e[1] == 0) return e[0] == '1';
+    return T >= kRowScalesMinT;
+}
+
 thread_local char g_hip_error[256] = "";
 
 size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -125,6 +136,7 @@ bool fill_layout(int32_t T, moe_mi355_workspace_layout* L) {
     L->sorted_tokens = take(R * 4);
     L->sorted_weights = take(R * 4);
     L->chunk_counts = take((size_t)((T + 255) / 256) * moe::kEL * 4);
+    L->row_scales = take(R * moe::kHB * 4);        // token scales in row order, [56, 8T]
     L->intermediate = take(R * moe::kI * 6);     // hi/lo, fp16, bf16 copies
     L->intermediate_scales = take(R * moe::kIB * 4);
     L->expert_out = take(R * moe::kH * 2);
@@ -278,6 +290,7 @@ int moe_mi355_forward(const moe_mi355_args* a, void* stream) {
     const moe::ExpertRows rows{reinterpret_cast<uint16_t*>(ws + L.expert_out),
                                reinterpret_cast<float*>(ws + L.expert_out_wide)};
     int* chunk_cnt = reinterpret_cast<int*>(ws + L.chunk_counts);
+    float* row_scales = reinterpret_cast<float*>(ws + L.row_scales);
     int* num_tiles = meta + moe::kEL + 1;
 
     const bool prof = (a->flags & MOE_MI355_FLAG_PROFILE) && g_prof.ev && g_prof.used < g_prof.slots;
@@ -295,8 +308,16 @@ int moe_mi355_forward(const moe_mi355_args* a, void* stream) {
     moe::launch_dispatch(ids, wts, T, clamp_offset(a->local_expert_offset), plan.tm, plan.tm2, meta,
                          num_tiles, tiles, stok, sw, inv, chunk_cnt, s, half ? num_tiles2 : nullptr,
                          half ? tiles2 : nullptr);
+    // GEMM1 reads the token scales gathered into row order (counted in the dispatch stage)
+    // or, where the gather would cost more than it saves, straight by token
+    const bool by_row = row_scales_for(T);
+    if (by_row)
+        moe::launch_gather_row_scales(a->hidden_states_scale, T, stok, meta, row_scales,
+                                      T * moe::kTopK, s);
+    const moe::TokenScales sa = by_row ? moe::TokenScales{row_scales, T * moe::kTopK, 1}
+                                       : moe::TokenScales{a->hidden_states_scale, T, 0};
     if (prof) prof_record(slot, 2, s);
-    moe::launch_gemm1(plan.g1, a->hidden_states, a->hidden_states_scale, T, a->gemm1_weights,
+    moe::launch_gemm1(plan.g1, a->hidden_states, sa, T, a->gemm1_weights,
                       a->gemm1_weights_scale, tiles, num_tiles, meta, max_tiles, stok, inter, s);
     if (prof) prof_record(slot, 3, s);
     if (plan.convert) moe::launch_c_f16_to_hilo(inter, meta, s);   // counted in the GEMM2 stage

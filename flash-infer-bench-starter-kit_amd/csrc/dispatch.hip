@@ -269,6 +269,29 @@ __global__ __launch_bounds__(kChunk) void dispatch_place_kernel(
     place(r, rank, chunk * kChunk + tid, T, wbase[wave], sorted_tok, sorted_w, inv);
 }
 
+// Token scales in row order for GEMM1 (reference kernel.cu:204-230, prepare_sfa_kernel,
+// builds the same table over its padded rows): row_scales[kb][row] =
+// hs_scale[kb][sorted_tok[row]] for the exp_off[32] rows of the permutation.  A GEMM1
+// tile then reads its rows' scales of a K block as one contiguous run.  Grid: y = K
+// block, x strides over rows (one pass up to 16384 rows); rows_cap is the row stride.
+__global__ __launch_bounds__(256) void gather_row_scales_kernel(
+    const float* __restrict__ hs_scale, int T, const int* __restrict__ sorted_tok,
+    const int* __restrict__ exp_off, float* __restrict__ row_scales, int rows_cap) {
+    const int na = exp_off[kEL];
+    const int kb = blockIdx.y;
+    for (int row = blockIdx.x * 256 + threadIdx.x; row < na; row += gridDim.x * 256)
+        row_scales[(size_t)kb * rows_cap + row] = hs_scale[(size_t)kb * T + sorted_tok[row]];
+}
+
+void launch_gather_row_scales(const float* hs_scale, int T, const int* sorted_tok,
+                              const int* exp_off, float* row_scales, int rows_cap,
+                              hipStream_t stream) {
+    if (rows_cap <= 0) return;
+    const int gx = min((rows_cap + 255) / 256, 64);
+    hipLaunchKernelGGL(gather_row_scales_kernel, dim3(gx, kHB), dim3(256), 0, stream, hs_scale, T,
+                       sorted_tok, exp_off, row_scales, rows_cap);
+}
+
 int dispatch_max_tiles(int T, int tm) {
     const long long rows = (long long)T * kTopK;
     return (int)((rows + tm - 1) / tm) + kEL;

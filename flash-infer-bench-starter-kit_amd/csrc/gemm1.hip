@@ -87,7 +87,7 @@ __device__ __forceinline__ void store_swiglu4(const Intermediate& C, int* __rest
 // ---------------------------------------------------------------------------
 template <int D, int CB, int NGRP>
 __global__ __launch_bounds__(256) void gemm1_rstream_kernel(
-    const uint8_t* __restrict__ hidden, const float* __restrict__ hs_scale, int T,
+    const uint8_t* __restrict__ hidden, TokenScales sa, int T,
     const uint8_t* __restrict__ w1, const float* __restrict__ s1,
     const int4* __restrict__ tiles, const int* __restrict__ num_tiles,
     const int* __restrict__ sorted_tok, Intermediate C, int* __restrict__ c_wide) {
@@ -128,9 +128,10 @@ __global__ __launch_bounds__(256) void gemm1_rstream_kernel(
         const float* sp[CB];
 #pragma unroll
         for (int c = 0; c < CB; ++c) {
-            const int tok = sorted_tok[row0 + min(16 * c + r16, nrows - 1)];
+            const int row = row0 + min(16 * c + r16, nrows - 1);
+            const int tok = sorted_tok[row];
             ap[c] = hidden + (size_t)tok * kH + kq * 32;
-            sp[c] = hs_scale + tok;
+            sp[c] = sa.p + (sa.by_row ? row : tok);
         }
         // slot rows 32 gi + 0..15: gate rows of group ng + gi, 32 gi + 16..31: its up rows
         const uint8_t* wsrc[NW];
@@ -155,7 +156,7 @@ __global__ __launch_bounds__(256) void gemm1_rstream_kernel(
 #pragma unroll
             for (int c = 0; c < CB; ++c) {
                 ba[k % D][c] = load_v8i(ap[c] + kb * kBlk);
-                bs[k % D][c] = sp[c][(size_t)kb * T];
+                bs[k % D][c] = sp[c][(size_t)kb * sa.stride];
             }
         };
 #pragma unroll
@@ -320,7 +321,7 @@ __device__ __forceinline__ void store_c_hilo(const v4f (&acc)[4][8], float* xch,
 // ---------------------------------------------------------------------------
 template <int NS>
 __global__ __launch_bounds__(256) void gemm1_prefill_kernel(
-    const uint8_t* __restrict__ hidden, const float* __restrict__ hs_scale, int T,
+    const uint8_t* __restrict__ hidden, TokenScales sa, int T,
     const uint8_t* __restrict__ w1, const float* __restrict__ s1,
     const int4* __restrict__ tiles, const int* __restrict__ num_tiles,
     const int* __restrict__ exp_off, const int* __restrict__ sorted_tok, Intermediate C) {
@@ -373,8 +374,9 @@ __global__ __launch_bounds__(256) void gemm1_prefill_kernel(
             const int n = (r < 128) ? ng * 128 + r : kI + ng * 128 + (r - 128);
             wsrc[i] = w1 + (size_t)(le * kN1 + n) * kH + ((dchunk ^ swz128(r)) << 4);
         }
-        // token scales: lane l of wave w fetches the scale of token 64*wm + l
-        const float* sap = hs_scale + sorted_tok[row0 + min(64 * wm + lane, nrows - 1)];
+        // token scales: lane l of wave w fetches the scale of row 64*wm + l
+        const int srow = row0 + min(64 * wm + lane, nrows - 1);
+        const float* sap = sa.p + (sa.by_row ? srow : sorted_tok[srow]);
         const float* sgp = s1 + (size_t)(le * kN1B + ng) * kHB;
         const float* sup = sgp + (size_t)kIB * kHB;
 
@@ -384,7 +386,7 @@ __global__ __launch_bounds__(256) void gemm1_prefill_kernel(
             for (int i = 0; i < 4; ++i) dma16(asrc[i] + kb * kBlk, st + (32 * wave + 8 * i) * kBlk);
 #pragma unroll
             for (int i = 0; i < 8; ++i) dma16(wsrc[i] + kb * kBlk, st + kA + (64 * wave + 8 * i) * kBlk);
-            dma4(sap + (size_t)kb * T, st + kA + kW + wave * 256);
+            dma4(sap + (size_t)kb * sa.stride, st + kA + kW + wave * 256);
         };
 
         v4f acc[4][8];
@@ -474,7 +476,7 @@ __global__ __launch_bounds__(256) void gemm1_prefill_kernel(
 // Token offsets are 32-bit: T * 7168 < 2^32 (T <= 2^19, checked by the host).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(512, 1) void gemm1_prefill8_kernel(
-    const uint8_t* __restrict__ hidden, const float* __restrict__ hs_scale, int T,
+    const uint8_t* __restrict__ hidden, TokenScales sa, int T,
     const uint8_t* __restrict__ w1, const float* __restrict__ s1,
     const int4* __restrict__ tiles, const int* __restrict__ num_tiles,
     const int* __restrict__ exp_off, const int* __restrict__ sorted_tok, Intermediate C) {
@@ -500,7 +502,7 @@ __global__ __launch_bounds__(512, 1) void gemm1_prefill8_kernel(
     const int swz = swz128(r16);
     const int c0 = ((2 * kq) ^ swz) << 4, c1 = ((2 * kq + 1) ^ swz) << 4;
     const __amdgpu_buffer_rsrc_t rs_tok = buffer_rsrc(hidden, (uint32_t)T * kH);
-    const __amdgpu_buffer_rsrc_t rs_sca = buffer_rsrc(hs_scale, (uint32_t)T * kHB * 4);
+    const __amdgpu_buffer_rsrc_t rs_sca = buffer_rsrc(sa.p, (uint32_t)sa.stride * kHB * 4);
 
     for (int round = 0; round * G < nitems; ++round) {
         const int item = round * G + xcd * per + slot;
@@ -521,7 +523,8 @@ __global__ __launch_bounds__(512, 1) void gemm1_prefill8_kernel(
             const int n = (r < 128) ? ng * 128 + r : kI + ng * 128 + (r - 128);
             woff[i] = (uint32_t)n * kH + ((dchunk ^ swz128(r)) << 4);
         }
-        const uint32_t soff = (uint32_t)sorted_tok[row0 + min(64 * wm + lane, nrows - 1)] * 4;
+        const int srow = row0 + min(64 * wm + lane, nrows - 1);
+        const uint32_t soff = (uint32_t)(sa.by_row ? srow : sorted_tok[srow]) * 4;
         const float* sgp = s1 + (size_t)(le * kN1B + ng) * kHB;
         const float* sup = sgp + (size_t)kIB * kHB;
 
@@ -534,7 +537,7 @@ __global__ __launch_bounds__(512, 1) void gemm1_prefill8_kernel(
             uint8_t* st = lds + (kb & 1) * kStage;
 #pragma unroll
             for (int i = 0; i < 4; ++i) bdma16(rs_w, woff[i], (uint32_t)kb * kBlk, st + kA + (32 * wave + 8 * i) * kBlk);
-            bdma4(rs_sca, soff, (uint32_t)kb * T * 4, st + kA + kW + wave * 256);
+            bdma4(rs_sca, soff, (uint32_t)kb * sa.stride * 4, st + kA + kW + wave * 256);
         };
 
         v4f acc[4][8];
@@ -613,7 +616,7 @@ static int grid_for(long long work) { return (int)(work < 4096 ? work : 4096); }
 //   2  register-staged, 2 row blocks x 2 column groups   32-row tiles   fp16 + bf16
 //   3  prefill, 4 waves, 128 x 256 workgroup tile        128-row tiles  fp8 hi/lo
 //   4  prefill, 8 waves, 256 x 256 workgroup tile        256-row tiles  fp8 hi/lo
-bool launch_gemm1(int variant, const uint8_t* hidden, const float* hs_scale, int T,
+bool launch_gemm1(int variant, const uint8_t* hidden, const TokenScales& sa, int T,
                   const uint8_t* w1, const float* s1, const int4* tiles, const int* num_tiles,
                   const int* exp_off, int max_tiles, const int* sorted_tok, const Intermediate& C,
                   hipStream_t stream) {
@@ -624,19 +627,19 @@ bool launch_gemm1(int variant, const uint8_t* hidden, const float* hs_scale, int
     switch (variant) {
         case 1:
             hipLaunchKernelGGL((gemm1_rstream_kernel<4, 1, 1>), dim3(grid_for(mt * G)), dim3(256), 0, stream,
-                               hidden, hs_scale, T, w1, s1, tiles, num_tiles, sorted_tok, C, c_wide);
+                               hidden, sa, T, w1, s1, tiles, num_tiles, sorted_tok, C, c_wide);
             return true;
         case 2:
             hipLaunchKernelGGL((gemm1_rstream_kernel<3, 2, 2>), dim3(grid_for(mt * G / 2)), dim3(256), 0, stream,
-                               hidden, hs_scale, T, w1, s1, tiles, num_tiles, sorted_tok, C, c_wide);
+                               hidden, sa, T, w1, s1, tiles, num_tiles, sorted_tok, C, c_wide);
             return true;
         case 3:
             hipLaunchKernelGGL(gemm1_prefill_kernel<3>, dim3(prefill_grid), dim3(256), 0, stream,
-                               hidden, hs_scale, T, w1, s1, tiles, num_tiles, exp_off, sorted_tok, C);
+                               hidden, sa, T, w1, s1, tiles, num_tiles, exp_off, sorted_tok, C);
             return true;
         case 4:
             hipLaunchKernelGGL(gemm1_prefill8_kernel, dim3(prefill_grid), dim3(512), 0, stream,
-                               hidden, hs_scale, T, w1, s1, tiles, num_tiles, exp_off, sorted_tok, C);
+                               hidden, sa, T, w1, s1, tiles, num_tiles, exp_off, sorted_tok, C);
             return true;
         default: return false;
     }

@@ -104,6 +104,17 @@ __device__ __forceinline__ void grouped_item(int item, int ncol, const int4* __r
     col = in / gm;
 }
 
+// Token scales as GEMM1 reads them: p[kb * stride + i], where i is the token (by_row 0:
+// the caller's hidden_states_scale [56, T], stride T) or the row of the permutation
+// (by_row 1: the gathered row scales [56, rows_cap], stride rows_cap, in which the rows
+// of a tile are contiguous, so a tile's scales of one K block are one or a few lines
+// instead of one 4-byte load per token).
+struct TokenScales {
+    const float* p;
+    int stride;
+    int by_row;
+};
+
 // One global_load_lds_dwordx4: lane L copies the 16 bytes at its own address g to
 // LDS l + 16 L (l must be wave-uniform).
 __device__ __forceinline__ void dma16(const uint8_t* g, uint8_t* l) {

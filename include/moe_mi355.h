@@ -164,6 +164,9 @@ typedef struct moe_mi355_workspace_layout {
     size_t sorted_tokens;   /* int32 [8T] */
     size_t sorted_weights;  /* fp32  [8T] */
     size_t chunk_counts;    /* int32 [ceil(T/256), 32] dispatch scratch */
+    size_t row_scales;      /* fp32  [56, 8T]: hidden_states_scale gathered into row order,
+                               [kb][row] = scale[kb][sorted_tokens[row]] (the rows
+                               in use, for the token counts where GEMM1 reads them) */
     size_t intermediate;    /* SwiGLU output rows C, 8T x 2048 x 6 bytes:
                                e4m3 hi [8T, 2048], e4m3 lo [8T, 2048]  (hi/lo form:
                                   C = s * (hi + lo / 16), s from intermediate_scales),

@@ -107,12 +107,13 @@ def test_small_odd_batches(T):
     assert st["frac_within"] == 1.0, st
 
 
-@pytest.mark.parametrize("T", [112, 113, 192, 193, 704, 705, 1024, 1025, 1408, 1409])
+@pytest.mark.parametrize("T", [112, 113, 192, 193, 511, 512, 704, 705, 1024, 1025, 1408, 1409])
 def test_plan_boundaries_match_oracle(T):
     """Token counts on both sides of every change of kernel plan (16-row streaming
     with 32 then 64 GEMM2 columns per wave, 32-row streaming, 32-row streaming GEMM1
-    with the prefill GEMM2, 256-row prefill tiles) and of the dispatch (one workgroup
-    up to T = 1024, count and place kernels over 256-token chunks beyond)."""
+    with the prefill GEMM2, 256-row prefill tiles), of the token scales GEMM1 reads
+    (by token, then gathered into row order from T = 512) and of the dispatch (one
+    workgroup up to T = 1024, count and place kernels over 256-token chunks beyond)."""
     d = first_tokens(config_inputs(3), T)
     note(f"[gpu] plan boundary T={T}")
     out = run_forward(d)
@@ -158,6 +159,31 @@ def test_batch_sizes_between_plan_boundaries(T, offset):
     st = compare_to_oracle(d, a, toks)
     note(f"[gpu] T={T} offset={offset} stats {st}")
     assert st["frac_within"] == 1.0, st
+
+
+@pytest.mark.parametrize("T", [64, 200, 1024, 3000])
+def test_row_order_token_scales_change_nothing(T, monkeypatch):
+    """GEMM1 reading the token scales gathered into row order (MOE_MI355_ROW_SCALES=1)
+    or straight by token (=0) gives bit-identical outputs on every plan; the gathered
+    table holds hidden_states_scale[kb][sorted_tokens[row]] for the rows in use."""
+    d = first_tokens(config_inputs(3), T)
+    k = pkg("kernel")
+    wl = pkg("workloads")
+    lay = k.workspace_layout(T)
+    outs = []
+    for flag in ("0", "1"):
+        monkeypatch.setenv("MOE_MI355_ROW_SCALES", flag)
+        note(f"[gpu] row-order token scales {flag} T={T}")
+        ws = torch.empty(lay.total, dtype=torch.uint8, device="cuda")
+        out = torch.full_like(d["output"], float("nan"))
+        k.forward(*wl.as_args({**d, "output": out}), workspace=ws)
+        torch.cuda.synchronize()
+        outs.append(out)
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    na = int(ws[lay.meta + 32 * 4:lay.meta + 33 * 4].view(torch.int32).item())
+    stok = ws[lay.sorted_tokens:lay.sorted_tokens + na * 4].view(torch.int32).long()
+    tab = ws[lay.row_scales:lay.row_scales + 56 * 8 * T * 4].view(torch.float32).view(56, 8 * T)
+    assert torch.equal(tab[:, :na], d["hidden_states_scale"][:, stok])
 
 
 @pytest.mark.parametrize("T", [64, 600, 2049])
