@@ -85,7 +85,7 @@ __device__ __forceinline__ void store_swiglu4(const Intermediate& C, int* __rest
 // weight groups: token re-reads, which hit L2 but still take the CU's outstanding
 // request slots, fall from half of the requests (NGRP = 1, CB = 2) to a third.
 // ---------------------------------------------------------------------------
-template <int D, int CB, int NGRP>
+template <int D, int CB, int NGRP, bool TL>
 __global__ __launch_bounds__(256) void gemm1_rstream_kernel(
     const uint8_t* __restrict__ hidden, TokenScales sa, int T,
     const uint8_t* __restrict__ w1, const float* __restrict__ s1,
@@ -98,7 +98,8 @@ __global__ __launch_bounds__(256) void gemm1_rstream_kernel(
     constexpr int kVmPerKb = NW + 3 * CB;             // per row block 2 token loads + 1 scale
     static_assert(D >= 2 && D <= 8 && (D - 1) * kVmPerKb < 64, "ring depth");
     static_assert(NGRP == 1 || NGRP == 2, "column groups per item");
-    __shared__ __attribute__((aligned(1024))) uint8_t slot_lds[4][32 * NGRP * kBlk];
+    constexpr int kTok = 32 * NGRP * kBlk;           // token rows after the weight rows
+    __shared__ __attribute__((aligned(1024))) uint8_t slot_lds[4][kTok + (TL ? 16 * CB * kBlk : 0)];
     __shared__ v4f red[4][2][NGRP * CB][64];
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -118,20 +119,32 @@ __global__ __launch_bounds__(256) void gemm1_rstream_kernel(
         const int r = 8 * i + drow;
         wr[i] = r * kBlk + ((dchunk ^ swz128(r)) << 4);
     }
+    int twr[2 * CB];                                   // the same for the token rows
+#pragma unroll
+    for (int i = 0; i < 2 * CB; ++i) {
+        const int r = 8 * i + drow;
+        twr[i] = kTok + r * kBlk + ((dchunk ^ swz128(r)) << 4);
+    }
     const int kb0 = ks * KB;
 
     for (int work = blockIdx.x; work < nwork; work += gridDim.x) {
         const int4 tile = tiles[work / kItems];
         const int ng = (work % kItems) * NGRP;         // first 16-column group
         const int le = tile.x, row0 = tile.y, nrows = tile.z;
-        const uint8_t* ap[CB];
+        // TL: token rows also come as full 128-byte lines (lane l: row 8 i + l / 8, chunk
+        // l % 8; offsets fit 32 bits, T * 7168 < 2^32) and reach the MFMA layout through
+        // the slot.  Otherwise each lane loads its 32 MFMA-layout bytes of row r16.
+        uint32_t toff[2 * CB];
+#pragma unroll
+        for (int i = 0; i < 2 * CB; ++i) {
+            if (TL) toff[i] = (uint32_t)sorted_tok[row0 + min(8 * i + drow, nrows - 1)] * kH + dchunk * 16;
+            else if (i < CB) toff[i] = (uint32_t)sorted_tok[row0 + min(16 * i + r16, nrows - 1)] * kH + kq * 32;
+        }
         const float* sp[CB];
 #pragma unroll
         for (int c = 0; c < CB; ++c) {
             const int row = row0 + min(16 * c + r16, nrows - 1);
-            const int tok = sorted_tok[row];
-            ap[c] = hidden + (size_t)tok * kH + kq * 32;
-            sp[c] = sa.p + (sa.by_row ? row : tok);
+            sp[c] = sa.p + (sa.by_row ? row : sorted_tok[row]);
         }
         // slot rows 32 gi + 0..15: gate rows of group ng + gi, 32 gi + 16..31: its up rows
         const uint8_t* wsrc[NW];
@@ -147,17 +160,19 @@ __global__ __launch_bounds__(256) void gemm1_rstream_kernel(
         const float* su = sg + (size_t)kIB * kHB;
 
         v4u bw[D][NW];
-        v8i ba[D][CB];
+        v4u bt[D][2 * CB];
         float bs[D][CB];
         auto issue = [&](int k) {
             const int kb = kb0 + k;
 #pragma unroll
             for (int i = 0; i < NW; ++i) bw[k % D][i] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(wsrc[i] + kb * kBlk));
 #pragma unroll
-            for (int c = 0; c < CB; ++c) {
-                ba[k % D][c] = load_v8i(ap[c] + kb * kBlk);
-                bs[k % D][c] = sp[c][(size_t)kb * sa.stride];
+            for (int i = 0; i < 2 * CB; ++i) {
+                const uint32_t o = TL ? toff[i] : toff[i >> 1] + 16 * (i & 1);
+                bt[k % D][i] = *reinterpret_cast<const v4u*>(hidden + o + kb * kBlk);
             }
+#pragma unroll
+            for (int c = 0; c < CB; ++c) bs[k % D][c] = sp[c][(size_t)kb * sa.stride];
         };
 #pragma unroll
         for (int k = 0; k < D - 1; ++k) {
@@ -187,6 +202,24 @@ __global__ __launch_bounds__(256) void gemm1_rstream_kernel(
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < NW; ++i) *reinterpret_cast<v4u*>(slot + wr[i]) = bw[k % D][i];
+            v8i ba[CB];
+            if constexpr (TL) {
+#pragma unroll
+                for (int i = 0; i < 2 * CB; ++i) *reinterpret_cast<v4u*>(slot + twr[i]) = bt[k % D][i];
+#pragma unroll
+                for (int c = 0; c < CB; ++c) {
+                    const uint8_t* ts = slot + kTok + 16 * c * kBlk;
+                    const v4u a0 = *reinterpret_cast<const v4u*>(ts + rd_g0);
+                    const v4u a1 = *reinterpret_cast<const v4u*>(ts + rd_g1);
+                    ba[c] = v8i{(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3], (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
+                }
+            } else {
+#pragma unroll
+                for (int c = 0; c < CB; ++c) {
+                    const v4u a0 = bt[k % D][2 * c], a1 = bt[k % D][2 * c + 1];
+                    ba[c] = v8i{(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3], (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
+                }
+            }
             const int kb = kb0 + k;
             const float wg = sg[kb], wu = su[kb];
 #pragma unroll
@@ -201,8 +234,8 @@ __global__ __launch_bounds__(256) void gemm1_rstream_kernel(
 #pragma unroll
                 for (int c = 0; c < CB; ++c) {
                     const float fg = bs[k % D][c] * wg, fu = bs[k % D][c] * wu;
-                    const v4f tg = mfma_fp8(bg, ba[k % D][c], zero);
-                    const v4f tu = mfma_fp8(bu, ba[k % D][c], zero);
+                    const v4f tg = mfma_fp8(bg, ba[c], zero);
+                    const v4f tu = mfma_fp8(bu, ba[c], zero);
 #pragma unroll
                     for (int v = 0; v < 4; ++v) {
                         ag[gi][c][v] = __builtin_fmaf(tg[v], fg, ag[gi][c][v]);
@@ -626,11 +659,11 @@ bool launch_gemm1(int variant, const uint8_t* hidden, const TokenScales& sa, int
     const long long mt = max_tiles;
     switch (variant) {
         case 1:
-            hipLaunchKernelGGL((gemm1_rstream_kernel<4, 1, 1>), dim3(grid_for(mt * G)), dim3(256), 0, stream,
+            hipLaunchKernelGGL((gemm1_rstream_kernel<4, 1, 1, false>), dim3(grid_for(mt * G)), dim3(256), 0, stream,
                                hidden, sa, T, w1, s1, tiles, num_tiles, sorted_tok, C, c_wide);
             return true;
         case 2:
-            hipLaunchKernelGGL((gemm1_rstream_kernel<3, 2, 2>), dim3(grid_for(mt * G / 2)), dim3(256), 0, stream,
+            hipLaunchKernelGGL((gemm1_rstream_kernel<2, 2, 2, true>), dim3(grid_for(mt * G / 2)), dim3(256), 0, stream,
                                hidden, sa, T, w1, s1, tiles, num_tiles, sorted_tok, C, c_wide);
             return true;
         case 3:
