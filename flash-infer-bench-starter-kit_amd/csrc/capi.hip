@@ -55,7 +55,7 @@ constexpr int kMinTileM = 16;           // smallest row tile; sizes the tile lis
 // tiles (GEMM1 with two column groups per wave) beyond, where an expert gets up to
 // about 36 rows at T = 1152 and streams its weights about once.  From T = 705 the
 // streaming GEMM1 feeds the prefill GEMM2 (128-row tiles, FP8 MFMA on the hi/lo form),
-// the faster GEMM2 there; from T = 1409 both GEMMs are the MFMA-bound prefill kernels
+// the faster GEMM2 there; from T = 1537 both GEMMs are the MFMA-bound prefill kernels
 // on 256-row tiles (GEMM2 on the 128-row second list).  The 128-row prefill pair
 // (variants 3 / 4) stays available to the override.  The boundaries come from
 // wall-clock sweeps of the pairs at T = 64 .. 2560 on MI355X.  MOE_MI355_G1 /
@@ -93,7 +93,7 @@ Plan choose_plan(int32_t T) {
     if (T <= 112) g1 = 1, g2 = 1;
     else if (T <= 192) g1 = 1, g2 = 2;
     else if (T <= 704) g1 = 2, g2 = 3;
-    else if (T <= 1408) g1 = 2, g2 = 5;
+    else if (T <= 1536) g1 = 2, g2 = 5;
     else g1 = 4, g2 = 5;
     Plan p;
     make_plan(g1, g2, &p);
