@@ -561,10 +561,15 @@ __global__ __launch_bounds__(512, 1) void gemm1_prefill8_kernel(
         const float* sgp = s1 + (size_t)(le * kN1B + ng) * kHB;
         const float* sup = sgp + (size_t)kIB * kHB;
 
+        // a wave whose 32 token rows all lie past the tile moves nothing: they would only
+        // repeat the last row, and the MFMAs of their 16-row blocks are skipped
+        const bool tok_live = 32 * wave < nrows;
         auto issue_tokens = [&](int kb) {
             uint8_t* st = lds + (kb & 1) * kStage;
+            if (tok_live) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) bdma16(rs_tok, aoff[i], (uint32_t)kb * kBlk, st + (32 * wave + 8 * i) * kBlk);
+                for (int i = 0; i < 4; ++i) bdma16(rs_tok, aoff[i], (uint32_t)kb * kBlk, st + (32 * wave + 8 * i) * kBlk);
+            }
         };
         auto issue_weights = [&](int kb) {
             uint8_t* st = lds + (kb & 1) * kStage;

@@ -387,14 +387,20 @@ __global__ __launch_bounds__(512, 1) void gemm2_prefill8_kernel(
         const uint32_t csoff = (uint32_t)min(64 * wave + lane, nrows - 1) * 4;
         const float* sbp = s2 + (size_t)(le * kHB + 2 * hg + (wn >> 1)) * kIB;
 
+        // a wave whose 16 C rows all lie past the tile moves nothing: they would only
+        // repeat the last row, and the MFMAs of their 16-row block are skipped
+        const bool c_live = 16 * wave < nrows;
         auto issue_c = [&](int kb) {
             uint8_t* st = lds + (kb & 1) * kStage;
+            if (c_live) {
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                bdma16(rs_hi, coff[i], (uint32_t)kb * kBlk, st + (16 * wave + 8 * i) * kBlk);
-                bdma16(rs_lo, coff[i], (uint32_t)kb * kBlk, st + kC + (16 * wave + 8 * i) * kBlk);
+                for (int i = 0; i < 2; ++i) {
+                    bdma16(rs_hi, coff[i], (uint32_t)kb * kBlk, st + (16 * wave + 8 * i) * kBlk);
+                    bdma16(rs_lo, coff[i], (uint32_t)kb * kBlk, st + kC + (16 * wave + 8 * i) * kBlk);
+                }
             }
-            if (wave < 2) bdma4(rs_cs, csoff, (uint32_t)kb * C.rows_cap * 4, st + 2 * kC + kW + wave * 256);
+            if (wave < 2 && 64 * wave < nrows)
+                bdma4(rs_cs, csoff, (uint32_t)kb * C.rows_cap * 4, st + 2 * kC + kW + wave * 256);
         };
         auto issue_w = [&](int kb) {
             uint8_t* st = lds + (kb & 1) * kStage;
