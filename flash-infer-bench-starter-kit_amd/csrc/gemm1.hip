@@ -575,7 +575,7 @@ __global__ __launch_bounds__(512, 1) void gemm1_prefill8_kernel(
             uint8_t* st = lds + (kb & 1) * kStage;
 #pragma unroll
             for (int i = 0; i < 4; ++i) bdma16(rs_w, woff[i], (uint32_t)kb * kBlk, st + kA + (32 * wave + 8 * i) * kBlk);
-            bdma4(rs_sca, soff, (uint32_t)kb * sa.stride * 4, st + kA + kW + wave * 256);
+            if (64 * wm < nrows) bdma4(rs_sca, soff, (uint32_t)kb * sa.stride * 4, st + kA + kW + wave * 256);
         };
 
         v4f acc[4][8];
