@@ -84,6 +84,10 @@ __device__ __forceinline__ void store_swiglu4(const Intermediate& C, int* __rest
 // NGRP groups of 16 SwiGLU columns, so each token fragment a wave loads feeds NGRP
 // weight groups: token re-reads, which hit L2 but still take the CU's outstanding
 // request slots, fall from half of the requests (NGRP = 1, CB = 2) to a third.
+// TL: token rows take the weights' path too (full-line loads into the ring, then the
+// LDS slot), instead of each lane loading its 32 MFMA-layout bytes, which covers half
+// of 16 lines per instruction.  That pays on 32-row tiles (T = 193 .. 1536), where the
+// kernel is bound by the CU's requests, and not on 16-row tiles.
 // ---------------------------------------------------------------------------
 template <int D, int CB, int NGRP, bool TL>
 __global__ __launch_bounds__(256) void gemm1_rstream_kernel(
