@@ -22,13 +22,16 @@
 
 namespace moe {
 
-// inclusive prefix sum over lanes 0..31 of a wave (lanes >= 32 unused)
+// inclusive prefix sum over lanes 0..31 of a wave (lanes >= 32 unused; every lane of
+// the wave must be active).  DPP: shifts by 1, 2, 4, 8 inside each row of 16 lanes (a
+// source outside the row reads 0), then lane 15's row total is added to lanes 16..31.
 __device__ __forceinline__ int scan32(int v, int lane) {
-#pragma unroll
-    for (int off = 1; off < 32; off <<= 1) {
-        const int o = __shfl_up(v, off, 64);
-        if (lane >= off) v += o;
-    }
+    (void)lane;
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);   // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);   // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);   // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);   // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);   // row_bcast:15
     return v;
 }
 
