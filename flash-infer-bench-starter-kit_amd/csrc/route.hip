@@ -128,18 +128,17 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
 #pragma unroll
     for (int g = 0; g < kNGroup; ++g)
         gk[g] = order_bits(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(gscore), 8 * g)));
-    uint32_t keep = 0;
+    // lane l ranks group l % 8 against all eight (a group beats it with a larger score,
+    // or an equal one at a lower index); the kept groups are those ranked 0..3, which is
+    // the set that four picks of the best remaining group, ties to the lower, select
+    const int mg = lane & (kNGroup - 1);
+    uint32_t mine = gk[0];
 #pragma unroll
-    for (int j = 0; j < kTopKGroup; ++j) {
-        int best = -1;
-        uint32_t bk = 0;
+    for (int g = 1; g < kNGroup; ++g) mine = (mg == g) ? gk[g] : mine;
+    int rank = 0;
 #pragma unroll
-        for (int g = 0; g < kNGroup; ++g) {
-            const bool free_g = ((keep >> g) & 1u) == 0u;
-            if (free_g && (best < 0 || gk[g] > bk)) { best = g; bk = gk[g]; }
-        }
-        keep |= 1u << best;
-    }
+    for (int g = 0; g < kNGroup; ++g) rank += (gk[g] > mine || (gk[g] == mine && g < mg)) ? 1 : 0;
+    const uint32_t keep = (uint32_t)__ballot(lane < kNGroup && rank < kTopKGroup) & ((1u << kNGroup) - 1u);
 
     // top-8 (moe.cu:198-200): candidate key = orderable score + 1 for kept experts,
     // 1 for pruned ones, 0 once taken.  Per round the wave maximum is found with DPP,
