@@ -1,24 +1,33 @@
 """Compile the gfx950 HIP sources of this directory into ``libmoe_mi355.so``.
 
 Usage: ``python build.py [--jobs N]``.  Each ``csrc/*.hip`` file is compiled to an
-object in ``_build/`` (in parallel), then linked into ``libmoe_mi355.so`` next to
-this file, where ``kernel.py`` loads it.  hipcc cross-compiles for gfx950 without a
-GPU.
+object (in parallel), then linked into ``libmoe_mi355.so`` next to this file, where
+``kernel.py`` loads it.  hipcc cross-compiles for gfx950 without a GPU.
+
+Several processes may build at once (harness workers that each load the solution on
+first use): a build holds an exclusive ``fcntl`` lock on ``libmoe_mi355.so.lock`` next
+to the library, compiles and links inside a private temporary directory, and installs
+the result with one atomic ``os.replace``, so no process ever loads a half-written
+library or links another process's objects.  ``ensure_built`` builds only when the
+library is missing, re-checking under the lock.
 """
 from __future__ import annotations
 
 import argparse
 import concurrent.futures as cf
+import contextlib
+import fcntl
 import os
 import shutil
 import subprocess
 import sys
+import tempfile
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 REPO = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
-BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libmoe_mi355.so")
+LOCK = LIB + ".lock"
 # the C-ABI header: include/ next to this file in a packed solution, else the repo's
 INCLUDE = os.path.join(HERE, "include") if os.path.isdir(os.path.join(HERE, "include")) \
     else os.path.join(REPO, "include")
@@ -39,8 +48,8 @@ def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
-def _compile(src: str) -> str:
-    obj = os.path.join(BUILD, os.path.basename(src) + ".o")
+def _compile(src: str, outdir: str) -> str:
+    obj = os.path.join(outdir, os.path.basename(src) + ".o")
     cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
@@ -52,20 +61,50 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(jobs: int = 8, verbose: bool = True) -> str:
-    os.makedirs(BUILD, exist_ok=True)
-    srcs = sources()
-    with cf.ThreadPoolExecutor(max_workers=max(1, min(jobs, len(srcs)))) as ex:
-        objs = list(ex.map(_compile, srcs))
-    tmp = LIB + ".tmp"
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
-    os.replace(tmp, LIB)
+@contextlib.contextmanager
+def _build_lock():
+    fd = os.open(LOCK, os.O_RDWR | os.O_CREAT, 0o644)
+    try:
+        fcntl.flock(fd, fcntl.LOCK_EX)
+        yield
+    finally:
+        fcntl.flock(fd, fcntl.LOCK_UN)
+        os.close(fd)
+
+
+def _build_locked(jobs: int, verbose: bool) -> str:
+    work = tempfile.mkdtemp(prefix="_build.", dir=HERE)
+    try:
+        srcs = sources()
+        with cf.ThreadPoolExecutor(max_workers=max(1, min(jobs, len(srcs)))) as ex:
+            objs = list(ex.map(lambda s: _compile(s, work), srcs))
+        tmp = os.path.join(work, os.path.basename(LIB))
+        cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
+        os.replace(tmp, LIB)
+    finally:
+        shutil.rmtree(work, ignore_errors=True)
     if verbose:
         print(f"built {LIB}")
     return LIB
+
+
+def build(jobs: int = 8, verbose: bool = True) -> str:
+    """Compile and link the library (always, even when one is present)."""
+    with _build_lock():
+        return _build_locked(jobs, verbose)
+
+
+def ensure_built(jobs: int = 8, verbose: bool = False) -> str:
+    """Build the library only if it is missing (the first use of a packed solution)."""
+    if os.path.exists(LIB):
+        return LIB
+    with _build_lock():
+        if os.path.exists(LIB):       # another process built it while this one waited
+            return LIB
+        return _build_locked(jobs, verbose)
 
 
 if __name__ == "__main__":

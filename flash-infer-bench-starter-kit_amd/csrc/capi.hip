@@ -57,15 +57,14 @@ constexpr int kMinTileM = 16;           // smallest row tile; sizes the tile lis
 // streaming GEMM1 feeds the prefill GEMM2 (128-row tiles, FP8 MFMA on the hi/lo form),
 // the faster GEMM2 there; from T = 1537 both GEMMs are the MFMA-bound prefill kernels
 // on 256-row tiles (GEMM2 on the 128-row second list).  The 128-row prefill pair
-// (variants 3 / 4) stays available to the override.  The boundaries come from
-// wall-clock sweeps of the pairs at T = 64 .. 2560 on MI355X.  MOE_MI355_G1 /
-// MOE_MI355_G2 override the variants for tuning sweeps; a pair that cannot run together
-// is ignored.
+// (variants 3 / 4) stays reachable through MOE_MI355_FLAG_FORCE_PLAN.  The boundaries
+// come from wall-clock sweeps of the pairs at T = 64 .. 2560 on MI355X.
 struct Plan {
     int tm;        // tile height of the first list
     int tm2;       // tile height of the second list (0: none)
     int g1, g2;
     bool convert;  // fp16 C converted to the hi/lo form between the GEMMs
+    bool by_row;   // GEMM1 reads the token scales gathered into row order
 };
 
 int g1_tile_m(int v) { return v == 1 ? 16 : v == 2 ? 32 : v == 3 ? 128 : 256; }
@@ -79,47 +78,57 @@ bool make_plan(int g1, int g2, Plan* p) {
     if (g1_hilo(g1) && !g2_hilo(g2)) return false;      // the fp16 GEMM2s need fp16 C
     if (g2 == 5) {                                       // the second list, 128-row tiles
         if (tm != 16 && tm != 32 && tm != 256) return false;
-        *p = {tm, 128, g1, g2, !g1_hilo(g1)};
+        *p = {tm, 128, g1, g2, !g1_hilo(g1), false};
         return true;
     }
     const int tm_g2 = g2 <= 2 ? 16 : g2 == 3 ? 32 : 128;
     if (tm_g2 != tm) return false;
-    *p = {tm, 0, g1, g2, g1_hilo(g1) != g2_hilo(g2)};
+    *p = {tm, 0, g1, g2, g1_hilo(g1) != g2_hilo(g2), false};
     return true;
 }
 
-Plan choose_plan(int32_t T) {
+// GEMM1 reads the token scales gathered into row order (see gather_row_scales_kernel)
+// from T = kRowScalesMinT on; below, the gather costs more than it saves.
+constexpr int32_t kRowScalesMinT = 512;
+constexpr int32_t kKnownFlags = MOE_MI355_FLAG_PROFILE | MOE_MI355_FLAG_FORCE_PLAN |
+                                MOE_MI355_FLAG_ROW_SCALES_ON | MOE_MI355_FLAG_ROW_SCALES_OFF |
+                                (0xff << 8);
+
+// The plan of a call over T tokens: chosen from T alone, unless the caller's flags force
+// a GEMM pair or the token-scale form (tuning sweeps and the tests of every variant).
+// Nothing outside the call's arguments (no environment) changes it.
+int plan_for(int32_t T, int32_t flags, Plan* p) {
+    if (flags & ~kKnownFlags) return MOE_ERR_BAD_FLAGS;
     int g1, g2;
     if (T <= 112) g1 = 1, g2 = 1;
     else if (T <= 192) g1 = 1, g2 = 2;
     else if (T <= 704) g1 = 2, g2 = 3;
     else if (T <= 1536) g1 = 2, g2 = 5;
     else g1 = 4, g2 = 5;
-    Plan p;
-    make_plan(g1, g2, &p);
-    const char* e1 = getenv("MOE_MI355_G1");
-    const char* e2 = getenv("MOE_MI355_G2");
-    Plan q;
-    if (e1 && e2 && make_plan(atoi(e1), atoi(e2), &q)) p = q;
-    return p;
-}
-
-// Whether GEMM1 reads the token scales gathered into row order (see
-// gather_row_scales_kernel): from T = kRowScalesMinT on; MOE_MI355_ROW_SCALES=0 / 1
-// overrides it for tuning sweeps (read on every call, as the plan overrides are).
-constexpr int32_t kRowScalesMinT = 512;
-bool row_scales_for(int32_t T) {
-    const char* e = getenv("MOE_MI355_ROW_SCALES");
-    if (e != nullptr && (e[0] == '0' || e[0] == '1') && e[1] == 0) return e[0] == '1';
-    return T >= kRowScalesMinT;
+    if (flags & MOE_MI355_FLAG_FORCE_PLAN) {
+        g1 = MOE_MI355_FLAGS_G1(flags);
+        g2 = MOE_MI355_FLAGS_G2(flags);
+    } else if (flags & (0xff << 8)) {
+        return MOE_ERR_BAD_FLAGS;            // variant bits without the force bit
+    }
+    if (!make_plan(g1, g2, p)) return MOE_ERR_BAD_FLAGS;
+    const bool on = flags & MOE_MI355_FLAG_ROW_SCALES_ON, off = flags & MOE_MI355_FLAG_ROW_SCALES_OFF;
+    if (on && off) return MOE_ERR_BAD_FLAGS;
+    p->by_row = on ? true : off ? false : T >= kRowScalesMinT;
+    return MOE_OK;
 }
 
 thread_local char g_hip_error[256] = "";
 
 size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
 
-bool fill_layout(int32_t T, moe_mi355_workspace_layout* L) {
-    if (T < 0 || T > kMaxT) return false;
+// Workspace layout of a call over T tokens with the given flags (the regions do not
+// depend on the flags; tile_m and intermediate_format report the plan they choose).
+int fill_layout(int32_t T, int32_t flags, moe_mi355_workspace_layout* L) {
+    if (T < 0 || T > kMaxT) return MOE_ERR_BAD_SIZE;
+    Plan plan;
+    const int st = plan_for(T, flags, &plan);
+    if (st != MOE_OK) return st;
     const size_t R = (size_t)T * moe::kTopK;
     const int mt = moe::dispatch_max_tiles(T, kMinTileM);
     size_t off = 0;
@@ -142,11 +151,10 @@ bool fill_layout(int32_t T, moe_mi355_workspace_layout* L) {
     L->expert_out = take(R * moe::kH * 2);
     L->expert_out_wide = take(R * moe::kH * 4);
     L->total = off;
-    const Plan plan = choose_plan(T);
     L->tile_m = plan.tm;
     L->max_tiles = mt;
     L->intermediate_format = g1_hilo(plan.g1) ? 1 : plan.convert ? 2 : 0;
-    return true;
+    return MOE_OK;
 }
 
 int hip_status(hipError_t e) {
@@ -175,6 +183,90 @@ void prof_record(int slot, int stage, hipStream_t s) {
     (void)hipEventRecord(g_prof.ev[slot * (MOE_MI355_NUM_STAGES + 1) + stage], s);
 }
 
+// The forward's launch sequence over a workspace of ws_bytes at ws (the caller's, or
+// for moe_mi355_forward_noalloc the library's own).  Returns MOE_OK or a status; a
+// status from a failed launch means the earlier launches of the call may have run.
+int forward_impl(const moe_mi355_args& a, void* workspace, size_t ws_bytes, hipStream_t s) {
+    const int32_t T = a.T;
+    moe_mi355_workspace_layout L;
+    const int lst = fill_layout(T, a.flags, &L);
+    if (lst != MOE_OK) return lst;
+    if (T == 0) return MOE_OK;
+    if (!a.routing_logits || !a.routing_bias || !a.hidden_states || !a.hidden_states_scale ||
+        !a.gemm1_weights || !a.gemm1_weights_scale || !a.gemm2_weights ||
+        !a.gemm2_weights_scale || !a.output)
+        return MOE_ERR_NULL_POINTER;
+    if (!aligned16(a.routing_logits) || ((uintptr_t)a.routing_bias & 7u) ||
+        !aligned16(a.hidden_states) || ((uintptr_t)a.hidden_states_scale & 3u) ||
+        !aligned16(a.gemm1_weights) || ((uintptr_t)a.gemm1_weights_scale & 3u) ||
+        !aligned16(a.gemm2_weights) || ((uintptr_t)a.gemm2_weights_scale & 3u) ||
+        !aligned16(a.output))
+        return MOE_ERR_MISALIGNED;
+    if (!workspace || ((uintptr_t)workspace & 255u) || ws_bytes < L.total)
+        return MOE_ERR_WORKSPACE;
+    Plan plan;
+    if (plan_for(T, a.flags, &plan) != MOE_OK) return MOE_ERR_BAD_FLAGS;
+
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    int* ids = reinterpret_cast<int*>(ws + L.topk_ids);
+    float* wts = reinterpret_cast<float*>(ws + L.topk_weights);
+    int* inv = reinterpret_cast<int*>(ws + L.inverse_rows);
+    int* meta = reinterpret_cast<int*>(ws + L.meta);
+    int4* tiles = reinterpret_cast<int4*>(ws + L.tiles);
+    int* stok = reinterpret_cast<int*>(ws + L.sorted_tokens);
+    float* sw = reinterpret_cast<float*>(ws + L.sorted_weights);
+    const moe::Intermediate inter{ws + L.intermediate, reinterpret_cast<float*>(ws + L.intermediate_scales),
+                                  T * moe::kTopK};
+    const moe::ExpertRows rows{reinterpret_cast<uint16_t*>(ws + L.expert_out),
+                               reinterpret_cast<float*>(ws + L.expert_out_wide)};
+    int* chunk_cnt = reinterpret_cast<int*>(ws + L.chunk_counts);
+    float* row_scales = reinterpret_cast<float*>(ws + L.row_scales);
+    int* num_tiles = meta + moe::kEL + 1;
+
+    // The status reports this call's launches only: an error some earlier, unrelated
+    // HIP call left in this thread's last-error slot is cleared first.
+    (void)hipGetLastError();
+    const bool prof = (a.flags & MOE_MI355_FLAG_PROFILE) && g_prof.ev && g_prof.used < g_prof.slots;
+    const int slot = prof ? g_prof.used++ : 0;
+
+    if (prof) prof_record(slot, 0, s);
+    moe::launch_route(a.routing_logits, a.routing_bias, T, (float)a.routed_scaling_factor, ids,
+                      wts, meta + moe::kCWideFlag, s);
+    if (prof) prof_record(slot, 1, s);
+    const int max_tiles = moe::dispatch_max_tiles(T, plan.tm);
+    const bool half = plan.tm2 > 0;   // GEMM2 walks the second (128-row) tile list
+    int4* tiles2 = tiles + max_tiles;
+    int* num_tiles2 = meta + moe::kEL + 2;
+    bool ok = moe::launch_dispatch(ids, wts, T, clamp_offset(a.local_expert_offset), plan.tm,
+                                   plan.tm2, meta, num_tiles, tiles, stok, sw, inv, chunk_cnt, s,
+                                   half ? num_tiles2 : nullptr, half ? tiles2 : nullptr);
+    // GEMM1 reads the token scales gathered into row order (counted in the dispatch stage)
+    // or, where the gather would cost more than it saves, straight by token
+    if (ok && plan.by_row)
+        moe::launch_gather_row_scales(a.hidden_states_scale, T, stok, meta, row_scales,
+                                      T * moe::kTopK, s);
+    const moe::TokenScales sa = plan.by_row ? moe::TokenScales{row_scales, T * moe::kTopK, 1}
+                                            : moe::TokenScales{a.hidden_states_scale, T, 0};
+    if (prof) prof_record(slot, 2, s);
+    ok = ok && moe::launch_gemm1(plan.g1, a.hidden_states, sa, T, a.gemm1_weights,
+                                 a.gemm1_weights_scale, tiles, num_tiles, meta, max_tiles, stok,
+                                 inter, s);
+    if (prof) prof_record(slot, 3, s);
+    if (ok && plan.convert) moe::launch_c_f16_to_hilo(inter, meta, s);   // in the GEMM2 stage
+    if (ok && half)
+        ok = moe::launch_gemm2(plan.g2, inter, a.gemm2_weights, a.gemm2_weights_scale, tiles2,
+                               num_tiles2, meta, moe::dispatch_max_tiles(T, plan.tm2), rows, s);
+    else if (ok)
+        ok = moe::launch_gemm2(plan.g2, inter, a.gemm2_weights, a.gemm2_weights_scale, tiles,
+                               num_tiles, meta, max_tiles, rows, s);
+    if (prof) prof_record(slot, 4, s);
+    if (ok) moe::launch_combine(rows, meta + moe::kRowsWideFlag, sw, inv, T, a.output, s);
+    if (prof) prof_record(slot, 5, s);
+    const int hst = hip_status(hipGetLastError());
+    if (hst != MOE_OK) return hst;
+    return ok ? MOE_OK : MOE_ERR_BAD_PLAN;
+}
+
 }  // namespace
 
 extern "C" {
@@ -192,6 +284,8 @@ const char* moe_mi355_strerror(int status) {
         case MOE_ERR_MISALIGNED: return "a tensor pointer is not 16-byte aligned";
         case MOE_ERR_HIP: return "HIP launch failed";
         case MOE_ERR_BAD_TILE: return "unsupported tile height";
+        case MOE_ERR_BAD_FLAGS: return "unknown flag bits, or a forced kernel plan that cannot run";
+        case MOE_ERR_BAD_PLAN: return "a kernel plan names a variant its launcher does not have";
         default: return "unknown status";
     }
 }
@@ -203,14 +297,13 @@ int32_t moe_mi355_max_tiles(int32_t T, int32_t tile_m) {
 
 size_t moe_mi355_workspace_bytes(int32_t T) {
     moe_mi355_workspace_layout L;
-    if (!fill_layout(T, &L)) return 0;
+    if (fill_layout(T, 0, &L) != MOE_OK) return 0;
     return L.total;
 }
 
-int moe_mi355_get_workspace_layout(int32_t T, moe_mi355_workspace_layout* out) {
+int moe_mi355_get_workspace_layout(int32_t T, int32_t flags, moe_mi355_workspace_layout* out) {
     if (!out) return MOE_ERR_NULL_POINTER;
-    if (!fill_layout(T, out)) return MOE_ERR_BAD_SIZE;
-    return MOE_OK;
+    return fill_layout(T, flags, out);
 }
 
 int moe_mi355_route(const float* routing_logits, const uint16_t* routing_bias, int32_t T,
@@ -259,78 +352,7 @@ int moe_mi355_dispatch(const int32_t* topk_ids, const float* topk_weights, int32
 
 int moe_mi355_forward(const moe_mi355_args* a, void* stream) {
     if (!a) return MOE_ERR_NULL_POINTER;
-    const int32_t T = a->T;
-    moe_mi355_workspace_layout L;
-    if (!fill_layout(T, &L)) return MOE_ERR_BAD_SIZE;
-    if (T == 0) return MOE_OK;
-    if (!a->routing_logits || !a->routing_bias || !a->hidden_states || !a->hidden_states_scale ||
-        !a->gemm1_weights || !a->gemm1_weights_scale || !a->gemm2_weights ||
-        !a->gemm2_weights_scale || !a->output)
-        return MOE_ERR_NULL_POINTER;
-    if (!aligned16(a->routing_logits) || ((uintptr_t)a->routing_bias & 7u) ||
-        !aligned16(a->hidden_states) || ((uintptr_t)a->hidden_states_scale & 3u) ||
-        !aligned16(a->gemm1_weights) || ((uintptr_t)a->gemm1_weights_scale & 3u) ||
-        !aligned16(a->gemm2_weights) || ((uintptr_t)a->gemm2_weights_scale & 3u) ||
-        !aligned16(a->output))
-        return MOE_ERR_MISALIGNED;
-    if (!a->workspace || ((uintptr_t)a->workspace & 255u) || a->workspace_bytes < L.total)
-        return MOE_ERR_WORKSPACE;
-
-    hipStream_t s = (hipStream_t)stream;
-    uint8_t* ws = static_cast<uint8_t*>(a->workspace);
-    int* ids = reinterpret_cast<int*>(ws + L.topk_ids);
-    float* wts = reinterpret_cast<float*>(ws + L.topk_weights);
-    int* inv = reinterpret_cast<int*>(ws + L.inverse_rows);
-    int* meta = reinterpret_cast<int*>(ws + L.meta);
-    int4* tiles = reinterpret_cast<int4*>(ws + L.tiles);
-    int* stok = reinterpret_cast<int*>(ws + L.sorted_tokens);
-    float* sw = reinterpret_cast<float*>(ws + L.sorted_weights);
-    const moe::Intermediate inter{ws + L.intermediate, reinterpret_cast<float*>(ws + L.intermediate_scales),
-                                  T * moe::kTopK};
-    const moe::ExpertRows rows{reinterpret_cast<uint16_t*>(ws + L.expert_out),
-                               reinterpret_cast<float*>(ws + L.expert_out_wide)};
-    int* chunk_cnt = reinterpret_cast<int*>(ws + L.chunk_counts);
-    float* row_scales = reinterpret_cast<float*>(ws + L.row_scales);
-    int* num_tiles = meta + moe::kEL + 1;
-
-    const bool prof = (a->flags & MOE_MI355_FLAG_PROFILE) && g_prof.ev && g_prof.used < g_prof.slots;
-    const int slot = prof ? g_prof.used++ : 0;
-
-    if (prof) prof_record(slot, 0, s);
-    moe::launch_route(a->routing_logits, a->routing_bias, T, (float)a->routed_scaling_factor, ids,
-                      wts, meta + moe::kCWideFlag, s);
-    if (prof) prof_record(slot, 1, s);
-    const Plan plan = choose_plan(T);
-    const int max_tiles = moe::dispatch_max_tiles(T, plan.tm);
-    const bool half = plan.tm2 > 0;   // GEMM2 walks the second (128-row) tile list
-    int4* tiles2 = tiles + max_tiles;
-    int* num_tiles2 = meta + moe::kEL + 2;
-    moe::launch_dispatch(ids, wts, T, clamp_offset(a->local_expert_offset), plan.tm, plan.tm2, meta,
-                         num_tiles, tiles, stok, sw, inv, chunk_cnt, s, half ? num_tiles2 : nullptr,
-                         half ? tiles2 : nullptr);
-    // GEMM1 reads the token scales gathered into row order (counted in the dispatch stage)
-    // or, where the gather would cost more than it saves, straight by token
-    const bool by_row = row_scales_for(T);
-    if (by_row)
-        moe::launch_gather_row_scales(a->hidden_states_scale, T, stok, meta, row_scales,
-                                      T * moe::kTopK, s);
-    const moe::TokenScales sa = by_row ? moe::TokenScales{row_scales, T * moe::kTopK, 1}
-                                       : moe::TokenScales{a->hidden_states_scale, T, 0};
-    if (prof) prof_record(slot, 2, s);
-    moe::launch_gemm1(plan.g1, a->hidden_states, sa, T, a->gemm1_weights,
-                      a->gemm1_weights_scale, tiles, num_tiles, meta, max_tiles, stok, inter, s);
-    if (prof) prof_record(slot, 3, s);
-    if (plan.convert) moe::launch_c_f16_to_hilo(inter, meta, s);   // counted in the GEMM2 stage
-    if (half)
-        moe::launch_gemm2(plan.g2, inter, a->gemm2_weights, a->gemm2_weights_scale, tiles2,
-                          num_tiles2, meta, moe::dispatch_max_tiles(T, plan.tm2), rows, s);
-    else
-        moe::launch_gemm2(plan.g2, inter, a->gemm2_weights, a->gemm2_weights_scale, tiles,
-                          num_tiles, meta, max_tiles, rows, s);
-    if (prof) prof_record(slot, 4, s);
-    moe::launch_combine(rows, meta + moe::kRowsWideFlag, sw, inv, T, a->output, s);
-    if (prof) prof_record(slot, 5, s);
-    return hip_status(hipGetLastError());
+    return forward_impl(*a, a->workspace, a->workspace_bytes, (hipStream_t)stream);
 }
 
 int moe_mi355_profile_begin(int32_t max_calls) {

@@ -11,10 +11,12 @@ reference's ``solution/python/kernel.py:95-120``; the work behind it is the C AB
 for small T, FP8 MFMA over an fp8 hi/lo split of the SwiGLU rows for large T) ->
 ordered combine, all on the caller's current stream, no host synchronisation).
 
-The reference JIT-compiles its extension on first use (kernel.py:57-92); this one
-is compiled ahead of time by ``build.py`` into this directory.  When the library is
-missing, ``kernel`` raises -- there is no CPU or PyTorch fallback.  Set
-``MOE_MI355_JIT=1`` to let the first call compile it with hipcc instead.
+Like the reference, which JIT-compiles its extension on first use
+(kernel.py:57-92), the first call builds ``libmoe_mi355.so`` with hipcc (gfx950)
+when it is not already next to this file (``build.py`` builds it ahead of time).
+Concurrent first calls from several processes are serialised by a file lock and
+install the library atomically.  If the library can neither be found nor built,
+``kernel`` raises: there is no CPU or PyTorch fallback.
 """
 from __future__ import annotations
 
@@ -66,7 +68,18 @@ class WorkspaceLayout(ctypes.Structure):
 MAX_TOKENS = 1 << 19    # MOE_MI355_MAX_TOKENS
 
 
+# call flags of include/moe_mi355.h (MOE_MI355_FLAG_*)
 FLAG_PROFILE = 1
+FLAG_FORCE_PLAN = 2
+FLAG_ROW_SCALES_ON = 4
+FLAG_ROW_SCALES_OFF = 8
+
+
+def plan_flags(g1: int, g2: int) -> int:
+    """Flags that force the GEMM1 / GEMM2 variant pair (MOE_MI355_FLAGS_PLAN)."""
+    return FLAG_FORCE_PLAN | ((int(g1) & 15) << 8) | ((int(g2) & 15) << 12)
+
+
 NUM_STAGES = 5
 STAGES = ("route", "dispatch", "gemm1", "gemm2", "combine")
 
@@ -79,7 +92,7 @@ def _declare(L: ctypes.CDLL) -> ctypes.CDLL:
         "moe_mi355_route": (ctypes.c_int, [P, P, I32, D, P, P, P]),
         "moe_mi355_dispatch": (ctypes.c_int, [P, P, I32, I64, I32, P, P, P, P, P, P, P, P]),
         "moe_mi355_max_tiles": (I32, [I32, I32]),
-        "moe_mi355_get_workspace_layout": (ctypes.c_int, [I32, ctypes.POINTER(WorkspaceLayout)]),
+        "moe_mi355_get_workspace_layout": (ctypes.c_int, [I32, I32, ctypes.POINTER(WorkspaceLayout)]),
         "moe_mi355_profile_begin": (ctypes.c_int, [I32]),
         "moe_mi355_profile_read": (ctypes.c_int, [P, I32]),
         "moe_mi355_profile_end": (ctypes.c_int, []),
@@ -98,7 +111,7 @@ def _declare(L: ctypes.CDLL) -> ctypes.CDLL:
 
 
 def _build_extension() -> ctypes.CDLL:
-    """Load (or, with MOE_MI355_JIT=1, first compile) the HIP library."""
+    """Load the HIP library, building it first if it is not there (kernel.py:57-92)."""
     global _lib
     if _lib is not None:
         return _lib
@@ -106,16 +119,15 @@ def _build_extension() -> ctypes.CDLL:
         if _lib is not None:
             return _lib
         if not os.path.exists(_LIB_PATH):
-            if os.environ.get("MOE_MI355_JIT") == "1":
-                import importlib.util
-                spec = importlib.util.spec_from_file_location("_moe_mi355_build", os.path.join(_HERE, "build.py"))
-                mod = importlib.util.module_from_spec(spec)
-                spec.loader.exec_module(mod)
-                mod.build(verbose=False)
-            else:
-                raise RuntimeError(
-                    f"{_LIB_PATH} is not built; run `python {os.path.join(_HERE, 'build.py')}` "
-                    "(or set MOE_MI355_JIT=1). There is no fallback path.")
+            import importlib.util
+            spec = importlib.util.spec_from_file_location("_moe_mi355_build", os.path.join(_HERE, "build.py"))
+            mod = importlib.util.module_from_spec(spec)
+            spec.loader.exec_module(mod)
+            try:
+                mod.ensure_built()
+            except Exception as e:
+                raise RuntimeError(f"{_LIB_PATH} is missing and could not be built "
+                                   f"(there is no fallback path): {e}") from e
         _lib = _declare(ctypes.CDLL(_LIB_PATH))
     return _lib
 
@@ -149,10 +161,12 @@ def workspace_bytes(T: int) -> int:
     return int(_build_extension().moe_mi355_workspace_bytes(int(T)))
 
 
-def workspace_layout(T: int) -> WorkspaceLayout:
+def workspace_layout(T: int, flags: int = 0) -> WorkspaceLayout:
+    """Workspace regions of a call over T tokens, and the plan a call with `flags` runs."""
     L = _build_extension()
     lay = WorkspaceLayout()
-    _check(L.moe_mi355_get_workspace_layout(int(T), ctypes.byref(lay)), "moe_mi355_get_workspace_layout")
+    _check(L.moe_mi355_get_workspace_layout(int(T), int(flags), ctypes.byref(lay)),
+           "moe_mi355_get_workspace_layout")
     return lay
 
 
@@ -230,7 +244,8 @@ def forward(routing_logits, routing_bias, hidden_states, hidden_states_scale, ge
             flags: int = 0):
     """``kernel`` with a caller-supplied uint8 workspace (>= workspace_bytes(T),
     256-byte aligned; it can be inspected afterwards with workspace_layout) and call
-    flags (FLAG_PROFILE records the stage profiler's events)."""
+    flags (FLAG_PROFILE records the stage profiler's events; plan_flags(g1, g2) and
+    FLAG_ROW_SCALES_ON / _OFF force a kernel plan for tuning and tests)."""
     L = _build_extension()
     T, logits, hs_scale = validate(routing_logits, routing_bias, hidden_states,
                                    hidden_states_scale, gemm1_weights, gemm1_weights_scale,

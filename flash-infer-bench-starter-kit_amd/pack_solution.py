@@ -14,9 +14,9 @@ destination passing takes exactly the definition's 10 inputs + 1 output.
 
 Sources: every text file the solution needs to build and run from its own directory
 (kernel.py, build.py, the HIP sources and headers, the C-ABI header as
-``include/moe_mi355.h``).  The compiled ``libmoe_mi355.so`` is not a source; the
-harness side builds it with ``python build.py`` (hipcc for gfx950) or sets
-``MOE_MI355_JIT=1`` to let kernel.py build it on first use.
+``include/moe_mi355.h``).  The compiled ``libmoe_mi355.so`` is not a source:
+kernel.py builds it with hipcc (gfx950) on first use, as the reference's kernel.py
+JIT-compiles its extension, or ``python build.py`` builds it ahead of time.
 
 Usage: ``python pack_solution.py [-o solution.json]``.
 """

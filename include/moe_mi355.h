@@ -56,7 +56,12 @@ typedef enum moe_mi355_status {
     MOE_ERR_WORKSPACE = -3,        /* workspace NULL, misaligned or too small */
     MOE_ERR_MISALIGNED = -4,       /* a tensor pointer is not 16-byte aligned */
     MOE_ERR_HIP = -5,              /* a HIP launch failed (see moe_mi355_last_hip_error) */
-    MOE_ERR_BAD_TILE = -6          /* tile_m not supported */
+    MOE_ERR_BAD_TILE = -6,         /* tile_m not supported */
+    MOE_ERR_BAD_FLAGS = -7,        /* unknown flag bits, or a forced kernel plan that
+                                      cannot run (MOE_MI355_FLAG_FORCE_PLAN) */
+    MOE_ERR_BAD_PLAN = -8          /* internal: a kernel plan names a variant that its
+                                      launcher does not have (earlier launches of the
+                                      call may have run; the output is not valid) */
 } moe_mi355_status;
 
 /* Arguments of one forward call.  Mirrors kernel.py:95-107 / main.cpp:66-77:
@@ -92,8 +97,29 @@ typedef struct moe_mi355_args {
     size_t workspace_bytes;
 } moe_mi355_args;
 
-/* Record per-stage HIP events for the profiler (moe_mi355_profile_*). */
+/* Call flags (moe_mi355_args.flags).  Without any, the library picks its kernel plan
+ * from T alone; nothing else (no environment variable) changes it.
+ *   MOE_MI355_FLAG_PROFILE         record per-stage HIP events (moe_mi355_profile_*)
+ *   MOE_MI355_FLAG_FORCE_PLAN      run the GEMM1 / GEMM2 variant pair in bits 8-11 /
+ *                                  12-15 (MOE_MI355_FLAGS_PLAN(g1, g2)); for tuning
+ *                                  sweeps and tests.  GEMM1: 1 streaming 16-row tiles,
+ *                                  2 streaming 32-row tiles, 3 prefill 128-row tiles,
+ *                                  4 prefill 256-row tiles; GEMM2: 1, 2 streaming 16-row,
+ *                                  3 streaming 32-row, 4 prefill 128-row, 5 prefill on a
+ *                                  second list of 128-row tiles.  A pair that cannot run
+ *                                  together gives MOE_ERR_BAD_FLAGS.
+ *   MOE_MI355_FLAG_ROW_SCALES_ON / _OFF  GEMM1 reads the token scales gathered into row
+ *                                  order / straight by token (default: gathered from
+ *                                  T = 512).  Bit-identical results either way.
+ * Every variant meets the same tolerance; the flags change speed only. */
 #define MOE_MI355_FLAG_PROFILE 1
+#define MOE_MI355_FLAG_FORCE_PLAN 2
+#define MOE_MI355_FLAG_ROW_SCALES_ON 4
+#define MOE_MI355_FLAG_ROW_SCALES_OFF 8
+#define MOE_MI355_FLAGS_PLAN(g1, g2) \
+    (MOE_MI355_FLAG_FORCE_PLAN | (((g1) & 15) << 8) | (((g2) & 15) << 12))
+#define MOE_MI355_FLAGS_G1(flags) (((flags) >> 8) & 15)
+#define MOE_MI355_FLAGS_G2(flags) (((flags) >> 12) & 15)
 
 /* Bytes of workspace a forward call over T tokens needs. */
 MOE_MI355_API size_t moe_mi355_workspace_bytes(int32_t T);
@@ -185,7 +211,11 @@ typedef struct moe_mi355_workspace_layout {
     int32_t intermediate_format;
 } moe_mi355_workspace_layout;
 
-MOE_MI355_API int moe_mi355_get_workspace_layout(int32_t T, moe_mi355_workspace_layout* out);
+/* The layout of a call over T tokens with the given call flags: the regions do not
+ * depend on the flags; tile_m and intermediate_format report the kernel plan that a
+ * forward call with the same T and flags runs. */
+MOE_MI355_API int moe_mi355_get_workspace_layout(int32_t T, int32_t flags,
+                                                 moe_mi355_workspace_layout* out);
 
 /* Stage profiler: with MOE_MI355_FLAG_PROFILE set, each forward call records HIP
  * events around each of its kernels into a ring of `max_calls` slots.

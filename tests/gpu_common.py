@@ -38,12 +38,17 @@ def first_tokens(d0: dict, T: int) -> dict:
     return d
 
 
-def run_forward(d: dict, **kw) -> torch.Tensor:
+def run_forward(d: dict, flags: int = 0, **kw) -> torch.Tensor:
+    """One forward call on a NaN-filled output: through the DPS entry `kernel`, or
+    through `forward` when call flags are given."""
     k = pkg("kernel")
     wl = pkg("workloads")
     out = torch.full_like(d["output"], float("nan"))
     args = wl.as_args({**d, "output": out, **kw})
-    k.kernel(*args)
+    if flags:
+        k.forward(*args, flags=flags)
+    else:
+        k.kernel(*args)
     torch.cuda.synchronize()
     return out
 

@@ -159,3 +159,70 @@ def test_no_oracle_import_in_product():
             if f.endswith((".py", ".hip", ".h", ".cpp")):
                 text = open(os.path.join(root, f)).read()
                 assert "moe_oracle" not in text and "oracle/" not in text, f
+
+
+def _fake_args(k, T=4):
+    """Arguments whose pointers are aligned but point nowhere: only calls that the
+    library rejects before any launch may use them."""
+    a = k.MoeArgs()
+    fake = 1 << 20
+    for f in ("routing_logits", "routing_bias", "hidden_states", "hidden_states_scale",
+              "gemm1_weights", "gemm1_weights_scale", "gemm2_weights", "gemm2_weights_scale",
+              "output", "workspace"):
+        setattr(a, f, fake)
+    a.T = T
+    a.workspace_bytes = k.workspace_bytes(T)
+    return a
+
+
+@pytest.mark.parametrize("g1,g2", [(4, 1), (3, 3), (1, 4), (2, 2), (0, 1), (5, 5), (3, 5)])
+def test_forced_plan_that_cannot_run_is_an_error(lib, g1, g2):
+    """A GEMM pair that cannot run together (GEMM1 writes hi/lo C but GEMM2 reads fp16,
+    mismatched tile heights, unknown variants) is rejected before any launch with
+    MOE_ERR_BAD_FLAGS, and the Python entry turns the status into a RuntimeError."""
+    k = pkg("kernel")
+    a = _fake_args(k)
+    a.flags = k.plan_flags(g1, g2)
+    rc = lib.moe_mi355_forward(ctypes.byref(a), None)
+    assert rc == -7
+    assert "forced kernel plan" in lib.moe_mi355_strerror(rc).decode()
+    with pytest.raises(RuntimeError, match="moe_mi355_forward failed: unknown flag bits"):
+        k._check(rc, "moe_mi355_forward")
+    lay = k.WorkspaceLayout()
+    assert lib.moe_mi355_get_workspace_layout(4, a.flags, ctypes.byref(lay)) == -7
+
+
+@pytest.mark.parametrize("flags", [1 << 20, 1 << 9, 4 | 8, 1 << 31])
+def test_unknown_flag_bits_are_an_error(lib, flags):
+    """Unknown bits, variant bits without the force bit, and both token-scale forms at
+    once are rejected."""
+    k = pkg("kernel")
+    a = _fake_args(k)
+    a.flags = flags - (1 << 32) if flags >= 1 << 31 else flags
+    assert lib.moe_mi355_forward(ctypes.byref(a), None) == -7
+
+
+def test_layout_reports_the_forced_plan():
+    k = pkg("kernel")
+    assert k.workspace_layout(64).tile_m == 16 and k.workspace_layout(64).intermediate_format == 0
+    lay = k.workspace_layout(64, k.plan_flags(3, 4))
+    assert lay.tile_m == 128 and lay.intermediate_format == 1
+    lay = k.workspace_layout(64, k.plan_flags(2, 5))
+    assert lay.tile_m == 32 and lay.intermediate_format == 2
+    assert lay.total == k.workspace_layout(64).total
+    assert k.workspace_layout(9000).tile_m == 256
+
+
+def test_environment_does_not_change_the_plan():
+    """The library reads no environment: variables that older builds read for plan
+    overrides leave the plan alone."""
+    import subprocess
+    import sys
+    code = ("import sys; sys.path.insert(0, %r); from conftest import pkg; "
+            "k = pkg('kernel'); l = k.workspace_layout(64); print(l.tile_m, l.intermediate_format)"
+            % os.path.join(REPO, "tests"))
+    env = dict(os.environ, MOE_MI355_G1="4", MOE_MI355_G2="5", MOE_MI355_ROW_SCALES="1")
+    out = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True,
+                         cwd=os.path.join(REPO, "tests"), timeout=300)
+    assert out.returncode == 0, out.stderr
+    assert out.stdout.split() == ["16", "0"]

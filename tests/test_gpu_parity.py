@@ -173,24 +173,23 @@ def test_forward_routing_in_workspace_is_bit_exact(T):
 
 
 @pytest.mark.parametrize("T,g1,g2", [(1500, 3, 4), (1500, 4, 5), (8192, 4, 5), (1024, 2, 5)])
-def test_prefill_intermediate_hilo_rows(T, g1, g2, monkeypatch):
-    """The prefill GEMM1 kernels (128-row tiles, forced through MOE_MI355_G1 / _G2, and
+def test_prefill_intermediate_hilo_rows(T, g1, g2):
+    """The prefill GEMM1 kernels (128-row tiles, forced through the plan flags, and
     the default 256-row tiles) write C in the fp8 hi/lo form, and the conversion kernel
     turns the streaming GEMM1's fp16 C into it (T = 1024); rebuilt rows match the fp32
     SwiGLU of the oracle to within the form's precision (2^-8 relative, plus the fp32
     GEMM's own rounding and, converted, the fp16 rounding)."""
-    monkeypatch.setenv("MOE_MI355_G1", str(g1))
-    monkeypatch.setenv("MOE_MI355_G2", str(g2))
     k = pkg("kernel")
+    flags = k.plan_flags(g1, g2)
     o = oracle()
     wl = pkg("workloads")
     d = first_tokens(config_inputs(3), T)
-    lay = k.workspace_layout(T)
+    lay = k.workspace_layout(T, flags)
     assert lay.intermediate_format in (1, 2)
     ws = torch.empty(lay.total, dtype=torch.uint8, device="cuda")
     out = torch.empty_like(d["output"])
-    note(f"[gpu] hi/lo intermediate T={T}")
-    k.forward(*wl.as_args({**d, "output": out}), workspace=ws)
+    note(f"[gpu] hi/lo intermediate T={T} g1={g1} g2={g2}")
+    k.forward(*wl.as_args({**d, "output": out}), workspace=ws, flags=flags)
     torch.cuda.synchronize()
     R = T * 8
     exp_off = ws[lay.meta:lay.meta + 33 * 4].view(torch.int32).cpu().numpy()

@@ -127,14 +127,12 @@ def test_plan_boundaries_match_oracle(T):
 @pytest.mark.parametrize("T,g1,g2", [(64, 1, 1), (64, 1, 2), (150, 1, 2), (64, 2, 3),
                                      (500, 2, 3), (1000, 3, 4), (3000, 4, 5), (1000, 2, 5),
                                      (150, 1, 5)])
-def test_every_gemm_variant_matches_oracle(T, g1, g2, monkeypatch):
-    """Each GEMM1 / GEMM2 kernel variant (forced with MOE_MI355_G1 / _G2, which the
-    library reads on every call) stays within the tolerance."""
+def test_every_gemm_variant_matches_oracle(T, g1, g2):
+    """Each GEMM1 / GEMM2 kernel variant (forced with the call's plan flags) stays
+    within the tolerance."""
     d = first_tokens(config_inputs(3), T)
-    monkeypatch.setenv("MOE_MI355_G1", str(g1))
-    monkeypatch.setenv("MOE_MI355_G2", str(g2))
     note(f"[gpu] variants g1={g1} g2={g2} T={T}")
-    out = run_forward(d)
+    out = run_forward(d, flags=pkg("kernel").plan_flags(g1, g2))
     rng = np.random.default_rng(T + 7)
     toks = sorted(rng.choice(T, 16, replace=False).tolist())
     st = compare_to_oracle(d, out, toks)
@@ -162,21 +160,21 @@ def test_batch_sizes_between_plan_boundaries(T, offset):
 
 
 @pytest.mark.parametrize("T", [64, 200, 1024, 3000])
-def test_row_order_token_scales_change_nothing(T, monkeypatch):
-    """GEMM1 reading the token scales gathered into row order (MOE_MI355_ROW_SCALES=1)
-    or straight by token (=0) gives bit-identical outputs on every plan; the gathered
-    table holds hidden_states_scale[kb][sorted_tokens[row]] for the rows in use."""
+def test_row_order_token_scales_change_nothing(T):
+    """GEMM1 reading the token scales gathered into row order (FLAG_ROW_SCALES_ON)
+    or straight by token (FLAG_ROW_SCALES_OFF) gives bit-identical outputs on every
+    plan; the gathered table holds hidden_states_scale[kb][sorted_tokens[row]] for
+    the rows in use."""
     d = first_tokens(config_inputs(3), T)
     k = pkg("kernel")
     wl = pkg("workloads")
     lay = k.workspace_layout(T)
     outs = []
-    for flag in ("0", "1"):
-        monkeypatch.setenv("MOE_MI355_ROW_SCALES", flag)
-        note(f"[gpu] row-order token scales {flag} T={T}")
+    for flag in (k.FLAG_ROW_SCALES_OFF, k.FLAG_ROW_SCALES_ON):
+        note(f"[gpu] row-order token scales flag {flag} T={T}")
         ws = torch.empty(lay.total, dtype=torch.uint8, device="cuda")
         out = torch.full_like(d["output"], float("nan"))
-        k.forward(*wl.as_args({**d, "output": out}), workspace=ws)
+        k.forward(*wl.as_args({**d, "output": out}), workspace=ws, flags=flag)
         torch.cuda.synchronize()
         outs.append(out)
     assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))

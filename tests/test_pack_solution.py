@@ -75,3 +75,32 @@ def test_builder_check_rejects_planted_entry_points(packer, tmp_path, src, msg):
 def test_value_returning_entry_allows_other_counts(packer, tmp_path):
     (tmp_path / "kernel.py").write_text("def kernel(a, b):\n    return a\n")
     packer.check_entry_point("kernel.py::kernel", False, root=str(tmp_path))
+
+
+def test_unpacked_solution_builds_on_first_use_from_two_processes(packer, tmp_path):
+    """A packed solution carries no library: the first call of kernel.py builds it, as
+    the reference's kernel.py JIT-compiles on first use (kernel.py:57-92).  Two worker
+    processes that load the solution at the same moment both end up with a working
+    library: the build runs under a file lock in a private directory and is installed
+    with one atomic rename, so neither loads a half-written file."""
+    import subprocess
+    import sys
+    out = packer.pack_solution(str(tmp_path / "solution.json"))
+    dest = tmp_path / "unpacked"
+    packer.unpack_solution(out, str(dest))
+    assert not (dest / "libmoe_mi355.so").exists()
+    code = ("import importlib.util, sys\n"
+            "spec = importlib.util.spec_from_file_location('k', sys.argv[1])\n"
+            "m = importlib.util.module_from_spec(spec); spec.loader.exec_module(m)\n"
+            "lib = m._build_extension()\n"
+            "print(lib.moe_mi355_version().decode(), lib.moe_mi355_workspace_bytes(64))\n")
+    procs = [subprocess.Popen([sys.executable, "-c", code, str(dest / "kernel.py")],
+                              stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)
+             for _ in range(2)]
+    outs = [p.communicate(timeout=600) for p in procs]
+    for p, (o, e) in zip(procs, outs):
+        assert p.returncode == 0, e
+        assert o.startswith("moe_mi355"), o
+    assert outs[0][0] == outs[1][0]
+    assert (dest / "libmoe_mi355.so").exists()
+    assert not [f for f in os.listdir(dest) if f.startswith("_build.")]   # private dirs removed
