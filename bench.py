@@ -5,15 +5,20 @@ experts) on one GPU.
     python bench.py [--steps K] [--warmup W] [--config IDX] [--gpus 1]
 
 A step is one call of ``kernel(...)`` (route -> dispatch -> GEMM1+SwiGLU -> GEMM2 ->
-combine) over one batch of seeded synthetic inputs already resident in HBM.
-Default workload: configs[1] of BASELINE.json (decode, T=64).  Weights and
-activations rotate over ``--rotate`` copies so that consecutive steps do not find
+combine) over one batch of seeded synthetic inputs already resident in HBM.  Weights
+and activations rotate over ``--rotate`` copies so that consecutive steps do not find
 the previous step's weights in the 256 MB MALL.
 
-Prints ONE JSON line: latency (us per call), effective TFLOP/s, the roofline of the
-dominant kernel measured with HIP events on the library's stream, and the CPU
-baseline (the reference's CPU-shaped path, moe.cu:137-240, restated in torch-CPU)
-timed on this host on a bounded sample.
+The headline (``value``) is configs[1] of BASELINE.json (decode, T=64): W untimed
+warmup steps, then exactly K timed steps between two ``torch.cuda.synchronize()``.
+Without ``--config``, every one of the five configs is measured the same way
+(K steps after W warmup, at least 20 warmup steps so the GPU reaches steady clocks)
+and reported in ``per_config``: latency, effective TFLOP/s, the fraction of the
+whole call's roofline, the roofline of the dominant kernel measured with HIP events
+on the library's stream, and the CPU baseline (the reference's CPU-shaped path,
+moe.cu:137-240, restated in torch-CPU) timed on this host on a bounded sample.
+
+Prints ONE JSON line.
 """
 from __future__ import annotations
 
@@ -27,9 +32,11 @@ REPO = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.join(REPO, "flash-infer-bench-starter-kit_amd")
 
 METRIC = "fused-MoE latency (us) + eff. TFLOPS vs T; % HBM / FP8-MFMA roofline"
+HEADLINE_CONFIG = 1
 HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0
 BF16_PEAK_TFLOPS = 2500.0
+MIN_CONFIG_WARMUP = 20
 
 
 def _load(name: str, path: str):
@@ -48,15 +55,16 @@ def log(msg: str) -> None:
 def parse():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
-    # 30 warmup calls bring the GPU to its steady clocks after the host-side set-up (with
-    # 5, the first timed calls of a 50-call run were measured up to 4% slower)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=30)
-    ap.add_argument("--config", type=int, default=1, help="index into BASELINE.json configs")
+    ap.add_argument("--config", type=int, default=None,
+                    help="measure only this index of BASELINE.json configs (it becomes the headline)")
     ap.add_argument("--rotate", type=int, default=4, help="input copies cycled over steps")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="skip the HIP-graph replay timing")
-    ap.add_argument("--cpu-budget-s", type=float, default=20.0)
+    ap.add_argument("--no-quantizer", action="store_true", help="skip the quantizer leg")
+    ap.add_argument("--cpu-budget-s", type=float, default=8.0,
+                    help="CPU-baseline time budget per config (seconds)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run K device-to-device copies of MIB MiB (calibrates "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE against known bytes)")
@@ -88,26 +96,73 @@ def traffic_from_profiles(workload: str, kernel: str):
     return None
 
 
-def main() -> int:
-    a = parse()
-    if a.gpus != 1:
-        print(f"bench.py measures one GPU only (one expert-parallel rank's share); "
-              f"--gpus {a.gpus} is not supported in this build.", file=sys.stderr)
-        return 2
-    if a.copy_calibration:
-        return copy_calibration(a.copy_calibration, a.steps)
+def kernel_work(stage: str, T: int, n_a: int, e_a: int, touched: int) -> dict:
+    """Algorithmic bytes and flops of one launch of a stage's kernel (never padded
+    rows): the per-unit figures times the units the launch processes."""
+    return {
+        "gemm1": dict(bytes=e_a * (4096 * 7168 + 32 * 56 * 4) + touched * (7168 + 56 * 4) + n_a * 2048 * 2,
+                      flops=n_a * 2 * 7168 * 4096, peak_tflops=FP8_PEAK_TFLOPS),
+        # GEMM2 runs fp16 MFMA (streaming) or two FP8 MFMAs per product (prefill hi/lo):
+        # either way its MFMA ceiling on the algorithmic flops is the 16-bit rate
+        "gemm2": dict(bytes=e_a * (7168 * 2048 + 56 * 16 * 4) + n_a * 2048 * 2 + n_a * 7168 * 2,
+                      flops=n_a * 2 * 2048 * 7168, peak_tflops=BF16_PEAK_TFLOPS),
+        "combine": dict(bytes=n_a * 7168 * 2 + T * 7168 * 2 + T * 8 * 4 + n_a * 4, flops=0,
+                        peak_tflops=FP8_PEAK_TFLOPS),
+        "route": dict(bytes=T * 256 * 4 + 512 + T * 8 * 8, flops=0, peak_tflops=FP8_PEAK_TFLOPS),
+        "dispatch": dict(bytes=T * 8 * 8 * 2 + n_a * 8, flops=0, peak_tflops=FP8_PEAK_TFLOPS),
+    }[stage]
 
+
+def roofline_of(stage: str, us: float, work: dict, workload: str) -> dict:
+    dur_s = us * 1e-6
+    ridge = work["peak_tflops"] * 1e12 / (HBM_PEAK_GBS * 1e9)
+    intensity = work["flops"] / max(1, work["bytes"])
+    if intensity > ridge:
+        ach = work["flops"] / dur_s / 1e12
+        roof = dict(bound="mfma", achieved=ach, peak=work["peak_tflops"], unit="TFLOP/s",
+                    frac=ach / work["peak_tflops"])
+    else:
+        ach = work["bytes"] / dur_s / 1e9
+        roof = dict(bound="hbm", achieved=ach, peak=HBM_PEAK_GBS, unit="GB/s", frac=ach / HBM_PEAK_GBS)
+    roof.update(kernel=stage, algorithmic_bytes=work["bytes"], algorithmic_flops=work["flops"],
+                kernel_us=us, traffic=traffic_from_profiles(workload, stage))
+    return roof
+
+
+def cpu_baseline(o, wl, base: dict, cfg, budget_s: float) -> dict:
+    """reference_cpu_forward (moe.cu's control flow: fp32 dequant of all 32 experts in
+    every call, routing, per-expert loop) on the host cores, 1 warmup + timed calls
+    until the budget runs out (at most 5); median."""
+    import numpy as np
+    import torch
+    ncores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(ncores)
+    host = {kk: (v.detach().cpu() if isinstance(v, torch.Tensor) else v) for kk, v in base.items()}
+    out_cpu = torch.empty_like(host["output"])
+    cargs = wl.as_args({**host, "output": out_cpu})
+    times = []
+    tb = time.perf_counter()
+    while True:
+        c0 = time.perf_counter()
+        o.reference_cpu_forward(*cargs)
+        times.append(time.perf_counter() - c0)
+        if len(times) >= 2 and (time.perf_counter() - tb + times[-1] > budget_s or len(times) >= 6):
+            break
+    timed = times[1:]
+    del host, cargs
+    return dict(value=float(np.median(timed)) * 1e3, unit="ms/call", cores=torch.get_num_threads(),
+                kind="port",
+                sample=f"{len(timed)} timed full calls of {cfg.name} (T={cfg.T}) after 1 warmup; "
+                       f"fp32 dequant of all 32 experts inside each call as in moe.cu:164-176")
+
+
+def measure_config(idx: int, a, k, wl, o, steps: int, warmup: int, quantizer: bool) -> dict:
     import numpy as np
     import torch
 
-    k = _load("moe_mi355_kernel", os.path.join(PKG, "kernel.py"))
-    wl = _load("moe_mi355_workloads", os.path.join(PKG, "workloads.py"))
-    k._build_extension()  # fail loudly before any timing if the library is missing
-
-    cfg = wl.CONFIGS[a.config]
+    cfg = wl.CONFIGS[idx]
     dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    log(f"[bench] config {a.config} {cfg.name} T={cfg.T}: generating inputs")
+    log(f"[bench] config {idx} {cfg.name} T={cfg.T}: generating inputs")
     base = wl.make_inputs(cfg, device=dev)
     copies = [base]
     for _ in range(max(0, a.rotate - 1)):
@@ -122,27 +177,27 @@ def main() -> int:
     work = wl.algorithmic_work(ids, cfg.local_expert_offset, T)
     le = ids.to(torch.int64) - cfg.local_expert_offset
     touched = int(((le >= 0) & (le < 32)).any(dim=1).sum())
+    n_a, e_a = work["N_a"], work["E_a"]
 
-    # warmup
-    for i in range(a.warmup):
+    for i in range(warmup):
         k.forward(*arglists[i % len(arglists)], workspace=ws)
     torch.cuda.synchronize()
 
-    # timed region: exactly K steps back to back, synchronised on both sides
+    # timed region: exactly `steps` calls back to back, synchronised on both sides
     stream = torch.cuda.current_stream(dev)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(a.steps):
+    for i in range(steps):
         k.forward(*arglists[i % len(arglists)], workspace=ws)
     torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    ms_per_step = (t1 - t0) * 1e3 / a.steps
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / steps
+    log(f"[bench] config {idx}: {ms_per_step * 1e3:.1f} us per call")
 
     # per-call distribution: a second pass with events around each call (the event
     # packets themselves add a few microseconds per call, so this is not the value)
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(a.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(a.steps)]
-    for i in range(a.steps):
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    for i in range(steps):
         starts[i].record(stream)
         k.forward(*arglists[i % len(arglists)], workspace=ws)
         ends[i].record(stream)
@@ -150,8 +205,8 @@ def main() -> int:
     ev_us = np.array([s.elapsed_time(e) * 1e3 for s, e in zip(starts, ends)])
 
     # per-kernel durations: HIP events recorded by the library on its launch stream
-    k.profile_begin(a.steps)
-    for i in range(a.steps):
+    k.profile_begin(steps)
+    for i in range(steps):
         k.forward(*arglists[i % len(arglists)], workspace=ws, flags=k.FLAG_PROFILE)
     torch.cuda.synchronize()
     n_prof, stage_ms = k.profile_read()
@@ -176,123 +231,73 @@ def main() -> int:
             with torch.cuda.graph(g):
                 k.forward(*al, workspace=ws)
             graphs.append(g)
-        for i in range(a.warmup):
+        for i in range(warmup):
             graphs[i % len(graphs)].replay()
         torch.cuda.synchronize()
         g0 = time.perf_counter()
-        for i in range(a.steps):
+        for i in range(steps):
             graphs[i % len(graphs)].replay()
         torch.cuda.synchronize()
-        graph_us = (time.perf_counter() - g0) * 1e6 / a.steps
+        graph_us = (time.perf_counter() - g0) * 1e6 / steps
+        del graphs
 
     # the step before the operator: blockwise FP8 quantizer of bf16 activations
     # [T, 7168] (algorithmic bytes: read 2 B, write 1 B per element, 4 B per scale)
-    xq = [torch.randn(T, 7168, device=dev).to(torch.bfloat16) for _ in range(2)]
-    qo = torch.empty(T, 7168, dtype=torch.float8_e4m3fn, device=dev)
-    qs = torch.empty(56, T, dtype=torch.float32, device=dev)
-    for i in range(a.warmup):
-        k.quantize_fp8_blockwise(xq[i % 2], qo, qs)
-    qe0, qe1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    qe0.record(stream)
-    for i in range(a.steps):
-        k.quantize_fp8_blockwise(xq[i % 2], qo, qs)
-    qe1.record(stream)
-    torch.cuda.synchronize()
-    q_us = qe0.elapsed_time(qe1) * 1e3 / a.steps
-    q_bytes = T * 7168 * 3 + T * 56 * 4
-    quant = dict(us=round(q_us, 3), bytes=q_bytes, gbs=q_bytes / (q_us * 1e-6) / 1e9,
-                 hbm_frac=q_bytes / (q_us * 1e-6) / (HBM_PEAK_GBS * 1e9),
-                 input="bf16 [T, 7168] -> e4m3 + fp32 [56, T]")
-    del xq
+    quant = None
+    if quantizer:
+        xq = [torch.randn(T, 7168, device=dev).to(torch.bfloat16) for _ in range(2)]
+        qo = torch.empty(T, 7168, dtype=torch.float8_e4m3fn, device=dev)
+        qs = torch.empty(56, T, dtype=torch.float32, device=dev)
+        for i in range(warmup):
+            k.quantize_fp8_blockwise(xq[i % 2], qo, qs)
+        qe0, qe1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        qe0.record(stream)
+        for i in range(steps):
+            k.quantize_fp8_blockwise(xq[i % 2], qo, qs)
+        qe1.record(stream)
+        torch.cuda.synchronize()
+        q_us = qe0.elapsed_time(qe1) * 1e3 / steps
+        q_bytes = T * 7168 * 3 + T * 56 * 4
+        quant = dict(us=round(q_us, 3), bytes=q_bytes, gbs=q_bytes / (q_us * 1e-6) / 1e9,
+                     hbm_frac=q_bytes / (q_us * 1e-6) / (HBM_PEAK_GBS * 1e9),
+                     input="bf16 [T, 7168] -> e4m3 + fp32 [56, T]")
+        del xq
 
     # roofline of the dominant kernel (algorithmic bytes / flops, never padded rows)
     dom = max(("gemm1", "gemm2", "combine", "route", "dispatch"), key=lambda s: stages_us[s])
-    n_a, e_a = work["N_a"], work["E_a"]
-    per_kernel = {
-        "gemm1": dict(bytes=e_a * (4096 * 7168 + 32 * 56 * 4) + touched * (7168 + 56 * 4) + n_a * 2048 * 2,
-                      flops=n_a * 2 * 7168 * 4096, peak_tflops=FP8_PEAK_TFLOPS),
-        # GEMM2 runs fp16 MFMA (streaming) or two FP8 MFMAs per product (prefill hi/lo):
-        # either way its MFMA ceiling on the algorithmic flops is the 16-bit rate
-        "gemm2": dict(bytes=e_a * (7168 * 2048 + 56 * 16 * 4) + n_a * 2048 * 2 + n_a * 7168 * 2,
-                      flops=n_a * 2 * 2048 * 7168, peak_tflops=BF16_PEAK_TFLOPS),
-        "combine": dict(bytes=n_a * 7168 * 2 + T * 7168 * 2 + T * 8 * 4 + n_a * 4, flops=0,
-                        peak_tflops=FP8_PEAK_TFLOPS),
-        "route": dict(bytes=T * 256 * 4 + 512 + T * 8 * 8, flops=0, peak_tflops=FP8_PEAK_TFLOPS),
-        "dispatch": dict(bytes=T * 8 * 8 * 2 + n_a * 8, flops=0, peak_tflops=FP8_PEAK_TFLOPS),
-    }[dom]
-    dur_s = stages_us[dom] * 1e-6
-    ridge = per_kernel["peak_tflops"] * 1e12 / (HBM_PEAK_GBS * 1e9)
-    intensity = per_kernel["flops"] / max(1, per_kernel["bytes"])
-    if intensity > ridge:
-        ach = per_kernel["flops"] / dur_s / 1e12
-        roof = dict(bound="mfma", achieved=ach, peak=per_kernel["peak_tflops"], unit="TFLOP/s",
-                    frac=ach / per_kernel["peak_tflops"])
-    else:
-        ach = per_kernel["bytes"] / dur_s / 1e9
-        roof = dict(bound="hbm", achieved=ach, peak=HBM_PEAK_GBS, unit="GB/s", frac=ach / HBM_PEAK_GBS)
-    roof["kernel"] = dom
-    roof["algorithmic_bytes"] = per_kernel["bytes"]
-    roof["algorithmic_flops"] = per_kernel["flops"]
-    roof["kernel_us"] = stages_us[dom]
-    roof["traffic"] = traffic_from_profiles(cfg.name, dom)
+    roof = roofline_of(dom, stages_us[dom], kernel_work(dom, T, n_a, e_a, touched), cfg.name)
 
     lat_us = ms_per_step * 1e3
     eff_tflops = work["flops"] / (lat_us * 1e-6) / 1e12
     floor_us = max(work["bytes"] / (HBM_PEAK_GBS * 1e9),
                    (n_a * 2 * 7168 * 4096) / (FP8_PEAK_TFLOPS * 1e12)
                    + (n_a * 2 * 2048 * 7168) / (BF16_PEAK_TFLOPS * 1e12)) * 1e6
-
-    # CPU baseline: the reference's CPU-shaped path on this host, bounded sample
     cpu = None
     if not a.no_cpu_baseline:
-        o = _load("moe_oracle", os.path.join(REPO, "oracle", "moe_oracle.py"))
-        ncores = len(os.sched_getaffinity(0))
-        torch.set_num_threads(ncores)
-        log(f"[bench] CPU baseline on {ncores} threads (budget {a.cpu_budget_s}s)")
-        host = {kk: (v.detach().cpu() if isinstance(v, torch.Tensor) else v) for kk, v in base.items()}
-        out_cpu = torch.empty_like(host["output"])
-        cargs = wl.as_args({**host, "output": out_cpu})
-        times = []
-        tb = time.perf_counter()
-        while True:
-            c0 = time.perf_counter()
-            o.reference_cpu_forward(*cargs)
-            times.append(time.perf_counter() - c0)
-            if time.perf_counter() - tb + times[-1] > a.cpu_budget_s or len(times) >= 6:
-                break
-        timed = times[1:] if len(times) > 1 else times
-        cpu = dict(value=float(np.median(timed)) * 1e3, unit="ms/call", cores=torch.get_num_threads(),
-                   kind="port",
-                   sample=f"{len(timed)} timed full calls of {cfg.name} (T={T}) after "
-                          f"{len(times) - len(timed)} warmup; fp32 dequant of all 32 experts inside "
-                          f"each call as in moe.cu:164-176")
-
-    line = {
-        "metric": METRIC,
+        log(f"[bench] config {idx}: CPU baseline (budget {a.cpu_budget_s}s)")
+        cpu = cpu_baseline(o, wl, base, cfg, a.cpu_budget_s)
+    res = {
+        "config_index": idx,
+        "workload": cfg.name,
+        "T": T,
+        "local_expert_offset": cfg.local_expert_offset,
+        "hot_local_experts": list(cfg.hot_local_experts),
         "value": round(lat_us, 3),
         "unit": "us",
-        "n_gpus": 1,
-        "steps": a.steps,
-        "warmup": a.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": round(ms_per_step, 6),
-        "higher_is_better": False,
-        "scaling": "weak",
-        "vs_baseline": None,
         "dtype": {0: "fp8_e4m3 GEMM1 + fp16 GEMM2 (W2 widened exactly), fp32 accumulate",
                   1: "fp8_e4m3 GEMM1 + fp8 hi/lo GEMM2 (two FP8 MFMAs per product), fp32 accumulate",
                   2: "fp8_e4m3 GEMM1 (fp16 C, converted to fp8 hi/lo) + fp8 hi/lo GEMM2, "
                      "fp32 accumulate"}[k.workspace_layout(T).intermediate_format],
-        "data": "synthetic (seeded N(0,1) logits/hidden, N(0,0.02) weights, block-quantised)",
-        "config": {"workload": cfg.name, "T": T, "local_expert_offset": cfg.local_expert_offset,
-                   "routed_scaling_factor": cfg.routed_scaling_factor,
-                   "hot_local_experts": list(cfg.hot_local_experts), "rotate_copies": len(copies),
-                   "parallelism": "ep-rank (32 of 256 experts) on 1 GPU"},
         "latency_us": {"mean_wall": round(lat_us, 3), "median_event": float(np.median(ev_us)),
                        "p10_event": float(np.percentile(ev_us, 10)),
                        "p90_event": float(np.percentile(ev_us, 90)),
                        "graph_replay_wall": None if graph_us is None else round(graph_us, 3)},
         "eff_tflops": eff_tflops,
+        "fp8_peak_frac": eff_tflops / FP8_PEAK_TFLOPS,
         "work": {"N_a": n_a, "E_a": e_a, "tokens_touched": touched, "flops": work["flops"],
                  "bytes": work["bytes"]},
         "roofline_floor_us": floor_us,
@@ -302,7 +307,70 @@ def main() -> int:
         "profiled_calls": n_prof,
         "roofline": roof,
         "cpu_baseline": cpu,
-        "quantizer": quant,
+    }
+    if quant is not None:
+        res["quantizer"] = quant
+    del arglists, copies, base, ws
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return res
+
+
+def main() -> int:
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU only (one expert-parallel rank's share); "
+              f"--gpus {a.gpus} is not supported in this build.", file=sys.stderr)
+        return 2
+    if a.copy_calibration:
+        return copy_calibration(a.copy_calibration, a.steps)
+
+    import torch
+
+    k = _load("moe_mi355_kernel", os.path.join(PKG, "kernel.py"))
+    wl = _load("moe_mi355_workloads", os.path.join(PKG, "workloads.py"))
+    k._build_extension()  # fail loudly before any timing if the library is missing
+    o = None if a.no_cpu_baseline else _load("moe_oracle", os.path.join(REPO, "oracle", "moe_oracle.py"))
+    torch.cuda.set_device(torch.device("cuda:0"))
+
+    head_idx = HEADLINE_CONFIG if a.config is None else a.config
+    order = [a.config] if a.config is not None else list(range(len(wl.CONFIGS)))
+    results = {}
+    for idx in order:
+        w = a.warmup if idx == head_idx else max(a.warmup, MIN_CONFIG_WARMUP)
+        results[idx] = measure_config(idx, a, k, wl, o, a.steps, w,
+                                      quantizer=(idx == head_idx and not a.no_quantizer))
+    h = results[head_idx]
+    line = {
+        "metric": METRIC,
+        "value": h["value"],
+        "unit": "us",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": h["ms_per_step"],
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": h["dtype"],
+        "data": "synthetic (seeded N(0,1) logits/hidden, N(0,0.02) weights, block-quantised)",
+        "config": {"workload": h["workload"], "T": h["T"],
+                   "local_expert_offset": h["local_expert_offset"],
+                   "routed_scaling_factor": wl.CONFIGS[head_idx].routed_scaling_factor,
+                   "hot_local_experts": h["hot_local_experts"], "rotate_copies": a.rotate,
+                   "parallelism": "ep-rank (32 of 256 experts) on 1 GPU"},
+        "latency_us": h["latency_us"],
+        "eff_tflops": h["eff_tflops"],
+        "work": h["work"],
+        "roofline_floor_us": h["roofline_floor_us"],
+        "frac_of_floor": h["frac_of_floor"],
+        "hbm_frac_whole_call": h["hbm_frac_whole_call"],
+        "stages_us": h["stages_us"],
+        "profiled_calls": h["profiled_calls"],
+        "roofline": h["roofline"],
+        "cpu_baseline": h["cpu_baseline"],
+        "quantizer": h.get("quantizer"),
+        "per_config": [results[i] for i in order],
     }
     print(json.dumps(line))
     return 0
