@@ -120,7 +120,38 @@ int plan_for(int32_t T, int32_t flags, Plan* p) {
 
 thread_local char g_hip_error[256] = "";
 
-size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
+constexpr size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Byte offsets of the workspace regions of a call over T tokens (all 256-aligned).
+// constexpr, so that the library's own scratch array (moe_mi355_forward_noalloc) is
+// sized by the same arithmetic as a caller's workspace.
+constexpr moe_mi355_workspace_layout workspace_regions(int32_t T) {
+    moe_mi355_workspace_layout L{};
+    const size_t R = (size_t)T * moe::kTopK;
+    const int mt = (int)((R + kMinTileM - 1) / kMinTileM) + moe::kEL;   // dispatch_max_tiles
+    size_t off = 0;
+    auto take = [&off](size_t bytes) {
+        const size_t o = off;
+        off = align_up(off + bytes);
+        return o;
+    };
+    L.topk_ids = take(R * 4);
+    L.topk_weights = take(R * 4);
+    L.inverse_rows = take(R * 4);
+    L.meta = take(64 * 4);
+    L.tiles = take((size_t)mt * 2 * 16);   // room for a second, half-height tile list
+    L.sorted_tokens = take(R * 4);
+    L.sorted_weights = take(R * 4);
+    L.chunk_counts = take((size_t)((T + 255) / 256) * moe::kEL * 4);
+    L.row_scales = take(R * moe::kHB * 4);        // token scales in row order, [56, 8T]
+    L.intermediate = take(R * moe::kI * 6);     // hi/lo, fp16, bf16 copies
+    L.intermediate_scales = take(R * moe::kIB * 4);
+    L.expert_out = take(R * moe::kH * 2);
+    L.expert_out_wide = take(R * moe::kH * 4);
+    L.total = off;
+    L.max_tiles = mt;
+    return L;
+}
 
 // Workspace layout of a call over T tokens with the given flags (the regions do not
 // depend on the flags; tile_m and intermediate_format report the plan they choose).
@@ -129,30 +160,8 @@ int fill_layout(int32_t T, int32_t flags, moe_mi355_workspace_layout* L) {
     Plan plan;
     const int st = plan_for(T, flags, &plan);
     if (st != MOE_OK) return st;
-    const size_t R = (size_t)T * moe::kTopK;
-    const int mt = moe::dispatch_max_tiles(T, kMinTileM);
-    size_t off = 0;
-    auto take = [&](size_t bytes) {
-        const size_t o = off;
-        off = align_up(off + bytes);
-        return o;
-    };
-    L->topk_ids = take(R * 4);
-    L->topk_weights = take(R * 4);
-    L->inverse_rows = take(R * 4);
-    L->meta = take(64 * 4);
-    L->tiles = take((size_t)mt * 2 * 16);   // room for a second, half-height tile list
-    L->sorted_tokens = take(R * 4);
-    L->sorted_weights = take(R * 4);
-    L->chunk_counts = take((size_t)((T + 255) / 256) * moe::kEL * 4);
-    L->row_scales = take(R * moe::kHB * 4);        // token scales in row order, [56, 8T]
-    L->intermediate = take(R * moe::kI * 6);     // hi/lo, fp16, bf16 copies
-    L->intermediate_scales = take(R * moe::kIB * 4);
-    L->expert_out = take(R * moe::kH * 2);
-    L->expert_out_wide = take(R * moe::kH * 4);
-    L->total = off;
+    *L = workspace_regions(T);
     L->tile_m = plan.tm;
-    L->max_tiles = mt;
     L->intermediate_format = g1_hilo(plan.g1) ? 1 : plan.convert ? 2 : 0;
     return MOE_OK;
 }
