@@ -18,6 +18,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "moe_device.h"
 #include "moe_mi355.h"
 
@@ -192,6 +194,46 @@ void prof_record(int slot, int stage, hipStream_t s) {
     (void)hipEventRecord(g_prof.ev[slot * (MOE_MI355_NUM_STAGES + 1) + stage], s);
 }
 
+// ---- the library's own workspace (moe_mi355_forward_noalloc) ---------------------
+// A workspace for calls of up to MOE_MI355_NOALLOC_MAX_TOKENS tokens in a file-scope
+// device array: the code object's loader places one copy on every GPU the library
+// runs on, held until the process ends, so a call needs no allocation.  In host code
+// `scratch` names a host-side stand-in, never the device memory: its device address
+// on the current GPU comes from hipGetSymbolAddress, once per device (kept in
+// g_scratch_dev), and only that address reaches the kernels.  Every call on one GPU
+// shares the array: nothing in it needs to start at zero (the route kernel clears the
+// flag words, dispatch writes every offset, count and row the later kernels read),
+// and calls that overlap on one GPU (two streams) race on it.
+constexpr size_t kScratchBytes = workspace_regions(MOE_MI355_NOALLOC_MAX_TOKENS).total;
+static_assert(kScratchBytes <= (size_t)64 << 20, "keep the per-GPU scratch array modest");
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};
+
+}  // namespace
+
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+namespace {
+
+// Device address of `scratch` on the current GPU, looked up on the first call there.
+int scratch_on_current_device(void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_status(e);
+    if (dev < 0 || dev >= kMaxDevices) return MOE_ERR_DEVICE;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_dev[dev] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_status(e);
+        if (p == nullptr || ((uintptr_t)p & 255u)) return MOE_ERR_DEVICE;
+        g_scratch_dev[dev] = p;
+    }
+    *out = g_scratch_dev[dev];
+    return MOE_OK;
+}
+
 // The forward's launch sequence over a workspace of ws_bytes at ws (the caller's, or
 // for moe_mi355_forward_noalloc the library's own).  Returns MOE_OK or a status; a
 // status from a failed launch means the earlier launches of the call may have run.
@@ -295,6 +337,9 @@ const char* moe_mi355_strerror(int status) {
         case MOE_ERR_BAD_TILE: return "unsupported tile height";
         case MOE_ERR_BAD_FLAGS: return "unknown flag bits, or a forced kernel plan that cannot run";
         case MOE_ERR_BAD_PLAN: return "a kernel plan names a variant its launcher does not have";
+        case MOE_ERR_NOALLOC_SIZE:
+            return "moe_mi355_forward_noalloc: T beyond MOE_MI355_NOALLOC_MAX_TOKENS (use moe_mi355_forward with a workspace)";
+        case MOE_ERR_DEVICE: return "the stream is not on the current device, or no device scratch there";
         default: return "unknown status";
     }
 }
@@ -363,6 +408,26 @@ int moe_mi355_forward(const moe_mi355_args* a, void* stream) {
     if (!a) return MOE_ERR_NULL_POINTER;
     return forward_impl(*a, a->workspace, a->workspace_bytes, (hipStream_t)stream);
 }
+
+int moe_mi355_forward_noalloc(const moe_mi355_args* a, void* stream) {
+    if (!a) return MOE_ERR_NULL_POINTER;
+    if (a->T < 0) return MOE_ERR_BAD_SIZE;
+    if (a->T > MOE_MI355_NOALLOC_MAX_TOKENS) return MOE_ERR_NOALLOC_SIZE;
+    if (a->T == 0) return MOE_OK;
+    hipStream_t s = (hipStream_t)stream;
+    int cur = -1, sdev = -1;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return hip_status(e);
+    e = hipStreamGetDevice(s, &sdev);
+    if (e != hipSuccess) return hip_status(e);
+    if (sdev != cur) return MOE_ERR_DEVICE;
+    void* ws = nullptr;
+    const int st = scratch_on_current_device(&ws);
+    if (st != MOE_OK) return st;
+    return forward_impl(*a, ws, kScratchBytes, s);
+}
+
+size_t moe_mi355_noalloc_scratch_bytes(void) { return kScratchBytes; }
 
 int moe_mi355_profile_begin(int32_t max_calls) {
     moe_mi355_profile_end();

@@ -89,6 +89,8 @@ def _declare(L: ctypes.CDLL) -> ctypes.CDLL:
     sig = {
         "moe_mi355_workspace_bytes": (SZ, [I32]),
         "moe_mi355_forward": (ctypes.c_int, [ctypes.POINTER(MoeArgs), P]),
+        "moe_mi355_forward_noalloc": (ctypes.c_int, [ctypes.POINTER(MoeArgs), P]),
+        "moe_mi355_noalloc_scratch_bytes": (SZ, []),
         "moe_mi355_route": (ctypes.c_int, [P, P, I32, D, P, P, P]),
         "moe_mi355_dispatch": (ctypes.c_int, [P, P, I32, I64, I32, P, P, P, P, P, P, P, P]),
         "moe_mi355_max_tiles": (I32, [I32, I32]),

@@ -59,9 +59,13 @@ typedef enum moe_mi355_status {
     MOE_ERR_BAD_TILE = -6,         /* tile_m not supported */
     MOE_ERR_BAD_FLAGS = -7,        /* unknown flag bits, or a forced kernel plan that
                                       cannot run (MOE_MI355_FLAG_FORCE_PLAN) */
-    MOE_ERR_BAD_PLAN = -8          /* internal: a kernel plan names a variant that its
+    MOE_ERR_BAD_PLAN = -8,         /* internal: a kernel plan names a variant that its
                                       launcher does not have (earlier launches of the
                                       call may have run; the output is not valid) */
+    MOE_ERR_NOALLOC_SIZE = -9,     /* moe_mi355_forward_noalloc: T above
+                                      MOE_MI355_NOALLOC_MAX_TOKENS */
+    MOE_ERR_DEVICE = -10           /* the stream is not on the current device, or the
+                                      library's scratch has no address there */
 } moe_mi355_status;
 
 /* Arguments of one forward call.  Mirrors kernel.py:95-107 / main.cpp:66-77:
@@ -127,6 +131,24 @@ MOE_MI355_API size_t moe_mi355_workspace_bytes(int32_t T);
 /* The whole operator: routing -> dispatch -> GEMM1+SwiGLU -> GEMM2 -> combine.
  * Replaces main.cpp:66-266 run(). */
 MOE_MI355_API int moe_mi355_forward(const moe_mi355_args* args, void* stream);
+
+/* The forward without a workspace argument and without any allocation: no reference
+ * counterpart.  It is for callers that cannot allocate device memory -- code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.  The
+ * workspace is the library's own file-scope device array (about 57 MB,
+ * moe_mi355_noalloc_scratch_bytes()), one copy on each GPU the library runs on,
+ * held until the process ends; its address on a GPU is looked up on the first call
+ * there.  args->workspace and args->workspace_bytes are ignored.
+ *   - T must be at most MOE_MI355_NOALLOC_MAX_TOKENS (MOE_ERR_NOALLOC_SIZE beyond).
+ *   - `stream` must belong to the current device (MOE_ERR_DEVICE otherwise).
+ *   - Calls on one GPU share the array: calls that overlap in time on one GPU (on
+ *     different streams) race and must not be issued; calls on one stream are
+ *     ordered and safe.  Nothing in the array needs clearing between calls.
+ * Results are bit-identical to moe_mi355_forward's. */
+#define MOE_MI355_NOALLOC_MAX_TOKENS 128
+MOE_MI355_API int moe_mi355_forward_noalloc(const moe_mi355_args* args, void* stream);
+/* Size in bytes of that per-GPU array. */
+MOE_MI355_API size_t moe_mi355_noalloc_scratch_bytes(void);
 
 /* Routing only (kernel.cu:56-200): topk_ids int32 [T,8], topk_weights fp32 [T,8],
  * ids in selection order (score desc, index asc).  routing_bias is bf16 bits. */
