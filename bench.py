@@ -265,6 +265,7 @@ def measure_config(idx: int, a, k, wl, o, steps: int, warmup: int, quantizer: bo
         del xq
 
     # roofline of the dominant kernel (algorithmic bytes / flops, never padded rows)
+    lay = k.workspace_layout(T)
     dom = max(("gemm1", "gemm2", "combine", "route", "dispatch"), key=lambda s: stages_us[s])
     roof = roofline_of(dom, stages_us[dom], kernel_work(dom, T, n_a, e_a, touched), cfg.name)
 
@@ -291,7 +292,8 @@ def measure_config(idx: int, a, k, wl, o, steps: int, warmup: int, quantizer: bo
         "dtype": {0: "fp8_e4m3 GEMM1 + fp16 GEMM2 (W2 widened exactly), fp32 accumulate",
                   1: "fp8_e4m3 GEMM1 + fp8 hi/lo GEMM2 (two FP8 MFMAs per product), fp32 accumulate",
                   2: "fp8_e4m3 GEMM1 (fp16 C, converted to fp8 hi/lo) + fp8 hi/lo GEMM2, "
-                     "fp32 accumulate"}[k.workspace_layout(T).intermediate_format],
+                     "fp32 accumulate"}[lay.intermediate_format],
+        "plan": {"tile_m": lay.tile_m, "dispatch_in_gemm1": bool(lay.dispatch_in_gemm1)},
         "latency_us": {"mean_wall": round(lat_us, 3), "median_event": float(np.median(ev_us)),
                        "p10_event": float(np.percentile(ev_us, 10)),
                        "p90_event": float(np.percentile(ev_us, 90)),

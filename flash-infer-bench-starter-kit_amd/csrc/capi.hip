@@ -31,6 +31,10 @@ int dispatch_max_tiles(int T, int tm);
 bool launch_gemm1(int, const uint8_t*, const TokenScales&, int, const uint8_t*, const float*,
                   const int4*, const int*, const int*, int, const int*, const Intermediate&,
                   hipStream_t);
+bool launch_gemm1_dispatch(const int*, const float*, int, int, const uint8_t*, const float*,
+                           const uint8_t*, const float*, int*, int4*, int*, float*, int*,
+                           const Intermediate&, hipStream_t);
+constexpr int kDispatchInGemm1MaxT = 64;
 bool launch_gemm2(int, const Intermediate&, const uint8_t*, const float*, const int4*, const int*,
                   const int*, int, const ExpertRows&, hipStream_t);
 void launch_combine(const ExpertRows&, const int*, const float*, const int*, int, uint16_t*, hipStream_t);
@@ -67,25 +71,34 @@ struct Plan {
     int g1, g2;
     bool convert;  // fp16 C converted to the hi/lo form between the GEMMs
     bool by_row;   // GEMM1 reads the token scales gathered into row order
+    bool dispatch_in_gemm1;   // GEMM1 variant 5 computes the dispatch itself (no launch)
 };
 
-int g1_tile_m(int v) { return v == 1 ? 16 : v == 2 ? 32 : v == 3 ? 128 : 256; }
-bool g1_hilo(int v) { return v >= 3; }        // GEMM1 writes the hi/lo form
+int g1_tile_m(int v) { return v == 1 || v == 5 ? 16 : v == 2 ? 32 : v == 3 ? 128 : 256; }
+bool g1_hilo(int v) { return v == 3 || v == 4; }   // GEMM1 writes the hi/lo form
 bool g2_hilo(int v) { return v >= 4; }        // GEMM2 reads the hi/lo form
 
-// The plan of a GEMM1 / GEMM2 pair, false when they cannot run together.
-bool make_plan(int g1, int g2, Plan* p) {
+// The plan of a GEMM1 / GEMM2 pair, false when they cannot run together.  GEMM1
+// variant 5 is variant 1 with the dispatch folded in (T <= 64): every workgroup of a
+// persistent grid computes the call's dispatch from the routing ids, and the separate
+// dispatch launch goes away.
+bool make_plan(int g1, int g2, int32_t T, Plan* p) {
+    if (g1 == 5) {
+        if (g2 > 2 || T > moe::kDispatchInGemm1MaxT) return false;
+        *p = {16, 0, 5, g2, false, false, true};
+        return true;
+    }
     if (g1 < 1 || g1 > 4 || g2 < 1 || g2 > 5) return false;
     const int tm = g1_tile_m(g1);
     if (g1_hilo(g1) && !g2_hilo(g2)) return false;      // the fp16 GEMM2s need fp16 C
     if (g2 == 5) {                                       // the second list, 128-row tiles
         if (tm != 16 && tm != 32 && tm != 256) return false;
-        *p = {tm, 128, g1, g2, !g1_hilo(g1), false};
+        *p = {tm, 128, g1, g2, !g1_hilo(g1), false, false};
         return true;
     }
     const int tm_g2 = g2 <= 2 ? 16 : g2 == 3 ? 32 : 128;
     if (tm_g2 != tm) return false;
-    *p = {tm, 0, g1, g2, g1_hilo(g1) != g2_hilo(g2), false};
+    *p = {tm, 0, g1, g2, g1_hilo(g1) != g2_hilo(g2), false, false};
     return true;
 }
 
@@ -101,8 +114,12 @@ constexpr int32_t kKnownFlags = MOE_MI355_FLAG_PROFILE | MOE_MI355_FLAG_FORCE_PL
 // Nothing outside the call's arguments (no environment) changes it.
 int plan_for(int32_t T, int32_t flags, Plan* p) {
     if (flags & ~kKnownFlags) return MOE_ERR_BAD_FLAGS;
+    const bool on = flags & MOE_MI355_FLAG_ROW_SCALES_ON, off = flags & MOE_MI355_FLAG_ROW_SCALES_OFF;
     int g1, g2;
-    if (T <= 112) g1 = 1, g2 = 1;
+    // GEMM1 with the dispatch folded in reads the token scales by token: asking for the
+    // gathered ones selects the separate dispatch there
+    if (T <= moe::kDispatchInGemm1MaxT && !on) g1 = 5, g2 = 1;
+    else if (T <= 112) g1 = 1, g2 = 1;
     else if (T <= 192) g1 = 1, g2 = 2;
     else if (T <= 704) g1 = 2, g2 = 3;
     else if (T <= 1536) g1 = 2, g2 = 5;
@@ -113,9 +130,8 @@ int plan_for(int32_t T, int32_t flags, Plan* p) {
     } else if (flags & (0xff << 8)) {
         return MOE_ERR_BAD_FLAGS;            // variant bits without the force bit
     }
-    if (!make_plan(g1, g2, p)) return MOE_ERR_BAD_FLAGS;
-    const bool on = flags & MOE_MI355_FLAG_ROW_SCALES_ON, off = flags & MOE_MI355_FLAG_ROW_SCALES_OFF;
-    if (on && off) return MOE_ERR_BAD_FLAGS;
+    if (!make_plan(g1, g2, T, p)) return MOE_ERR_BAD_FLAGS;
+    if (on && (off || p->dispatch_in_gemm1)) return MOE_ERR_BAD_FLAGS;
     p->by_row = on ? true : off ? false : T >= kRowScalesMinT;
     return MOE_OK;
 }
@@ -165,6 +181,7 @@ int fill_layout(int32_t T, int32_t flags, moe_mi355_workspace_layout* L) {
     *L = workspace_regions(T);
     L->tile_m = plan.tm;
     L->intermediate_format = g1_hilo(plan.g1) ? 1 : plan.convert ? 2 : 0;
+    L->dispatch_in_gemm1 = plan.dispatch_in_gemm1 ? 1 : 0;
     return MOE_OK;
 }
 
@@ -288,7 +305,9 @@ int forward_impl(const moe_mi355_args& a, void* workspace, size_t ws_bytes, hipS
     const bool half = plan.tm2 > 0;   // GEMM2 walks the second (128-row) tile list
     int4* tiles2 = tiles + max_tiles;
     int* num_tiles2 = meta + moe::kEL + 2;
-    bool ok = moe::launch_dispatch(ids, wts, T, clamp_offset(a.local_expert_offset), plan.tm,
+    // GEMM1 variant 5 computes the dispatch itself (timed as the GEMM1 stage)
+    bool ok = plan.dispatch_in_gemm1 ||
+              moe::launch_dispatch(ids, wts, T, clamp_offset(a.local_expert_offset), plan.tm,
                                    plan.tm2, meta, num_tiles, tiles, stok, sw, inv, chunk_cnt, s,
                                    half ? num_tiles2 : nullptr, half ? tiles2 : nullptr);
     // GEMM1 reads the token scales gathered into row order (counted in the dispatch stage)
@@ -299,9 +318,15 @@ int forward_impl(const moe_mi355_args& a, void* workspace, size_t ws_bytes, hipS
     const moe::TokenScales sa = plan.by_row ? moe::TokenScales{row_scales, T * moe::kTopK, 1}
                                             : moe::TokenScales{a.hidden_states_scale, T, 0};
     if (prof) prof_record(slot, 2, s);
-    ok = ok && moe::launch_gemm1(plan.g1, a.hidden_states, sa, T, a.gemm1_weights,
-                                 a.gemm1_weights_scale, tiles, num_tiles, meta, max_tiles, stok,
-                                 inter, s);
+    if (plan.dispatch_in_gemm1)
+        ok = ok && moe::launch_gemm1_dispatch(ids, wts, T, clamp_offset(a.local_expert_offset),
+                                              a.hidden_states, a.hidden_states_scale,
+                                              a.gemm1_weights, a.gemm1_weights_scale, meta, tiles,
+                                              stok, sw, inv, inter, s);
+    else
+        ok = ok && moe::launch_gemm1(plan.g1, a.hidden_states, sa, T, a.gemm1_weights,
+                                     a.gemm1_weights_scale, tiles, num_tiles, meta, max_tiles,
+                                     stok, inter, s);
     if (prof) prof_record(slot, 3, s);
     if (ok && plan.convert) moe::launch_c_f16_to_hilo(inter, meta, s);   // in the GEMM2 stage
     if (ok && half)

@@ -18,136 +18,9 @@
 // writes per-chunk (256 tokens) expert counts and a place kernel (one workgroup per
 // chunk) turns them into each chunk's base and writes the permutation.
 
-#include "moe_device.h"
+#include "dispatch_rows.h"
 
 namespace moe {
-
-// inclusive prefix sum over lanes 0..31 of a wave (lanes >= 32 unused; every lane of
-// the wave must be active).  DPP: shifts by 1, 2, 4, 8 inside each row of 16 lanes (a
-// source outside the row reads 0), then lane 15's row total is added to lanes 16..31.
-__device__ __forceinline__ int scan32(int v, int lane) {
-    (void)lane;
-    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);   // row_shr:1
-    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);   // row_shr:2
-    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);   // row_shr:4
-    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);   // row_shr:8
-    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);   // row_bcast:15
-    return v;
-}
-
-// Per-thread view of one token's 8 assignments: local expert (or -1), weight, and a
-// 32-bit mask of its local experts.
-struct TokenRoutes {
-    int lek[kTopK];
-    float wk[kTopK];
-    uint32_t mask;
-};
-
-__device__ __forceinline__ TokenRoutes load_routes(const int* __restrict__ topk_ids,
-                                                   const float* __restrict__ topk_w, int t, int T,
-                                                   int offset) {
-    TokenRoutes r;
-    r.mask = 0;
-    if (t < T) {
-        const int4* ip = reinterpret_cast<const int4*>(topk_ids + (size_t)t * kTopK);
-        const float4* wp = reinterpret_cast<const float4*>(topk_w + (size_t)t * kTopK);
-        const int4 i0 = ip[0], i1 = ip[1];
-        const float4 w0 = wp[0], w1 = wp[1];
-        const int ids[kTopK] = {i0.x, i0.y, i0.z, i0.w, i1.x, i1.y, i1.z, i1.w};
-        const float ws[kTopK] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-#pragma unroll
-        for (int k = 0; k < kTopK; ++k) {
-            const int le = ids[k] - offset;
-            const bool loc = (unsigned)le < (unsigned)kEL;
-            r.lek[k] = loc ? le : -1;
-            r.wk[k] = ws[k];
-            if (loc) r.mask |= 1u << le;
-        }
-    } else {
-#pragma unroll
-        for (int k = 0; k < kTopK; ++k) { r.lek[k] = -1; r.wk[k] = 0.f; }
-    }
-    return r;
-}
-
-// For each expert e: the wave's count into wcnt[wave][e]; returns in rank[k] this
-// lane's rank among the wave's lanes holding expert lek[k].  One ballot per expert;
-// lane e keeps expert e's ballot and writes it to the wave's table bal[kEL] in LDS,
-// from which every lane reads the ballots of its own experts.  The table is written
-// and read by the same wave only (LDS operations of a wave complete in order).
-__device__ __forceinline__ void wave_ranks(const TokenRoutes& r, int wave, int lane,
-                                           int (*wcnt)[kEL], uint64_t* bal, int* rank) {
-    uint64_t mine = 0;
-#pragma unroll
-    for (int e = 0; e < kEL; ++e) {
-        const uint64_t b = __ballot((r.mask >> e) & 1u);
-        mine = (lane == e) ? b : mine;
-    }
-    if (lane < kEL) {
-        bal[lane] = mine;
-        wcnt[wave][lane] = __popcll(mine);
-    }
-    __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (int k = 0; k < kTopK; ++k) {
-        rank[k] = 0;
-        if (r.lek[k] >= 0) {
-            const uint64_t b = bal[r.lek[k]];
-            rank[k] = __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32),
-                                                __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
-        }
-    }
-}
-
-__device__ __forceinline__ void place(const TokenRoutes& r, const int* rank, int t, int T,
-                                      const int* base, int* __restrict__ sorted_tok,
-                                      float* __restrict__ sorted_w, int* __restrict__ inv) {
-    if (t >= T) return;
-#pragma unroll
-    for (int k = 0; k < kTopK; ++k) {
-        int row = -1;
-        if (r.lek[k] >= 0) {
-            row = base[r.lek[k]] + rank[k];
-            sorted_tok[row] = t;
-            sorted_w[row] = r.wk[k];
-        }
-        inv[(size_t)t * kTopK + k] = row;
-    }
-}
-
-// expert offsets, tile list and tile count from the per-expert totals (wave 0).
-// With TM2 > 0 (and tiles2 set), also a second list of tiles of TM2 rows over the same
-// rows (num_tiles2 = its count), for a GEMM2 that walks other tiles than the GEMM1.
-template <int TM, int TM2>
-__device__ __forceinline__ void write_offsets_and_tiles(int c, int lane, int* off_lds,
-                                                        int* __restrict__ exp_off,
-                                                        int* __restrict__ num_tiles,
-                                                        int4* __restrict__ tiles,
-                                                        int* __restrict__ num_tiles2,
-                                                        int4* __restrict__ tiles2) {
-    constexpr int TM2r = TM2 > 0 ? TM2 : TM;
-    const int nt = (c + TM - 1) / TM;
-    const int nt2 = (c + TM2r - 1) / TM2r;
-    const int ci = scan32(c, lane);
-    const int ti = scan32(nt, lane);
-    const int ti2 = scan32(nt2, lane);
-    if (lane < kEL) {
-        const int o = ci - c, to = ti - nt;
-        off_lds[lane] = o;
-        exp_off[lane] = o;
-        for (int j = 0; j < nt; ++j) tiles[to + j] = make_int4(lane, o + j * TM, min(TM, c - j * TM), 0);
-        if (TM2 > 0 && tiles2) {
-            const int to2 = ti2 - nt2;
-            for (int j = 0; j < nt2; ++j)
-                tiles2[to2 + j] = make_int4(lane, o + j * TM2r, min(TM2r, c - j * TM2r), 0);
-        }
-    }
-    if (lane == kEL - 1) {
-        exp_off[kEL] = ci;
-        *num_tiles = ti;
-        if (TM2 > 0 && tiles2) *num_tiles2 = ti2;
-    }
-}
 
 // T <= 1024: one workgroup of NW waves (64 NW >= T), one token per thread, one pass
 // over the routes.

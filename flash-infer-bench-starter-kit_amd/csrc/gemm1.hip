@@ -20,260 +20,86 @@
 // operand B (16 tokens); lane l holds row/token l%16 and K bytes 32*(l/16)..+31 of
 // the block for both operands, and receives D[n = 4*(l/16)+v][token = l%16].
 
-#include "moe_device.h"
+#include "dispatch_rows.h"
+#include "gemm1_stream.h"
+
+#include <mutex>
 
 namespace moe {
 
-__device__ __forceinline__ v8i load_v8i(const uint8_t* p) {
-    const uint4* q = reinterpret_cast<const uint4*>(p);
-    const uint4 a = q[0];
-    const uint4 b = q[1];
-    v8i r;
-    r[0] = (int)a.x; r[1] = (int)a.y; r[2] = (int)a.z; r[3] = (int)a.w;
-    r[4] = (int)b.x; r[5] = (int)b.y; r[6] = (int)b.z; r[7] = (int)b.w;
-    return r;
-}
-
-__device__ __forceinline__ v4f mfma_fp8(const v8i& a, const v8i& b, const v4f& c) {
-    // scale operands 0 -> plain (unscaled) e4m3 x e4m3 MFMA
-    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
-}
-
-__device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
-
-// Four SwiGLU values of row `row`, columns n0..n0+3 in fp16 (round to nearest even).
-// When one of them lies beyond the fp16 range, the four also go to the bf16 region and
-// the flag word is raised; GEMM2 then takes the bf16 value wherever the fp16 one is
-// infinite.  (Writing the bf16 copy on every call costs ~10 us at T = 1024.)
-__device__ __forceinline__ void store_swiglu4(const Intermediate& C, int* __restrict__ c_wide, int row,
-                                              int n0, const v4f& g, const v4f& u) {
-    float c[4];
-    uint32_t h[4];
-    bool wide = false;
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-        c[v] = silu_f32(u[v]) * g[v];
-        h[v] = __builtin_bit_cast(uint16_t, (_Float16)c[v]);
-        wide = wide || fabsf(c[v]) > kF16Max;
-    }
-    const size_t off = (size_t)row * kI + n0;
-    *reinterpret_cast<uint2*>(C.f16() + off) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
-    if (wide) {
-        uint32_t b[4];
-#pragma unroll
-        for (int v = 0; v < 4; ++v) b[v] = f32_to_bf16_bits(c[v]);
-        *reinterpret_cast<uint2*>(C.bf16() + off) = make_uint2(b[0] | (b[1] << 16), b[2] | (b[3] << 16));
-        *c_wide = 1;
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Register-staged weight streaming (decode and small prefill).  A work item is one row
-// tile x one group of 16 SwiGLU columns (16 gate + 16 up weight rows); the 4 waves of
-// a workgroup take 14 of its 56 K blocks each and reduce through LDS in a fixed order.
-// Weight bytes come into registers with full-line loads (global_load_dwordx4, lane l
-// reads row 8i + l/8, 16-byte chunk l%8 of the K block: 8 rows x 128 B per
-// instruction) through a ring of D K blocks held in VGPRs, and each K block is turned
-// into the MFMA layout through a 4 KB per-wave LDS slot (ds_write_b128 at the
-// swizzled position, then ds_read_b128 by the MFMA lanes).  Keeping the in-flight
-// bytes in VGPRs instead of an LDS ring lets more waves run per CU, so more bytes are
-// in flight per CU (a streaming probe of this access pattern: 7.1 TB/s against
-// 6.3 TB/s for LDS-landed DMA).
-// A tile holds CB blocks of 16 token rows: every weight fragment feeds 2 CB MFMAs, so
-// an expert with up to 16 CB routed rows streams its weights once.  An item covers
-// NGRP groups of 16 SwiGLU columns, so each token fragment a wave loads feeds NGRP
-// weight groups: token re-reads, which hit L2 but still take the CU's outstanding
-// request slots, fall from half of the requests (NGRP = 1, CB = 2) to a third.
-// TL: token rows take the weights' path too (full-line loads into the ring, then the
-// LDS slot), instead of each lane loading its 32 MFMA-layout bytes, which covers half
-// of 16 lines per instruction.  That pays on 32-row tiles (T = 193 .. 1536), where the
-// kernel is bound by the CU's requests, and not on 16-row tiles.
-// ---------------------------------------------------------------------------
+// The streaming GEMM1 over the row tiles of a dispatch (see gemm1_rstream_item).
 template <int D, int CB, int NGRP, bool TL>
 __global__ __launch_bounds__(256) void gemm1_rstream_kernel(
     const uint8_t* __restrict__ hidden, TokenScales sa, int T,
     const uint8_t* __restrict__ w1, const float* __restrict__ s1,
     const int4* __restrict__ tiles, const int* __restrict__ num_tiles,
     const int* __restrict__ sorted_tok, Intermediate C, int* __restrict__ c_wide) {
-    constexpr int KSPLIT = 4;
-    constexpr int KB = kHB / KSPLIT;                  // 14 K blocks per wave
-    constexpr int kItems = kI / (16 * NGRP);
-    constexpr int NW = 4 * NGRP;                      // weight loads per K block (8 rows each)
-    constexpr int kVmPerKb = NW + 3 * CB;             // per row block 2 token loads + 1 scale
-    static_assert(D >= 2 && D <= 8 && (D - 1) * kVmPerKb < 64, "ring depth");
-    static_assert(NGRP == 1 || NGRP == 2, "column groups per item");
-    constexpr int kTok = 32 * NGRP * kBlk;           // token rows after the weight rows
-    __shared__ __attribute__((aligned(1024))) uint8_t slot_lds[4][kTok + (TL ? 16 * CB * kBlk : 0)];
+    using S = Gemm1Stream<CB, NGRP, TL>;
+    __shared__ __attribute__((aligned(1024))) uint8_t slot_lds[4][S::kSlot];
     __shared__ v4f red[4][2][NGRP * CB][64];
-
+    const int nwork = (*num_tiles) * S::kItems;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    const int r16 = lane & 15, kq = lane >> 4;
-    const int ks = wave;
-    const int nwork = (*num_tiles) * kItems;
-    const v4f zero = {0.f, 0.f, 0.f, 0.f};
-    uint8_t* slot = &slot_lds[wave][0];
-    const int drow = lane >> 3, dchunk = lane & 7;
-    const int swz = swz128(r16);
-    const int rd_g0 = r16 * kBlk + (((2 * kq) ^ swz) << 4);
-    const int rd_g1 = r16 * kBlk + (((2 * kq + 1) ^ swz) << 4);
-    int wr[NW];                                        // LDS position of this lane's chunk
-#pragma unroll
-    for (int i = 0; i < NW; ++i) {
-        const int r = 8 * i + drow;
-        wr[i] = r * kBlk + ((dchunk ^ swz128(r)) << 4);
-    }
-    int twr[2 * CB];                                   // the same for the token rows
-#pragma unroll
-    for (int i = 0; i < 2 * CB; ++i) {
-        const int r = 8 * i + drow;
-        twr[i] = kTok + r * kBlk + ((dchunk ^ swz128(r)) << 4);
-    }
-    const int kb0 = ks * KB;
-
     for (int work = blockIdx.x; work < nwork; work += gridDim.x) {
-        const int4 tile = tiles[work / kItems];
-        const int ng = (work % kItems) * NGRP;         // first 16-column group
-        const int le = tile.x, row0 = tile.y, nrows = tile.z;
-        // TL: token rows also come as full 128-byte lines (lane l: row 8 i + l / 8, chunk
-        // l % 8; offsets fit 32 bits, T * 7168 < 2^32) and reach the MFMA layout through
-        // the slot.  Otherwise each lane loads its 32 MFMA-layout bytes of row r16.
-        uint32_t toff[2 * CB];
-#pragma unroll
-        for (int i = 0; i < 2 * CB; ++i) {
-            if (TL) toff[i] = (uint32_t)sorted_tok[row0 + min(8 * i + drow, nrows - 1)] * kH + dchunk * 16;
-            else if (i < CB) toff[i] = (uint32_t)sorted_tok[row0 + min(16 * i + r16, nrows - 1)] * kH + kq * 32;
-        }
-        const float* sp[CB];
-#pragma unroll
-        for (int c = 0; c < CB; ++c) {
-            const int row = row0 + min(16 * c + r16, nrows - 1);
-            sp[c] = sa.p + (sa.by_row ? row : sorted_tok[row]);
-        }
-        // slot rows 32 gi + 0..15: gate rows of group ng + gi, 32 gi + 16..31: its up rows
-        const uint8_t* wsrc[NW];
-#pragma unroll
-        for (int i = 0; i < NW; ++i) {
-            const int r = 8 * i + drow;
-            const int gi = r >> 5, rr = r & 31;
-            const int n = (rr < 16) ? (ng + gi) * 16 + rr : kI + (ng + gi) * 16 + (rr - 16);
-            wsrc[i] = w1 + (size_t)(le * kN1 + n) * kH + dchunk * 16;
-        }
-        // the NGRP groups lie in one 128-column scale block (16 NGRP divides 128)
-        const float* sg = s1 + (size_t)(le * kN1B + (ng >> 3)) * kHB;
-        const float* su = sg + (size_t)kIB * kHB;
+        const int4 tile = tiles[work / S::kItems];
+        gemm1_rstream_item<D, CB, NGRP, TL>(hidden, sa, w1, s1, tile.x, tile.y, tile.z,
+                                            (work % S::kItems) * NGRP, sorted_tok, C, c_wide,
+                                            slot_lds, red, wave);
+    }
+}
 
-        v4u bw[D][NW];
-        v4u bt[D][2 * CB];
-        float bs[D][CB];
-        auto issue = [&](int k) {
-            const int kb = kb0 + k;
-#pragma unroll
-            for (int i = 0; i < NW; ++i) bw[k % D][i] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(wsrc[i] + kb * kBlk));
-#pragma unroll
-            for (int i = 0; i < 2 * CB; ++i) {
-                const uint32_t o = TL ? toff[i] : toff[i >> 1] + 16 * (i & 1);
-                bt[k % D][i] = *reinterpret_cast<const v4u*>(hidden + o + kb * kBlk);
-            }
-#pragma unroll
-            for (int c = 0; c < CB; ++c) bs[k % D][c] = sp[c][(size_t)kb * sa.stride];
-        };
-#pragma unroll
-        for (int k = 0; k < D - 1; ++k) {
-            issue(k);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        v4f ag[NGRP][CB], au[NGRP][CB];
-#pragma unroll
-        for (int gi = 0; gi < NGRP; ++gi)
-#pragma unroll
-            for (int c = 0; c < CB; ++c) ag[gi][c] = au[gi][c] = zero;
-#pragma unroll
-        for (int k = 0; k < KB; ++k) {
-            if (k + D - 1 < KB) issue(k + D - 1);
-            __builtin_amdgcn_sched_barrier(0);
-            const int younger = (KB - 1 - k) < (D - 1) ? (KB - 1 - k) : (D - 1);
-            switch (younger) {   // resolved at compile time after unrolling
-                case 0: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
-                case 1: __builtin_amdgcn_s_waitcnt(vmcnt_imm(1 * kVmPerKb)); break;
-                case 2: __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kVmPerKb)); break;
-                case 3: __builtin_amdgcn_s_waitcnt(vmcnt_imm(3 * kVmPerKb)); break;
-                case 4: __builtin_amdgcn_s_waitcnt(vmcnt_imm(4 * kVmPerKb)); break;
-                case 5: __builtin_amdgcn_s_waitcnt(vmcnt_imm(5 * kVmPerKb)); break;
-                case 6: __builtin_amdgcn_s_waitcnt(vmcnt_imm(6 * kVmPerKb)); break;
-                default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(7 * kVmPerKb)); break;
-            }
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int i = 0; i < NW; ++i) *reinterpret_cast<v4u*>(slot + wr[i]) = bw[k % D][i];
-            v8i ba[CB];
-            if constexpr (TL) {
-#pragma unroll
-                for (int i = 0; i < 2 * CB; ++i) *reinterpret_cast<v4u*>(slot + twr[i]) = bt[k % D][i];
-#pragma unroll
-                for (int c = 0; c < CB; ++c) {
-                    const uint8_t* ts = slot + kTok + 16 * c * kBlk;
-                    const v4u a0 = *reinterpret_cast<const v4u*>(ts + rd_g0);
-                    const v4u a1 = *reinterpret_cast<const v4u*>(ts + rd_g1);
-                    ba[c] = v8i{(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3], (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
-                }
-            } else {
-#pragma unroll
-                for (int c = 0; c < CB; ++c) {
-                    const v4u a0 = bt[k % D][2 * c], a1 = bt[k % D][2 * c + 1];
-                    ba[c] = v8i{(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3], (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
-                }
-            }
-            const int kb = kb0 + k;
-            const float wg = sg[kb], wu = su[kb];
-#pragma unroll
-            for (int gi = 0; gi < NGRP; ++gi) {
-                const uint8_t* gs = slot + gi * 32 * kBlk;
-                const v4u g0 = *reinterpret_cast<const v4u*>(gs + rd_g0);
-                const v4u g1 = *reinterpret_cast<const v4u*>(gs + rd_g1);
-                const v4u u0 = *reinterpret_cast<const v4u*>(gs + 16 * kBlk + rd_g0);
-                const v4u u1 = *reinterpret_cast<const v4u*>(gs + 16 * kBlk + rd_g1);
-                const v8i bg = {(int)g0[0], (int)g0[1], (int)g0[2], (int)g0[3], (int)g1[0], (int)g1[1], (int)g1[2], (int)g1[3]};
-                const v8i bu = {(int)u0[0], (int)u0[1], (int)u0[2], (int)u0[3], (int)u1[0], (int)u1[1], (int)u1[2], (int)u1[3]};
-#pragma unroll
-                for (int c = 0; c < CB; ++c) {
-                    const float fg = bs[k % D][c] * wg, fu = bs[k % D][c] * wu;
-                    const v4f tg = mfma_fp8(bg, ba[c], zero);
-                    const v4f tu = mfma_fp8(bu, ba[c], zero);
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        ag[gi][c][v] = __builtin_fmaf(tg[v], fg, ag[gi][c][v]);
-                        au[gi][c][v] = __builtin_fmaf(tu[v], fu, au[gi][c][v]);
-                    }
-                }
-            }
-            __builtin_amdgcn_sched_barrier(0);
-        }
+// The streaming GEMM1 of variant 1 with the dispatch folded in, for T <= 64: every
+// workgroup of a persistent grid computes the call's dispatch from the routing ids
+// (dispatch_wave: one wave, a token per lane, into LDS) and takes its work items from
+// that tile list; workgroup 0 also writes the dispatch (offsets, tile count and list,
+// permutation, row weights, inverse map) to the workspace, where the GEMM2 and combine
+// kernels after it read it.  The dispatch launch goes away; the dispatch itself costs a
+// workgroup about what the separate kernel's two dependent loads (tile list, then
+// permutation) cost before its first weight load.
+constexpr int kDispatchInGemm1MaxT = 64;
+constexpr int kDG1MaxTiles = kDispatchInGemm1MaxT * kTopK / 16 + kEL;   // 64
 
-#pragma unroll
-        for (int gi = 0; gi < NGRP; ++gi)
-#pragma unroll
-            for (int c = 0; c < CB; ++c) {
-                red[wave][0][gi * CB + c][lane] = ag[gi][c];
-                red[wave][1][gi * CB + c][lane] = au[gi][c];
-            }
-        __syncthreads();
-        if (wave == 0) {
-#pragma unroll
-            for (int gi = 0; gi < NGRP; ++gi)
-#pragma unroll
-                for (int c = 0; c < CB; ++c) {
-                    v4f g = red[0][0][gi * CB + c][lane], u = red[0][1][gi * CB + c][lane];
-#pragma unroll
-                    for (int q = 1; q < KSPLIT; ++q) {
-                        g += red[q][0][gi * CB + c][lane];
-                        u += red[q][1][gi * CB + c][lane];
-                    }
-                    if (16 * c + r16 < nrows)
-                        store_swiglu4(C, c_wide, row0 + 16 * c + r16, (ng + gi) * 16 + kq * 4, g, u);
-                }
+__global__ __launch_bounds__(256) void gemm1_rstream_dispatch_kernel(
+    const int* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int offset,
+    const uint8_t* __restrict__ hidden, const float* __restrict__ hs_scale,
+    const uint8_t* __restrict__ w1, const float* __restrict__ s1, int* __restrict__ meta,
+    int4* __restrict__ tiles, int* __restrict__ sorted_tok, float* __restrict__ sorted_w,
+    int* __restrict__ inv, Intermediate C) {
+    using S = Gemm1Stream<1, 1, false>;
+    constexpr int R = kDispatchInGemm1MaxT * kTopK;
+    __shared__ __attribute__((aligned(1024))) uint8_t slot_lds[4][S::kSlot];
+    __shared__ v4f red[4][2][1][64];
+    __shared__ int s_exp_off[kEL + 1];
+    __shared__ int s_num_tiles;
+    __shared__ int4 s_tiles[kDG1MaxTiles];
+    __shared__ int s_stok[R];
+    __shared__ float s_sw[R];
+    __shared__ int s_inv[R];
+    __shared__ DispatchWaveLds s_dw;
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    if (wave == 0)
+        dispatch_wave<16>(topk_ids, topk_w, T, offset, tid & 63, s_dw, s_exp_off, &s_num_tiles,
+                          s_tiles, s_stok, s_sw, s_inv);
+    __syncthreads();
+    const int ntiles = s_num_tiles;
+    if (blockIdx.x == 0) {
+        const int na = s_exp_off[kEL];
+        for (int i = tid; i <= kEL; i += 256) meta[i] = s_exp_off[i];
+        if (tid == 0) meta[kEL + 1] = ntiles;
+        for (int i = tid; i < ntiles; i += 256) tiles[i] = s_tiles[i];
+        for (int i = tid; i < na; i += 256) {
+            sorted_tok[i] = s_stok[i];
+            sorted_w[i] = s_sw[i];
         }
-        __syncthreads();
+        for (int i = tid; i < T * kTopK; i += 256) inv[i] = s_inv[i];
+    }
+    const TokenScales sa{hs_scale, T, 0};
+    const int nwork = ntiles * S::kItems;
+    for (int work = blockIdx.x; work < nwork; work += gridDim.x) {
+        const int4 tile = s_tiles[work / S::kItems];
+        gemm1_rstream_item<4, 1, 1, false>(hidden, sa, w1, s1, tile.x, tile.y, tile.z,
+                                           work % S::kItems, s_stok, C, meta + kCWideFlag,
+                                           slot_lds, red, wave);
     }
 }
 
@@ -652,6 +478,43 @@ __global__ __launch_bounds__(512, 1) void gemm1_prefill8_kernel(
 }
 
 static int grid_for(long long work) { return (int)(work < 4096 ? work : 4096); }
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_dg1_mu;
+int g_dg1_grid[kMaxDevices] = {};
+}  // namespace
+
+// GEMM1 with the dispatch folded in: a persistent grid of as many workgroups as the
+// device holds at once (occupancy x CUs, looked up once per device), capped by the most
+// work items T tokens can have.
+bool launch_gemm1_dispatch(const int* topk_ids, const float* topk_w, int T, int offset,
+                           const uint8_t* hidden, const float* hs_scale, const uint8_t* w1,
+                           const float* s1, int* meta, int4* tiles, int* sorted_tok,
+                           float* sorted_w, int* inv, const Intermediate& C, hipStream_t stream) {
+    if (T <= 0 || T > kDispatchInGemm1MaxT) return false;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
+    int resident = 0;
+    {
+        std::lock_guard<std::mutex> lock(g_dg1_mu);
+        if (g_dg1_grid[dev] == 0) {
+            int per_cu = 0, cus = 0;
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemm1_rstream_dispatch_kernel, 256, 0) != hipSuccess ||
+                hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+                per_cu * cus <= 0)
+                return false;
+            g_dg1_grid[dev] = per_cu * cus;
+        }
+        resident = g_dg1_grid[dev];
+    }
+    const long long items = (long long)(((long long)T * kTopK + 15) / 16 + kEL) * Gemm1Stream<1, 1, false>::kItems;
+    const int grid = (int)(items < resident ? items : resident);
+    hipLaunchKernelGGL(gemm1_rstream_dispatch_kernel, dim3(grid), dim3(256), 0, stream, topk_ids,
+                       topk_w, T, offset, hidden, hs_scale, w1, s1, meta, tiles, sorted_tok, sorted_w,
+                       inv, C);
+    return true;
+}
 
 // Variants (the tile height of the dispatch they expect, and the form of C they write):
 //   1  register-staged streaming, 1 row block per item    16-row tiles   fp16 + bf16

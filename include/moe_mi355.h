@@ -112,9 +112,16 @@ typedef struct moe_mi355_args {
  *                                  3 streaming 32-row, 4 prefill 128-row, 5 prefill on a
  *                                  second list of 128-row tiles.  A pair that cannot run
  *                                  together gives MOE_ERR_BAD_FLAGS.
+ *                                  GEMM1 variant 5 is variant 1 with the dispatch
+ *                                  computed inside it (T <= 64, the default there; pairs
+ *                                  with GEMM2 variants 1 and 2): bit-identical output,
+ *                                  one launch fewer.
  *   MOE_MI355_FLAG_ROW_SCALES_ON / _OFF  GEMM1 reads the token scales gathered into row
  *                                  order / straight by token (default: gathered from
- *                                  T = 512).  Bit-identical results either way.
+ *                                  T = 512).  Bit-identical results either way.  GEMM1
+ *                                  variant 5 reads them by token: _ON selects the separate
+ *                                  dispatch at T <= 64 (and is an error with variant 5
+ *                                  forced).
  * Every variant meets the same tolerance; the flags change speed only. */
 #define MOE_MI355_FLAG_PROFILE 1
 #define MOE_MI355_FLAG_FORCE_PLAN 2
@@ -231,6 +238,7 @@ typedef struct moe_mi355_workspace_layout {
     int32_t tile_m;
     int32_t max_tiles;
     int32_t intermediate_format;
+    int32_t dispatch_in_gemm1;  /* 1: GEMM1 computes the dispatch (no dispatch launch) */
 } moe_mi355_workspace_layout;
 
 /* The layout of a call over T tokens with the given call flags: the regions do not

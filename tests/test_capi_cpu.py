@@ -205,12 +205,19 @@ def test_unknown_flag_bits_are_an_error(lib, flags):
 def test_layout_reports_the_forced_plan():
     k = pkg("kernel")
     assert k.workspace_layout(64).tile_m == 16 and k.workspace_layout(64).intermediate_format == 0
-    lay = k.workspace_layout(64, k.plan_flags(3, 4))
-    assert lay.tile_m == 128 and lay.intermediate_format == 1
-    lay = k.workspace_layout(64, k.plan_flags(2, 5))
-    assert lay.tile_m == 32 and lay.intermediate_format == 2
-    assert lay.total == k.workspace_layout(64).total
-    assert k.workspace_layout(9000).tile_m == 256
+    # GEMM1 computes the dispatch itself up to T = 64, a dispatch launch from T = 65
+    assert [k.workspace_layout(t).dispatch_in_gemm1 for t in (1, 8, 64, 65, 200, 9000)] == [1, 1, 1, 0, 0, 0]
+    assert k.workspace_layout(64, k.plan_flags(1, 1)).dispatch_in_gemm1 == 0
+    assert k.workspace_layout(8, k.plan_flags(5, 2)).dispatch_in_gemm1 == 1
+    lay = k.WorkspaceLayout()
+    lib = k._build_extension()
+    assert lib.moe_mi355_get_workspace_layout(65, k.plan_flags(5, 1), ctypes.byref(lay)) == -7
+    assert lib.moe_mi355_get_workspace_layout(8, k.plan_flags(5, 3), ctypes.byref(lay)) == -7
+    # gathered token scales need the separate dispatch
+    assert k.workspace_layout(8, k.FLAG_ROW_SCALES_ON).dispatch_in_gemm1 == 0
+    assert k.workspace_layout(8, k.FLAG_ROW_SCALES_OFF).dispatch_in_gemm1 == 1
+    assert lib.moe_mi355_get_workspace_layout(8, k.plan_flags(5, 1) | k.FLAG_ROW_SCALES_ON,
+                                              ctypes.byref(lay)) == -7
 
 
 def test_environment_does_not_change_the_plan():

@@ -23,7 +23,7 @@ def _eager(k, wl, d, ws):
     return out
 
 
-@pytest.mark.parametrize("idx", [0, 1, 2, 3])
+@pytest.mark.parametrize("idx", [0, 1, 2, 3, 4])
 def test_graph_replay_matches_eager(idx):
     k = pkg("kernel")
     wl = pkg("workloads")

@@ -213,7 +213,7 @@ def _flags(ws, lay):
     return ws[lay.meta + 35 * 4:lay.meta + 37 * 4].view(torch.int32).cpu().tolist()
 
 
-def _huge_inputs_check(d, c_flag):
+def _huge_inputs_check(d, c_flag, flags=0):
     """Hidden-state scales 2^10 times larger: |C| and the expert rows reach ~1e6, far
     beyond the fp16 range.  The call must raise the expert-row flag (meta[36]) and,
     on the streaming plans, the C flag (meta[35]); the combine and GEMM2 then take the
@@ -225,12 +225,12 @@ def _huge_inputs_check(d, c_flag):
     k = pkg("kernel")
     wl = pkg("workloads")
     T = d["routing_logits"].shape[0]
-    lay = k.workspace_layout(T)
+    lay = k.workspace_layout(T, flags)
     ws = torch.empty(lay.total, dtype=torch.uint8, device="cuda")
     big = dict(d)
     big["hidden_states_scale"] = d["hidden_states_scale"] * 1024.0
     out = torch.full_like(d["output"], float("nan"))
-    k.forward(*wl.as_args({**big, "output": out}), workspace=ws)
+    k.forward(*wl.as_args({**big, "output": out}), workspace=ws, flags=flags)
     torch.cuda.synchronize()
     assert _flags(ws, lay) == [c_flag, 1]
     o = oracle()
@@ -253,7 +253,7 @@ def _huge_inputs_check(d, c_flag):
     assert e_32 <= 1e-2 * scale
 
     out2 = torch.full_like(d["output"], float("nan"))
-    k.forward(*wl.as_args({**d, "output": out2}), workspace=ws)
+    k.forward(*wl.as_args({**d, "output": out2}), workspace=ws, flags=flags)
     torch.cuda.synchronize()
     assert _flags(ws, lay) == [0, 0]
     ref = run_forward(d)
@@ -261,12 +261,19 @@ def _huge_inputs_check(d, c_flag):
 
 
 def test_values_beyond_fp16_range_streaming_plan():
-    """T = 64 (streaming plan, fp16 C): C and the expert rows both overflow fp16; GEMM2
-    runs its bf16 path (the output then equals the oracle with C rounded to bf16, to
-    4e-3 of the largest output)."""
+    """T = 64 (streaming plan, fp16 C, GEMM1 with the dispatch folded in): C and the
+    expert rows both overflow fp16; GEMM2 runs its bf16 path (the output then equals
+    the oracle with C rounded to bf16, to 4e-3 of the largest output)."""
     d = dict(config_inputs(1))
     note("[gpu] values beyond the fp16 range, T=64")
     _huge_inputs_check(d, c_flag=1)
+
+
+def test_values_beyond_fp16_range_separate_dispatch():
+    """The same with the separate dispatch launch (plan 1/1)."""
+    d = dict(config_inputs(1))
+    note("[gpu] values beyond the fp16 range, T=64, separate dispatch")
+    _huge_inputs_check(d, c_flag=1, flags=pkg("kernel").plan_flags(1, 1))
 
 
 def test_values_beyond_fp16_range_converted_plan():
