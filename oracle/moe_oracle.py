@@ -24,7 +24,6 @@ from __future__ import annotations
 import ctypes
 import os
 import subprocess
-import time
 from typing import Optional, Sequence
 
 import numpy as np
@@ -393,19 +392,3 @@ def reference_cpu_forward(routing_logits, routing_bias, hidden_states, hidden_st
     output.copy_(acc.to(torch.bfloat16))
 
 
-def time_reference_cpu(inputs: dict, runs: int = 3, warmup: int = 1) -> dict:
-    """Median wall time of ``reference_cpu_forward`` on host copies of ``inputs``."""
-    host = {k: (v.detach().cpu() if isinstance(v, torch.Tensor) else v) for k, v in inputs.items()}
-    out = torch.empty_like(host["output"])
-    args = [host[k] for k in ("routing_logits", "routing_bias", "hidden_states",
-                              "hidden_states_scale", "gemm1_weights", "gemm1_weights_scale",
-                              "gemm2_weights", "gemm2_weights_scale",
-                              "local_expert_offset", "routed_scaling_factor")]
-    for _ in range(warmup):
-        reference_cpu_forward(*args, out)
-    ts = []
-    for _ in range(runs):
-        t0 = time.perf_counter()
-        reference_cpu_forward(*args, out)
-        ts.append(time.perf_counter() - t0)
-    return dict(median_s=float(np.median(ts)), runs=ts, threads=torch.get_num_threads(), output=out)
