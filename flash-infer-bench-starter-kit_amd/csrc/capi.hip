@@ -162,10 +162,11 @@ constexpr moe_mi355_workspace_layout workspace_regions(int32_t T) {
     L.sorted_weights = take(R * 4);
     L.chunk_counts = take((size_t)((T + 255) / 256) * moe::kEL * 4);
     L.row_scales = take(R * moe::kHB * 4);        // token scales in row order, [56, 8T]
-    L.intermediate = take(R * moe::kI * 6);     // hi/lo, fp16, bf16 copies
+    // hi/lo, fp16 and the fp16 form's group exponents
+    L.intermediate = take(R * (moe::kI * 4 + moe::kI / moe::kGroup16));
     L.intermediate_scales = take(R * moe::kIB * 4);
     L.expert_out = take(R * moe::kH * 2);
-    L.expert_out_wide = take(R * moe::kH * 4);
+    L.expert_out_exp = take(R * (moe::kH / moe::kGroup16));
     L.total = off;
     L.max_tiles = mt;
     return L;
@@ -286,7 +287,7 @@ int forward_impl(const moe_mi355_args& a, void* workspace, size_t ws_bytes, hipS
     const moe::Intermediate inter{ws + L.intermediate, reinterpret_cast<float*>(ws + L.intermediate_scales),
                                   T * moe::kTopK};
     const moe::ExpertRows rows{reinterpret_cast<uint16_t*>(ws + L.expert_out),
-                               reinterpret_cast<float*>(ws + L.expert_out_wide)};
+                               ws + L.expert_out_exp};
     int* chunk_cnt = reinterpret_cast<int*>(ws + L.chunk_counts);
     float* row_scales = reinterpret_cast<float*>(ws + L.row_scales);
     int* num_tiles = meta + moe::kEL + 1;

@@ -7,7 +7,7 @@
 // (gemm1.hip, store_c_hilo): s = amax/448 (1 for an all-zero block),
 // hi = e4m3(clamp(c * 448/amax)), lo = e4m3(clamp((c - hi*s) * 16*448/amax)) with
 // c - hi*s one fma.  On a call where GEMM1 flagged a value beyond the fp16 range, c is
-// GEMM1's bf16 copy wherever the fp16 value is infinite.
+// the fp16 value times its group exponent (moe_device.h).
 
 #include "moe_device.h"
 
@@ -25,17 +25,11 @@ __global__ __launch_bounds__(256) void c_f16_to_hilo_kernel(Intermediate C, cons
         const size_t off = (size_t)row * kI + col;
         const uint4 hv = *reinterpret_cast<const uint4*>(C.f16() + off);
         const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
+        // the group exponent applies only on a call whose flag is raised
+        const int e = wide ? C.f16_exp()[(size_t)row * (kI / kGroup16) + col / kGroup16] : 0;
         float x[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-            x[j] = (float)__builtin_bit_cast(_Float16, (uint16_t)((hw[j >> 1] >> (16 * (j & 1))) & 0xffffu));
-        if (wide) {
-            const uint4 bv = *reinterpret_cast<const uint4*>(C.bf16() + off);
-            const uint32_t bw[4] = {bv.x, bv.y, bv.z, bv.w};
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-                if (__builtin_isinf(x[j])) x[j] = bf16_bits_to_f32((bw[j >> 1] >> (16 * (j & 1))) & 0xffffu);
-        }
+        for (int j = 0; j < 8; ++j) x[j] = f16_scaled_to_f32((hw[j >> 1] >> (16 * (j & 1))) & 0xffffu, e);
         float m = 0.f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(x[j]));

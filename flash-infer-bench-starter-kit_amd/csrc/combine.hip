@@ -12,7 +12,7 @@
 // +0.0.  One thread produces 8 consecutive outputs (one 16-byte store), with the loads
 // of all the token's rows in flight together.  The expert rows arrive in fp16
 // (ExpertRows); on a call where GEMM2 flagged a value beyond the fp16 range, the
-// fp32 copy GEMM2 wrote replaces every infinite fp16 value.
+// rows' group exponents scale them back.
 
 #include "combine_rows.h"
 

@@ -21,7 +21,7 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
 // rows (negative: not local), sorted_w the routing weight of each row; the rows are
 // added in ascending order (ascending local expert) in fp32 and rounded once to bf16
 // into dst[0..8).  `wide` (uniform): GEMM2 flagged a value beyond the fp16 range, so
-// the fp32 copies replace the infinite fp16 values.
+// the rows' group exponents apply (moe_device.h).
 __device__ __forceinline__ void combine_token8(const ExpertRows& rows, bool wide, const int* inv_t,
                                                const float* sorted_w, int h0, uint16_t* dst) {
     // o * w, then + in ascending row order, never an fma: the fp32 accumulation of
@@ -67,10 +67,9 @@ __device__ __forceinline__ void combine_token8(const ExpertRows& rows, bool wide
 #pragma unroll
             for (int j = 0; j < 8; ++j) o[j] = f16_bits_to_f32((hw[j >> 1] >> (16 * (j & 1))) & 0xffffu);
             if constexpr (kWide) {
-                const float* cp = rows.f32 + (size_t)r[k] * kH + h0;
+                const int e = rows.exp[(size_t)r[k] * (kH / kGroup16) + h0 / kGroup16];
 #pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    if (__builtin_isinf(o[j])) o[j] = cp[j];
+                for (int j = 0; j < 8; ++j) o[j] = e ? ldexpf(o[j], e) : o[j];
             }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {

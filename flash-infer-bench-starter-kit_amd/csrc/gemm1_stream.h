@@ -14,30 +14,24 @@ __device__ __forceinline__ v4f mfma_fp8(const v8i& a, const v8i& b, const v4f& c
 
 __device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
 
-// Four SwiGLU values of row `row`, columns n0..n0+3 in fp16 (round to nearest even).
-// When one of them lies beyond the fp16 range, the four also go to the bf16 region and
-// the flag word is raised; GEMM2 then takes the bf16 value wherever the fp16 one is
-// infinite.  (Writing the bf16 copy on every call costs ~10 us at T = 1024.)
+// Four SwiGLU values of row `row`, columns n0..n0+3, in the fp16 form of C with its
+// 16-column group exponent (moe_device.h): the plain fp16 rounding unless the group
+// holds a value beyond the fp16 range, which raises the flag word.  Every lane of the
+// wave calls it; lanes with `valid` false (rows past the tile) store nothing.
 __device__ __forceinline__ void store_swiglu4(const Intermediate& C, int* __restrict__ c_wide, int row,
-                                              int n0, const v4f& g, const v4f& u) {
+                                              int n0, const v4f& g, const v4f& u, bool valid) {
     float c[4];
-    uint32_t h[4];
-    bool wide = false;
+    float m = 0.f;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
         c[v] = silu_f32(u[v]) * g[v];
-        h[v] = __builtin_bit_cast(uint16_t, (_Float16)c[v]);
-        wide = wide || fabsf(c[v]) > kF16Max;
+        m = fmaxf(m, fabsf(c[v]));
     }
-    const size_t off = (size_t)row * kI + n0;
-    *reinterpret_cast<uint2*>(C.f16() + off) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
-    if (wide) {
-        uint32_t b[4];
-#pragma unroll
-        for (int v = 0; v < 4; ++v) b[v] = f32_to_bf16_bits(c[v]);
-        *reinterpret_cast<uint2*>(C.bf16() + off) = make_uint2(b[0] | (b[1] << 16), b[2] | (b[3] << 16));
-        *c_wide = 1;
-    }
+    const int e = group_exponent(m);
+    if (!valid) return;
+    store_f16x4_scaled(C.f16() + (size_t)row * kI + n0, c, e);
+    if ((n0 & (kGroup16 - 1)) == 0) C.f16_exp()[(size_t)row * (kI / kGroup16) + n0 / kGroup16] = (uint8_t)e;
+    if (e) *c_wide = 1;
 }
 
 // ---------------------------------------------------------------------------
@@ -247,8 +241,8 @@ __device__ __forceinline__ void gemm1_rstream_item(
                     g += red[q][0][gi * CB + c][lane];
                     u += red[q][1][gi * CB + c][lane];
                 }
-                if (16 * c + r16 < nrows)
-                    store_swiglu4(C, c_wide, row0 + 16 * c + r16, (ng + gi) * 16 + kq * 4, g, u);
+                store_swiglu4(C, c_wide, row0 + 16 * c + r16, (ng + gi) * 16 + kq * 4, g, u,
+                              16 * c + r16 < nrows);
             }
     }
     __syncthreads();

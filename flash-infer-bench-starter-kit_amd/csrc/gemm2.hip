@@ -47,7 +47,7 @@ __global__ __launch_bounds__(256) void gemm2_rstream_kernel(
     } else {
         for (int work = blockIdx.x; work < nwork; work += gridDim.x) {
             const int4 tile = tiles[work / kItems];
-            gemm2_rstream_rare_item<KSPLIT, HF, CB>(C.f16(), C.bf16(), w2, s2, tile.x, tile.y,
+            gemm2_rstream_rare_item<KSPLIT, HF, CB>(C.f16(), C.f16_exp(), w2, s2, tile.x, tile.y,
                                                     tile.z, (work % kItems) * NGW * HF, rows,
                                                     flags + 1, red, wave);
         }
@@ -217,11 +217,10 @@ __global__ __launch_bounds__(512, 1) void gemm2_prefill8_kernel(
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             const int r = 64 * wm + 16 * s + r16;
-            if (r < nrows) {
 #pragma unroll
-                for (int n = 0; n < 4; ++n)
-                    store_rows4(rows, rows_wide, (size_t)(row0 + r) * kH + hg * 256 + 64 * wn + 16 * n + 4 * kq, acc[s][n]);
-            }
+            for (int n = 0; n < 4; ++n)
+                store_rows4(rows, rows_wide, row0 + r, hg * 256 + 64 * wn + 16 * n + 4 * kq, acc[s][n],
+                            r < nrows);
         }
     }
 }

@@ -31,23 +31,13 @@ __device__ __forceinline__ void e4m3x4_to_f16x4(uint32_t w, uint32_t& d0, uint32
     d1 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)w, 1.0f, true));
 }
 
-// 8 fp16 C values as bf16: the bf16 copy where the fp16 value is infinite (GEMM1 wrote
-// the copy for every value beyond the fp16 range), else the fp16 value rounded to bf16.
-__device__ __forceinline__ v4u c_f16_or_copy_to_bf16(const v4u& h, const v4u& b) {
+// 8 fp16 C values of one 16-column group (exponent e) as bf16 (round to nearest even).
+__device__ __forceinline__ v4u c_f16_scaled_to_bf16(const v4u& h, int e) {
     v4u r;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        uint32_t out = 0;
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            const uint32_t hb = (h[i] >> (16 * half)) & 0xffffu;
-            const uint32_t bb = (b[i] >> (16 * half)) & 0xffffu;
-            const float f = (float)__builtin_bit_cast(_Float16, (uint16_t)hb);
-            const uint32_t v = ((hb & 0x7fffu) == 0x7c00u) ? bb : f32_to_bf16_bits(f);
-            out |= v << (16 * half);
-        }
-        r[i] = out;
-    }
+    for (int i = 0; i < 4; ++i)
+        r[i] = f32_to_bf16_bits(f16_scaled_to_f32(h[i] & 0xffffu, e)) |
+               (f32_to_bf16_bits(f16_scaled_to_f32(h[i] >> 16, e)) << 16);
     return r;
 }
 
@@ -84,14 +74,13 @@ __device__ __forceinline__ void reduce_store(const v4f (&acc)[HF][CB], v4f (*red
     if (ks == 0) {
 #pragma unroll
         for (int c = 0; c < CB; ++c) {
-            if (16 * c + r16 < nrows) {
 #pragma unroll
-                for (int hf = 0; hf < HF; ++hf) {
-                    v4f o = red[wave][hf][c][lane];
+            for (int hf = 0; hf < HF; ++hf) {
+                v4f o = red[wave][hf][c][lane];
 #pragma unroll
-                    for (int q = 1; q < KSPLIT; ++q) o += red[wave + q][hf][c][lane];
-                    store_rows4(rows, rows_wide, (size_t)(row0 + 16 * c + r16) * kH + (hg + hf) * 16 + kq * 4, o);
-                }
+                for (int q = 1; q < KSPLIT; ++q) o += red[wave + q][hf][c][lane];
+                store_rows4(rows, rows_wide, row0 + 16 * c + r16, (hg + hf) * 16 + kq * 4, o,
+                            16 * c + r16 < nrows);
             }
         }
     }
@@ -215,12 +204,12 @@ __device__ __forceinline__ void gemm2_rstream_item(
 }
 
 // The same work items when C went beyond the fp16 range somewhere (rare): bf16 MFMAs on
-// C taken from GEMM1's bf16 copy wherever the fp16 value is infinite.  Plain loads in
+// C rebuilt from its fp16 form and group exponents.  Plain loads in
 // the MFMA layout, one K block at a time: slow, but light on registers, so the normal
 // path keeps its occupancy.
 template <int KSPLIT, int HF, int CB>
 __device__ __forceinline__ void gemm2_rstream_rare_item(
-    const uint16_t* __restrict__ inter, const uint16_t* __restrict__ inter_bf16,
+    const uint16_t* __restrict__ inter, const uint8_t* __restrict__ inter_exp,
     const uint8_t* __restrict__ w2, const float* __restrict__ s2, int le, int row0, int nrows,
     int hg0, const ExpertRows& rows, int* __restrict__ rows_wide, v4f (*red)[HF][CB][64], int wave) {
     constexpr int KB = kIB / KSPLIT;
@@ -239,11 +228,12 @@ __device__ __forceinline__ void gemm2_rstream_rare_item(
         v4u cf[CB][4];
 #pragma unroll
         for (int c = 0; c < CB; ++c) {
-            const size_t off = (size_t)(row0 + min(16 * c + r16, nrows - 1)) * kI + kb * kBlk + kq * 32;
+            const int row = row0 + min(16 * c + r16, nrows - 1);
+            const size_t off = (size_t)row * kI + kb * kBlk + kq * 32;
+            const uint8_t* ep = inter_exp + (size_t)row * (kI / kGroup16) + (kb * kBlk + kq * 32) / kGroup16;
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                cf[c][j] = c_f16_or_copy_to_bf16(*reinterpret_cast<const v4u*>(inter + off + 8 * j),
-                                                 *reinterpret_cast<const v4u*>(inter_bf16 + off + 8 * j));
+                cf[c][j] = c_f16_scaled_to_bf16(*reinterpret_cast<const v4u*>(inter + off + 8 * j), ep[j >> 1]);
         }
 #pragma unroll
         for (int hf = 0; hf < HF; ++hf) {

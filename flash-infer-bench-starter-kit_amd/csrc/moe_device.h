@@ -179,8 +179,42 @@ __device__ __forceinline__ void bdma4(__amdgpu_buffer_rsrc_t r, uint32_t voff, u
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)l, 4, voff, soff, 0, 0);
 }
 
+// Values beyond the fp16 range.  The fp16 forms below (C of the streaming GEMM1, the
+// expert rows of GEMM2) keep 11 significant bits, but overflow past 65504.  Each
+// (row, 16-column group) therefore carries a power-of-two exponent e >= 0 in one byte
+// and holds fp16(x * 2^-e): e = 0, the plain fp16 rounding, unless the group holds a
+// value beyond the fp16 range (then |x| 2^-e < 2^15 for every value of the group).
+// Readers that find the call's flag word raised apply the exponents; otherwise they
+// read the fp16 values as they are.
+constexpr int kCWideFlag = kEL + 3;    // meta word: C exceeds the fp16 range
+constexpr int kRowsWideFlag = kEL + 4; // meta word: an expert row exceeds the fp16 range
+constexpr float kF16Max = 65504.f;
+constexpr int kGroup16 = 16;           // columns per exponent byte
+
+// Exponent of a 16-column group of which this lane holds 4 values (the other 12 are in
+// lanes l ^ 16, l ^ 32, l ^ 48: the same row, the other column quads of an MFMA 16x16
+// output block), from m = the largest |x| of the lane's 4.  Every lane of the wave must
+// call it (it exchanges across lanes).
+__device__ __forceinline__ int group_exponent(float m) {
+    m = fmaxf(m, __shfl_xor(m, 16));
+    m = fmaxf(m, __shfl_xor(m, 32));
+    if (!(m > kF16Max) || !(m < __builtin_inff())) return 0;
+    int k;
+    (void)frexpf(m, &k);        // m in [2^(k-1), 2^k)
+    return k - 15;              // m 2^-e in [2^14, 2^15)
+}
+
+// Four fp16 values of a group with exponent e (element offset `off` of a row-major
+// [rows, width] array of fp16 bits), written as one 8-byte store.
+__device__ __forceinline__ void store_f16x4_scaled(uint16_t* __restrict__ dst, const float (&x)[4], int e) {
+    uint32_t h[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) h[v] = __builtin_bit_cast(uint16_t, (_Float16)(e ? ldexpf(x[v], -e) : x[v]));
+    *reinterpret_cast<uint2*>(dst) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+}
+
 // The SwiGLU rows C [rows, 2048] between GEMM1 and GEMM2 live in one workspace region
-// of rows_cap x 2048 x 6 bytes, in up to two forms chosen by the kernel plan:
+// of rows_cap x (2048 x 4 + 128) bytes, in up to two forms chosen by the kernel plan:
 //   fp8 hi/lo (bytes [0, 4 rows_cap) x 512; written by the prefill GEMM1 kernels, or
 //     converted from the fp16 form, and read by the prefill GEMM2 kernel): per row and
 //     128-column block b a scale s = amax/448 and two e4m3 rows hi = e4m3(C/s),
@@ -189,44 +223,33 @@ __device__ __forceinline__ void bdma4(__amdgpu_buffer_rsrc_t r, uint32_t voff, u
 //     first rows_cap*2048 bytes, lo the next; the scales are fp32 [16, rows_cap]
 //     (block-major, so a tile's rows are contiguous).
 //   fp16 (written by the streaming GEMM1 kernels): C rounded to fp16 in the next
-//     rows_cap*2048 halves.  fp16 keeps 11 significant bits, and so GEMM2 adds no
-//     error that matters next to the bf16 output rounding (bf16 C, 8 bits, reaches
-//     the 1e-2 tolerance on tokens whose 8 experts are all local).  For a group of 4
-//     values with one beyond the fp16 range, GEMM1 also writes the group in bf16 to
-//     the last rows_cap*2048 halves and raises the flag word meta[kCWideFlag]; the
-//     kernels that read fp16 C then take those copies where the fp16 value is
-//     infinite.
-constexpr int kCWideFlag = kEL + 3;    // meta word: C exceeds the fp16 range
-constexpr int kRowsWideFlag = kEL + 4; // meta word: an expert row exceeds the fp16 range
-constexpr float kF16Max = 65504.f;
-
+//     rows_cap*2048 halves, then the group exponents, uint8 [rows_cap, 128].  fp16 keeps
+//     11 significant bits, and so GEMM2 adds no error that matters next to the bf16
+//     output rounding (bf16 C, 8 bits, reaches the 1e-2 tolerance on tokens whose 8
+//     experts are all local).  A group beyond the fp16 range raises meta[kCWideFlag].
 // GEMM2's output, one row of 7168 per routed assignment, read by the combine: fp16
 // rows (11 significant bits keep the combine's result as close to the fp32 sums as
 // fp32 rows do, at half the bytes; bf16 rows were tried and break the 1e-2 tolerance
-// where large rows cancel).  A group of 4 values with one beyond the fp16 range is
-// also written in fp32 to `f32` (same [rows, 7168] indexing) and raises the flag word
-// meta[kRowsWideFlag]; the combine then takes those copies where the fp16 value is
-// infinite.
+// where large rows cancel), and their group exponents, uint8 [rows, 448]; a group
+// beyond the fp16 range raises meta[kRowsWideFlag].
 struct ExpertRows {
     uint16_t* f16;
-    float* f32;
+    uint8_t* exp;
 };
 
-// Four consecutive values of an expert row (element offset `off`).
+// Four consecutive values of an expert row (element offset `off`; row `row`, columns
+// col .. col + 3): fp16 with the group exponent, and the exponent byte from the lane of
+// the group's first column quad.  Every lane of the wave must call it; lanes with
+// `valid` false (rows past a tile) store nothing.
 __device__ __forceinline__ void store_rows4(const ExpertRows& rows, int* __restrict__ wide_flag,
-                                            size_t off, const v4f& o) {
-    uint32_t h[4];
-    bool wide = false;
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-        h[v] = __builtin_bit_cast(uint16_t, (_Float16)o[v]);
-        wide = wide || fabsf(o[v]) > kF16Max;
-    }
-    *reinterpret_cast<uint2*>(rows.f16 + off) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
-    if (wide) {
-        *reinterpret_cast<v4f*>(rows.f32 + off) = o;
-        *wide_flag = 1;
-    }
+                                            int row, int col, const v4f& o, bool valid) {
+    const float x[4] = {o[0], o[1], o[2], o[3]};
+    const float m = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
+    const int e = group_exponent(m);
+    if (!valid) return;
+    store_f16x4_scaled(rows.f16 + (size_t)row * kH + col, x, e);
+    if ((col & (kGroup16 - 1)) == 0) rows.exp[(size_t)row * (kH / kGroup16) + col / kGroup16] = (uint8_t)e;
+    if (e) *wide_flag = 1;
 }
 
 struct Intermediate {
@@ -236,13 +259,19 @@ struct Intermediate {
     __host__ __device__ uint16_t* f16() const {
         return static_cast<uint16_t*>(base) + (size_t)rows_cap * kI;
     }
-    __host__ __device__ uint16_t* bf16() const {
-        return static_cast<uint16_t*>(base) + 2 * (size_t)rows_cap * kI;
+    __host__ __device__ uint8_t* f16_exp() const {
+        return static_cast<uint8_t*>(base) + 4 * (size_t)rows_cap * kI;
     }
     __host__ __device__ uint8_t* hi() const { return static_cast<uint8_t*>(base); }
     __host__ __device__ uint8_t* lo() const {
         return static_cast<uint8_t*>(base) + (size_t)rows_cap * kI;
     }
 };
+
+// fp16 bits and group exponent -> fp32 (exact: the fp16 value times 2^e).
+__device__ __forceinline__ float f16_scaled_to_f32(uint32_t h, int e) {
+    const float v = (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+    return e ? ldexpf(v, e) : v;
+}
 
 }  // namespace moe

@@ -142,7 +142,7 @@ MOE_MI355_API int moe_mi355_forward(const moe_mi355_args* args, void* stream);
 /* The forward without a workspace argument and without any allocation: no reference
  * counterpart.  It is for callers that cannot allocate device memory -- code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.  The
- * workspace is the library's own file-scope device array (about 57 MB,
+ * workspace is the library's own file-scope device array (about 46 MB,
  * moe_mi355_noalloc_scratch_bytes()), one copy on each GPU the library runs on,
  * held until the process ends; its address on a GPU is looked up on the first call
  * there.  args->workspace and args->workspace_bytes are ignored.
@@ -152,7 +152,7 @@ MOE_MI355_API int moe_mi355_forward(const moe_mi355_args* args, void* stream);
  *     different streams) race and must not be issued; calls on one stream are
  *     ordered and safe.  Nothing in the array needs clearing between calls.
  * Results are bit-identical to moe_mi355_forward's. */
-#define MOE_MI355_NOALLOC_MAX_TOKENS 128
+#define MOE_MI355_NOALLOC_MAX_TOKENS 256
 MOE_MI355_API int moe_mi355_forward_noalloc(const moe_mi355_args* args, void* stream);
 /* Size in bytes of that per-GPU array. */
 MOE_MI355_API size_t moe_mi355_noalloc_scratch_bytes(void);
@@ -222,18 +222,20 @@ typedef struct moe_mi355_workspace_layout {
     size_t row_scales;      /* fp32  [56, 8T]: hidden_states_scale gathered into row order,
                                [kb][row] = scale[kb][sorted_tokens[row]] (the rows
                                in use, for the token counts where GEMM1 reads them) */
-    size_t intermediate;    /* SwiGLU output rows C, 8T x 2048 x 6 bytes:
+    size_t intermediate;    /* SwiGLU output rows C, 8T x (2048 x 4 + 128) bytes:
                                e4m3 hi [8T, 2048], e4m3 lo [8T, 2048]  (hi/lo form:
                                   C = s * (hi + lo / 16), s from intermediate_scales),
                                fp16 [8T, 2048]                          (fp16 form),
-                               bf16 [8T, 2048]  copies of the 4-value groups of the fp16
-                                  form with a value beyond the fp16 range (meta[35] set).
+                               uint8 [8T, 128] the fp16 form's exponents: per row and
+                                  16-column group e >= 0, the values held as
+                                  fp16(C 2^-e); e = 0 unless the group holds a value
+                                  beyond the fp16 range (meta[35] set).
                                intermediate_format: 0 fp16 form, 1 hi/lo form, 2 fp16
                                form converted to the hi/lo form before GEMM2 */
     size_t intermediate_scales; /* fp32 [16, 8T]: s of row r, 128-column block b at [b][r] */
     size_t expert_out;      /* fp16  [8T, 7168]  GEMM2 output rows */
-    size_t expert_out_wide; /* fp32  [8T, 7168]  copies of the 4-value groups of expert rows
-                               with a value beyond the fp16 range (meta[36] set) */
+    size_t expert_out_exp;  /* uint8 [8T, 448]   their 16-column group exponents, as for
+                               the fp16 form of C (meta[36] set when one is nonzero) */
     size_t total;
     int32_t tile_m;
     int32_t max_tiles;

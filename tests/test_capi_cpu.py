@@ -52,15 +52,20 @@ def test_workspace_bytes(lib):
     assert lay.total == sizes[3]
     offs = [lay.topk_ids, lay.topk_weights, lay.inverse_rows, lay.meta, lay.tiles,
             lay.sorted_tokens, lay.sorted_weights, lay.chunk_counts, lay.row_scales, lay.intermediate,
-            lay.expert_out, lay.expert_out_wide]
+            lay.expert_out, lay.expert_out_exp]
     assert offs == sorted(offs) and all(o % 256 == 0 for o in offs)
     assert lay.row_scales + 56 * 64 * 8 * 4 <= lay.intermediate               # [56, 8T] fp32
-    assert lay.intermediate + 64 * 8 * 2048 * 6 <= lay.intermediate_scales   # hi/lo, fp16, bf16 copies
-    assert lay.expert_out + 64 * 8 * 7168 * 2 <= lay.expert_out_wide         # fp16 expert rows
-    assert lay.expert_out_wide + 64 * 8 * 7168 * 4 <= lay.total              # their fp32 copies
+    assert lay.intermediate + 64 * 8 * (2048 * 4 + 128) <= lay.intermediate_scales  # hi/lo, fp16, exps
+    assert lay.expert_out + 64 * 8 * 7168 * 2 <= lay.expert_out_exp          # fp16 expert rows
+    assert lay.expert_out_exp + 64 * 8 * 448 <= lay.total                    # their group exponents
     assert lay.max_tiles == (64 * 8 + 15) // 16 + 32   # sized for the smallest tile height
     assert lib.moe_mi355_workspace_bytes(-1) == 0
     assert lib.moe_mi355_workspace_bytes(1 << 21) == 0
+    # no full-size shadow copies for values beyond the fp16 range: about 23 KB per routed
+    # row; with fp32 copies of the expert rows and bf16 copies of C it was 3.56 GB at
+    # T = 8192, and the cut must be at least 40 %
+    assert k.workspace_bytes(8192) < 8192 * 8 * 23.5e3
+    assert k.workspace_bytes(8192) <= 0.6 * 3_556_769_792
 
 
 def test_forward_rejects_bad_arguments_without_a_gpu(lib):

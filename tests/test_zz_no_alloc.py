@@ -11,7 +11,7 @@ import torch
 
 from conftest import pkg
 
-MAX_T = 128          # MOE_MI355_NOALLOC_MAX_TOKENS
+MAX_T = 256          # MOE_MI355_NOALLOC_MAX_TOKENS
 
 
 def _args(k, d, out):
@@ -53,7 +53,7 @@ def test_noalloc_rejects_sizes_beyond_its_maximum():
 
 @pytest.mark.gpu
 def test_noalloc_matches_forward_on_consecutive_calls():
-    """T = 128 (the maximum), then smaller calls on the same array (37 tokens with
+    """T = 256 (the maximum), then smaller calls on the same array (37 tokens with
     another expert offset, then 5): each output is bit-identical to
     moe_mi355_forward's with a fresh workspace, and the call allocates no memory
     through torch."""
