@@ -335,9 +335,21 @@ __global__ __launch_bounds__(256) void gemm1_prefill_kernel(
 // offsets, the K step in the scalar offset), issued in two bursts per K block:
 // the token rows right after the barrier, the weight rows and token scales after
 // the third weight block's MFMAs, so the texture path is not flooded at once.
-// Each weight operand is read from LDS one block ahead of its MFMAs.
+// Each weight operand is read from LDS one block ahead of its MFMAs, and each fresh
+// partial is scaled into its accumulator only after the next weight block's MFMA of
+// the same token block has issued (fixed order), so no FMA waits on its MFMA.
+// A workgroup resolves the metadata of all its items at kernel start
+// (prefill_items) and issues the first stage of its next item at the top of the
+// current item's last K block; the epilogue's row-maximum exchange therefore uses
+// stage 1, which the last K block reads.
 // Token offsets are 32-bit: T * 7168 < 2^32 (T <= 2^19, checked by the host).
 // ---------------------------------------------------------------------------
+struct Gemm1Item {   // uniform part of an item; the per-lane DMA offsets live apart
+    __amdgpu_buffer_rsrc_t w;
+    int le, row0, nrows, ng;
+    bool tok_live, sca_live;
+};
+
 __global__ __launch_bounds__(512, 1) void gemm1_prefill8_kernel(
     const uint8_t* __restrict__ hidden, TokenScales sa, int T,
     const uint8_t* __restrict__ w1, const float* __restrict__ s1,
@@ -350,83 +362,113 @@ __global__ __launch_bounds__(512, 1) void gemm1_prefill8_kernel(
     constexpr int kW = 256 * kBlk;              // 32 KB weight rows
     constexpr int kStage = kA + kW + 8 * 256;   // + per-wave token-scale rows
     constexpr int kWeightBurstAfter = 2;        // weight block after which burst 2 goes
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * kStage];
+    constexpr int kItemCap = 1024;              // per-workgroup item table (16 KB of LDS)
+    static_assert(kHB % 2 == 0, "the next item's first stage must be stage 0");
+    // one LDS object: the stages, then the item table
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * kStage + kItemCap * sizeof(int4)];
+    int4* const s_items = reinterpret_cast<int4*>(lds + NS * kStage);
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int r16 = lane & 15, kq = lane >> 4;
     const int wm = wave >> 1, wn = wave & 1;
     const v4f zero = {0.f, 0.f, 0.f, 0.f};
-    const int ntl = *num_tiles;
-    const int nitems = ntl * NG;
+    const int nitems = *num_tiles * NG;
     const int G = gridDim.x;
-    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, per = G >> 3;
+    const int base = (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3);   // XCD-contiguous slot
     const int drow = lane >> 3, dchunk = lane & 7;
     const int swz = swz128(r16);
     const int c0 = ((2 * kq) ^ swz) << 4, c1 = ((2 * kq + 1) ^ swz) << 4;
     const __amdgpu_buffer_rsrc_t rs_tok = buffer_rsrc(hidden, (uint32_t)T * kH);
     const __amdgpu_buffer_rsrc_t rs_sca = buffer_rsrc(sa.p, (uint32_t)sa.stride * kHB * 4);
+    // wave w moves token rows 32w..32w+31 and weight rows 32w..32w+31 of the stage; the
+    // weight rows' lane offsets are relative to the item's first gate row (the resource
+    // base), so they do not depend on the item
+    uint32_t woff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = 32 * wave + 8 * i + drow;
+        const int n = (r < 128) ? r : kI + (r - 128);
+        woff[i] = (uint32_t)n * kH + ((dchunk ^ swz128(r)) << 4);
+    }
 
-    for (int round = 0; round * G < nitems; ++round) {
-        const int item = round * G + xcd * per + slot;
-        if (item >= nitems) continue;
-        int tix, ng;
-        grouped_item<BM>(item, NG, tiles, exp_off, tix, ng);
-        const int4 tile = tiles[tix];
-        const int le = tile.x, row0 = tile.y, nrows = tile.z;
-        const __amdgpu_buffer_rsrc_t rs_w = buffer_rsrc(w1 + (size_t)le * kN1 * kH, (uint32_t)kN1 * kH);
+    const int nr = prefill_items<BM>(s_items, kItemCap, nitems, NG, base, G, tiles, exp_off);
+    if (nr == 0) return;   // uniform: the whole workgroup has no item
+    __syncthreads();
 
-        // wave w moves token rows 32w..32w+31 and weight rows 32w..32w+31
-        uint32_t aoff[4], woff[4];
+    // token-row and token-scale offsets of the item whose stages are being fetched
+    uint32_t aoff[4], soff;
+    auto make_item = [&](int r) {
+        const int4 m = prefill_item<BM>(s_items, kItemCap, r, NG, base, G, tiles, exp_off);
+        Gemm1Item it;
+        it.le = m.x;
+        it.row0 = m.y;
+        it.nrows = m.z;
+        it.ng = m.w;
+        const size_t first = (size_t)it.le * kN1 + (size_t)it.ng * 128;
+        it.w = buffer_rsrc(w1 + first * kH, (uint32_t)(((size_t)(it.le + 1) * kN1 - first) * kH));
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int r = 32 * wave + 8 * i + drow;
-            const int tok = sorted_tok[row0 + min(r, nrows - 1)];
+            const int tok = sorted_tok[it.row0 + min(r, it.nrows - 1)];
             aoff[i] = (uint32_t)tok * kH + ((dchunk ^ swz128(r)) << 4);
-            const int n = (r < 128) ? ng * 128 + r : kI + ng * 128 + (r - 128);
-            woff[i] = (uint32_t)n * kH + ((dchunk ^ swz128(r)) << 4);
         }
-        const int srow = row0 + min(64 * wm + lane, nrows - 1);
-        const uint32_t soff = (uint32_t)(sa.by_row ? srow : sorted_tok[srow]) * 4;
-        const float* sgp = s1 + (size_t)(le * kN1B + ng) * kHB;
-        const float* sup = sgp + (size_t)kIB * kHB;
-
+        const int srow = it.row0 + min(64 * wm + lane, it.nrows - 1);
+        soff = (uint32_t)(sa.by_row ? srow : sorted_tok[srow]) * 4;
         // a wave whose 32 token rows all lie past the tile moves nothing: they would only
         // repeat the last row, and the MFMAs of their 16-row blocks are skipped
-        const bool tok_live = 32 * wave < nrows;
-        auto issue_tokens = [&](int kb) {
-            uint8_t* st = lds + (kb & 1) * kStage;
-            if (tok_live) {
+        it.tok_live = 32 * wave < it.nrows;
+        it.sca_live = 64 * wm < it.nrows;
+        return it;
+    };
+    auto issue_tokens = [&](const Gemm1Item& it, int kb) {
+        uint8_t* st = lds + (kb & 1) * kStage;
+        if (it.tok_live) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) bdma16(rs_tok, aoff[i], (uint32_t)kb * kBlk, st + (32 * wave + 8 * i) * kBlk);
-            }
-        };
-        auto issue_weights = [&](int kb) {
-            uint8_t* st = lds + (kb & 1) * kStage;
+            for (int i = 0; i < 4; ++i) bdma16(rs_tok, aoff[i], (uint32_t)kb * kBlk, st + (32 * wave + 8 * i) * kBlk);
+        }
+    };
+    auto issue_weights = [&](const Gemm1Item& it, int kb) {
+        uint8_t* st = lds + (kb & 1) * kStage;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) bdma16(rs_w, woff[i], (uint32_t)kb * kBlk, st + kA + (32 * wave + 8 * i) * kBlk);
-            if (64 * wm < nrows) bdma4(rs_sca, soff, (uint32_t)kb * sa.stride * 4, st + kA + kW + wave * 256);
-        };
+        for (int i = 0; i < 4; ++i) bdma16(it.w, woff[i], (uint32_t)kb * kBlk, st + kA + (32 * wave + 8 * i) * kBlk);
+        if (it.sca_live) bdma4(rs_sca, soff, (uint32_t)kb * sa.stride * 4, st + kA + kW + wave * 256);
+    };
 
+    Gemm1Item cur = make_item(0), nxt = cur;
+    issue_tokens(cur, 0);
+    issue_weights(cur, 0);
+    for (int r = 0; r < nr; ++r) {
+        const bool more = r + 1 < nr;
+        // weight block scales of the gate and up rows (scalar loads from the kernel argument)
+        const float* sgp = s1 + (size_t)(cur.le * kN1B + cur.ng) * kHB;
+        const float* sup = sgp + (size_t)kIB * kHB;
         v4f acc[4][8];
 #pragma unroll
         for (int s = 0; s < 4; ++s)
 #pragma unroll
             for (int j = 0; j < 8; ++j) acc[s][j] = zero;
 
-        __syncthreads();
-        issue_tokens(0);
-        issue_weights(0);
         // token rows 64 wm + 16 s .. of this wave that exist: the MFMAs of padding
         // blocks are skipped (the DMA and barriers stay the same for every wave)
         auto kloop = [&](auto live) {
         constexpr int NLIVE = decltype(live)::value;
+        constexpr int NT = NLIVE > 0 ? NLIVE : 1;
 #pragma unroll 1
         for (int kb = 0; kb < kHB; ++kb) {
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
             __syncthreads();
-            if (kb + 1 < kHB) issue_tokens(kb + 1);
+            if (kb + 1 < kHB) {
+                issue_tokens(cur, kb + 1);
+                if (kWeightBurstAfter < 0 || NLIVE == 0) issue_weights(cur, kb + 1);
+            } else if (more) {
+                // stage 0 is free (every wave is past K block kHB - 2): the next item's first stage
+                nxt = make_item(r + 1);
+                issue_tokens(nxt, 0);
+                issue_weights(nxt, 0);
+            }
             __builtin_amdgcn_sched_barrier(0);
+            if (NLIVE == 0) continue;
 
             const uint8_t* st = lds + (kb & 1) * kStage;
             const float fsg = sgp[kb], fsu = sup[kb];
@@ -450,30 +492,43 @@ __global__ __launch_bounds__(512, 1) void gemm1_prefill8_kernel(
                 const v4u x1 = *reinterpret_cast<const v4u*>(rp + c1);
                 return v8i{(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
             };
-            v8i bw_next = NLIVE ? read_w(0) : v8i{};
+            v8i bw = read_w(0);
+            v4f tp[NT];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                __builtin_amdgcn_sched_barrier(0);
-                const v8i bw = bw_next;
-                if (NLIVE && j < 7) bw_next = read_w(j + 1);
+                v8i bwn = bw;
+                if (j < 7) bwn = read_w(j + 1);
                 if (j == kWeightBurstAfter && kb + 1 < kHB) {
                     __builtin_amdgcn_sched_barrier(0);
-                    issue_weights(kb + 1);
-                    __builtin_amdgcn_sched_barrier(0);
+                    issue_weights(cur, kb + 1);
                 }
 #pragma unroll
                 for (int s = 0; s < NLIVE; ++s) {
-                    const v4f t = mfma_fp8(bw, bt[s], zero);
-                    const float f = (j < 4) ? fg[s] : fu[s];
+                    __builtin_amdgcn_sched_barrier(0);
+                    const v4f tc = mfma_fp8(bw, bt[s], zero);
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (j > 0) {
+                        const float f = (j - 1 < 4) ? fg[s] : fu[s];
 #pragma unroll
-                    for (int v = 0; v < 4; ++v) acc[s][j][v] = __builtin_fmaf(t[v], f, acc[s][j][v]);
+                        for (int v = 0; v < 4; ++v) acc[s][j - 1][v] = __builtin_fmaf(tp[s][v], f, acc[s][j - 1][v]);
+                    }
+                    tp[s] = tc;
                 }
+                bw = bwn;
             }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int s = 0; s < NLIVE; ++s)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[s][7][v] = __builtin_fmaf(tp[s][v], fu[s], acc[s][7][v]);
         }
         };
-        with_live_blocks(live_blocks(64 * wm, nrows), kloop);
+        with_live_blocks(live_blocks(64 * wm, cur.nrows), kloop);
 
-        store_c_hilo(acc, reinterpret_cast<float*>(lds), wm, wn, kq, r16, row0, nrows, ng, C);
+        // the next item's first stage is landing in stage 0: the exchange uses stage 1
+        store_c_hilo(acc, reinterpret_cast<float*>(lds + kStage), wm, wn, kq, r16, cur.row0, cur.nrows,
+                     cur.ng, C);
+        cur = nxt;
     }
 }
 

@@ -12,7 +12,13 @@ __device__ __forceinline__ v4f mfma_fp8(const v8i& a, const v8i& b, const v4f& c
     return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
 
-__device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
+// SiLU x / (1 + e^-x) = x * rcp(1 + 2^(-x log2 e)) on the hardware exp2 and reciprocal
+// (v_exp_f32, v_rcp_f32, about 1 ulp each): five instructions instead of a libm expf and
+// an IEEE division, which made the GEMM1 epilogues VALU-bound.  Large |x| behave as the
+// exact form: 2^+big -> inf -> rcp 0 -> -0 for x << 0, 2^-big -> 0 -> x for x >> 0.
+__device__ __forceinline__ float silu_f32(float x) {
+    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * 1.4426950408889634f));
+}
 
 // Four SwiGLU values of row `row`, columns n0..n0+3, in the fp16 form of C with its
 // 16-column group exponent (moe_device.h): the plain fp16 rounding unless the group

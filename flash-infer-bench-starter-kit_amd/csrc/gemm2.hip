@@ -70,8 +70,21 @@ __global__ __launch_bounds__(256) void gemm2_rstream_kernel(
 // the barrier, W2 after the second column block's MFMAs); rows keep 16-byte chunk c
 // at c ^ swz128(r).  Items (128-row piece, 256-column group) are grouped up to 4
 // pieces of one expert x all column groups with an XCD-contiguous mapping, as in
-// the prefill GEMM1.
+// the prefill GEMM1.  A workgroup resolves the metadata of all its items at kernel
+// start (prefill_items) and issues the first stage of its next item at the top of
+// the current item's last K block, so the next item's data arrives while the last
+// block computes and the epilogue stores.  In a K block, each 16 x 16 block's hi
+// and lo MFMAs are separated by the other row blocks' MFMAs, and the fresh partials
+// of one column block are scaled into the accumulators while the next column
+// block's MFMAs run (fixed order), so no instruction waits on the MFMA before it.
 // Tiles hold at most 128 rows.
+struct Gemm2Item {
+    __amdgpu_buffer_rsrc_t hi, lo, cs, w;
+    uint32_t coff[2], csoff;
+    int le, row0, nrows, hg;
+    bool c_live;
+};
+
 __global__ __launch_bounds__(512, 1) void gemm2_prefill8_kernel(
     Intermediate C, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
     const int4* __restrict__ tiles, const int* __restrict__ num_tiles,
@@ -83,88 +96,110 @@ __global__ __launch_bounds__(512, 1) void gemm2_prefill8_kernel(
     constexpr int kW = 256 * kBlk;              // 32 KB of W2 rows
     constexpr int kStage = 2 * kC + kW + BM * 4;
     constexpr int kWeightBurstAfter = 1;
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * kStage];
+    constexpr int kItemCap = 1024;              // per-workgroup item table (16 KB of LDS)
+    static_assert(kIB % 2 == 0, "the next item's first stage must be stage 0");
+    // one LDS object: the stages, then the item table
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * kStage + kItemCap * sizeof(int4)];
+    int4* const s_items = reinterpret_cast<int4*>(lds + NS * kStage);
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int r16 = lane & 15, kq = lane >> 4;
     const int wm = wave >> 2, wn = wave & 3;
     const v4f zero = {0.f, 0.f, 0.f, 0.f};
-    const int nvt = *num_tiles;
-    const int nitems = nvt * NG;
+    const int nitems = *num_tiles * NG;
     const int G = gridDim.x;
-    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, per = G >> 3;
+    const int base = (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3);   // XCD-contiguous slot
     const int drow = lane >> 3, dchunk = lane & 7;
     const int swz = swz128(r16);
     const int c0 = ((2 * kq) ^ swz) << 4, c1 = ((2 * kq + 1) ^ swz) << 4;
+    // W2 rows of a wave's DMA do not depend on the item
+    uint32_t woff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = 32 * wave + 8 * i + drow;
+        woff[i] = (uint32_t)r * kI + ((dchunk ^ swz128(r)) << 4);
+    }
 
-    for (int round = 0; round * G < nitems; ++round) {
-        const int item = round * G + xcd * per + slot;
-        if (item >= nitems) continue;            // uniform per workgroup
-        int vix, hg;
-        grouped_item<BM>(item, NG, tiles, exp_off, vix, hg);
-        const int4 tile = tiles[vix];
-        const int le = tile.x, row0 = tile.y, nrows = tile.z;
+    const int nr = prefill_items<BM>(s_items, kItemCap, nitems, NG, base, G, tiles, exp_off);
+    if (nr == 0) return;   // uniform: the whole workgroup has no item
+    __syncthreads();
 
-        const __amdgpu_buffer_rsrc_t rs_hi = buffer_rsrc(C.hi() + (size_t)row0 * kI, BM * kI);
-        const __amdgpu_buffer_rsrc_t rs_lo = buffer_rsrc(C.lo() + (size_t)row0 * kI, BM * kI);
-        const __amdgpu_buffer_rsrc_t rs_cs = buffer_rsrc(C.scales + row0, (uint32_t)(kIB * C.rows_cap - row0) * 4);
-        const __amdgpu_buffer_rsrc_t rs_w = buffer_rsrc(w2 + ((size_t)le * kH + hg * 256) * kI, 256 * kI);
+    auto make_item = [&](int r) {
+        const int4 m = prefill_item<BM>(s_items, kItemCap, r, NG, base, G, tiles, exp_off);
+        Gemm2Item it;
+        const int le = m.x;
+        it.le = le;
+        it.row0 = m.y;
+        it.nrows = m.z;
+        it.hg = m.w;
+        it.hi = buffer_rsrc(C.hi() + (size_t)it.row0 * kI, BM * kI);
+        it.lo = buffer_rsrc(C.lo() + (size_t)it.row0 * kI, BM * kI);
+        it.cs = buffer_rsrc(C.scales + it.row0, (uint32_t)(kIB * C.rows_cap - it.row0) * 4);
+        it.w = buffer_rsrc(w2 + ((size_t)le * kH + it.hg * 256) * kI, 256 * kI);
         // wave w moves C rows 16w..16w+15 (hi and lo) and W2 rows 32w..32w+31; waves 0
         // and 1 move the row scales of rows 64w..64w+63
-        uint32_t coff[2], woff[4];
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int r = 16 * wave + 8 * i + drow;
-            coff[i] = (uint32_t)min(r, nrows - 1) * kI + ((dchunk ^ swz128(r)) << 4);
+            it.coff[i] = (uint32_t)min(r, it.nrows - 1) * kI + ((dchunk ^ swz128(r)) << 4);
         }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = 32 * wave + 8 * i + drow;
-            woff[i] = (uint32_t)r * kI + ((dchunk ^ swz128(r)) << 4);
-        }
-        const uint32_t csoff = (uint32_t)min(64 * wave + lane, nrows - 1) * 4;
-        const float* sbp = s2 + (size_t)(le * kHB + 2 * hg + (wn >> 1)) * kIB;
-
+        it.csoff = (uint32_t)min(64 * wave + lane, it.nrows - 1) * 4;
         // a wave whose 16 C rows all lie past the tile moves nothing: they would only
         // repeat the last row, and the MFMAs of their 16-row block are skipped
-        const bool c_live = 16 * wave < nrows;
-        auto issue_c = [&](int kb) {
-            uint8_t* st = lds + (kb & 1) * kStage;
-            if (c_live) {
+        it.c_live = 16 * wave < it.nrows;
+        return it;
+    };
+    auto issue_c = [&](const Gemm2Item& it, int kb) {
+        uint8_t* st = lds + (kb & 1) * kStage;
+        if (it.c_live) {
 #pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    bdma16(rs_hi, coff[i], (uint32_t)kb * kBlk, st + (16 * wave + 8 * i) * kBlk);
-                    bdma16(rs_lo, coff[i], (uint32_t)kb * kBlk, st + kC + (16 * wave + 8 * i) * kBlk);
-                }
+            for (int i = 0; i < 2; ++i) {
+                bdma16(it.hi, it.coff[i], (uint32_t)kb * kBlk, st + (16 * wave + 8 * i) * kBlk);
+                bdma16(it.lo, it.coff[i], (uint32_t)kb * kBlk, st + kC + (16 * wave + 8 * i) * kBlk);
             }
-            if (wave < 2 && 64 * wave < nrows)
-                bdma4(rs_cs, csoff, (uint32_t)kb * C.rows_cap * 4, st + 2 * kC + kW + wave * 256);
-        };
-        auto issue_w = [&](int kb) {
-            uint8_t* st = lds + (kb & 1) * kStage;
+        }
+        if (wave < 2 && 64 * wave < it.nrows)
+            bdma4(it.cs, it.csoff, (uint32_t)kb * C.rows_cap * 4, st + 2 * kC + kW + wave * 256);
+    };
+    auto issue_w = [&](const Gemm2Item& it, int kb) {
+        uint8_t* st = lds + (kb & 1) * kStage;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) bdma16(rs_w, woff[i], (uint32_t)kb * kBlk, st + 2 * kC + (32 * wave + 8 * i) * kBlk);
-        };
+        for (int i = 0; i < 4; ++i) bdma16(it.w, woff[i], (uint32_t)kb * kBlk, st + 2 * kC + (32 * wave + 8 * i) * kBlk);
+    };
 
+    Gemm2Item cur = make_item(0), nxt = cur;
+    issue_c(cur, 0);
+    issue_w(cur, 0);
+    for (int r = 0; r < nr; ++r) {
+        const bool more = r + 1 < nr;
+        // W2 block scales of this wave's columns (scalar loads from the kernel argument)
+        const float* sbp = s2 + (size_t)(cur.le * kHB + 2 * cur.hg + (wn >> 1)) * kIB;
         v4f acc[4][4];
 #pragma unroll
         for (int s = 0; s < 4; ++s)
 #pragma unroll
             for (int n = 0; n < 4; ++n) acc[s][n] = zero;
 
-        __syncthreads();
-        issue_c(0);
-        issue_w(0);
         // 16-row blocks of this wave that exist: padding blocks skip their MFMAs
         auto kloop = [&](auto live) {
         constexpr int NLIVE = decltype(live)::value;
+        constexpr int NT = NLIVE > 0 ? NLIVE : 1;
 #pragma unroll 1
         for (int kb = 0; kb < kIB; ++kb) {
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
             __syncthreads();
-            if (kb + 1 < kIB) issue_c(kb + 1);
+            if (kb + 1 < kIB) {
+                issue_c(cur, kb + 1);
+                if (NLIVE == 0) issue_w(cur, kb + 1);
+            } else if (more) {
+                // stage 0 is free (every wave is past K block kIB - 2): the next item's first stage
+                nxt = make_item(r + 1);
+                issue_c(nxt, 0);
+                issue_w(nxt, 0);
+            }
             __builtin_amdgcn_sched_barrier(0);
+            if (NLIVE == 0) continue;
 
             const uint8_t* st = lds + (kb & 1) * kStage;
             const float sw = sbp[kb];
@@ -173,16 +208,16 @@ __global__ __launch_bounds__(512, 1) void gemm2_prefill8_kernel(
             float f[4];
 #pragma unroll
             for (int s = 0; s < NLIVE; ++s) {
-                const int r = 64 * wm + 16 * s + r16;
-                const uint8_t* ph = st + r * kBlk;
-                const uint8_t* pl = st + kC + r * kBlk;
+                const int rr = 64 * wm + 16 * s + r16;
+                const uint8_t* ph = st + rr * kBlk;
+                const uint8_t* pl = st + kC + rr * kBlk;
                 const v4u h0 = *reinterpret_cast<const v4u*>(ph + c0);
                 const v4u h1 = *reinterpret_cast<const v4u*>(ph + c1);
                 const v4u l0 = *reinterpret_cast<const v4u*>(pl + c0);
                 const v4u l1 = *reinterpret_cast<const v4u*>(pl + c1);
                 ch[s] = v8i{(int)h0[0], (int)h0[1], (int)h0[2], (int)h0[3], (int)h1[0], (int)h1[1], (int)h1[2], (int)h1[3]};
                 cl[s] = v8i{(int)l0[0], (int)l0[1], (int)l0[2], (int)l0[3], (int)l1[0], (int)l1[1], (int)l1[2], (int)l1[3]};
-                f[s] = csr[r] * sw;
+                f[s] = csr[rr] * sw;
             }
             auto read_w = [&](int n) {
                 const uint8_t* rp = st + 2 * kC + (64 * wn + 16 * n + r16) * kBlk;
@@ -190,42 +225,58 @@ __global__ __launch_bounds__(512, 1) void gemm2_prefill8_kernel(
                 const v4u x1 = *reinterpret_cast<const v4u*>(rp + c1);
                 return v8i{(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
             };
-            v8i w_next = NLIVE ? read_w(0) : v8i{};
+            v8i w = read_w(0);
+            v4f tp[NT];
 #pragma unroll
             for (int n = 0; n < 4; ++n) {
-                __builtin_amdgcn_sched_barrier(0);
-                const v8i w = w_next;
-                if (NLIVE && n < 3) w_next = read_w(n + 1);
+                v8i wnx = w;
+                if (n < 3) wnx = read_w(n + 1);
                 if (n == kWeightBurstAfter && kb + 1 < kIB) {
                     __builtin_amdgcn_sched_barrier(0);
-                    issue_w(kb + 1);
+                    issue_w(cur, kb + 1);
+                }
+                v4f tc[NT];
+#pragma unroll
+                for (int s = 0; s < NLIVE; ++s) {
                     __builtin_amdgcn_sched_barrier(0);
+                    tc[s] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(w, ch[s], zero, 0, 0, 0, 0, 0, 0);
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (n > 0) {
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) acc[s][n - 1][v] = __builtin_fmaf(tp[s][v], f[s], acc[s][n - 1][v]);
+                    }
                 }
 #pragma unroll
                 for (int s = 0; s < NLIVE; ++s) {
-                    v4f t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(w, ch[s], zero, 0, 0, 0, 0, 0, 0);
-                    t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(w, cl[s], t, 0, 0, 0, 127, 0, 123);
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) acc[s][n][v] = __builtin_fmaf(t[v], f[s], acc[s][n][v]);
+                    __builtin_amdgcn_sched_barrier(0);
+                    tc[s] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(w, cl[s], tc[s], 0, 0, 0, 127, 0, 123);
                 }
+#pragma unroll
+                for (int s = 0; s < NLIVE; ++s) tp[s] = tc[s];
+                w = wnx;
             }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int s = 0; s < NLIVE; ++s)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[s][3][v] = __builtin_fmaf(tp[s][v], f[s], acc[s][3][v]);
         }
         };
-        with_live_blocks(live_blocks(64 * wm, nrows), kloop);
+        with_live_blocks(live_blocks(64 * wm, cur.nrows), kloop);
 
         // lane holds D[h = 64 wn + 16 n + 4 kq + v][row = 64 wm + 16 s + r16]
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            const int r = 64 * wm + 16 * s + r16;
+            const int rr = 64 * wm + 16 * s + r16;
 #pragma unroll
             for (int n = 0; n < 4; ++n)
-                store_rows4(rows, rows_wide, row0 + r, hg * 256 + 64 * wn + 16 * n + 4 * kq, acc[s][n],
-                            r < nrows);
+                store_rows4(rows, rows_wide, cur.row0 + rr, cur.hg * 256 + 64 * wn + 16 * n + 4 * kq, acc[s][n],
+                            rr < cur.nrows);
         }
+        cur = nxt;
     }
 }
 
-// Debug: widen e4m3 bytes to bf16 with the same conversion GEMM2 uses (n % 4 == 0).
 __global__ void e4m3_to_bf16_kernel(const uint32_t* __restrict__ in, uint2* __restrict__ out, int nwords) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= nwords) return;

@@ -104,6 +104,45 @@ __device__ __forceinline__ void grouped_item(int item, int ncol, const int4* __r
     col = in / gm;
 }
 
+// Work list of one workgroup of a prefill GEMM: round r handles item r * G + base
+// (base = XCD-aware slot of the workgroup, G = grid size), and {expert, first row,
+// rows, column group} of that item is one grouped_item chain of three dependent loads.
+// prefill_items resolves the chains of all rounds at once, one lane per round, into
+// `tab` (LDS, `cap` entries), so that a workgroup waits for one chain at kernel start
+// instead of one per item; rounds past `cap` are resolved when they come
+// (prefill_item).  Returns the number of rounds that have an item.
+template <int TM>
+__device__ __forceinline__ int prefill_items(int4* tab, int cap, int nitems, int ncol, int base,
+                                             int G, const int4* __restrict__ tiles,
+                                             const int* __restrict__ exp_off) {
+    const int nr = nitems > base ? (nitems - base + G - 1) / G : 0;
+    for (int r = threadIdx.x; r < min(nr, cap); r += blockDim.x) {
+        int tix, col;
+        grouped_item<TM>(r * G + base, ncol, tiles, exp_off, tix, col);
+        const int4 t = tiles[tix];
+        tab[r] = int4{t.x, t.y, t.z, col};
+    }
+    return nr;
+}
+
+template <int TM>
+__device__ __forceinline__ int4 prefill_item(const int4* tab, int cap, int r, int ncol, int base,
+                                             int G, const int4* __restrict__ tiles,
+                                             const int* __restrict__ exp_off) {
+    int4 m;
+    if (r < cap) {
+        m = tab[r];
+    } else {
+        int tix, col;
+        grouped_item<TM>(r * G + base, ncol, tiles, exp_off, tix, col);
+        const int4 t = tiles[tix];
+        m = int4{t.x, t.y, t.z, col};
+    }
+    // the same for every lane: keep it in scalar registers (buffer resources, loop bounds)
+    return int4{__builtin_amdgcn_readfirstlane(m.x), __builtin_amdgcn_readfirstlane(m.y),
+                __builtin_amdgcn_readfirstlane(m.z), __builtin_amdgcn_readfirstlane(m.w)};
+}
+
 // Token scales as GEMM1 reads them: p[kb * stride + i], where i is the token (by_row 0:
 // the caller's hidden_states_scale [56, T], stride T) or the row of the permutation
 // (by_row 1: the gathered row scales [56, rows_cap], stride rows_cap, in which the rows
