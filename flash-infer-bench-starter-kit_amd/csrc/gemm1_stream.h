@@ -33,6 +33,12 @@ __device__ __forceinline__ void store_swiglu4(const Intermediate& C, int* __rest
         c[v] = silu_f32(u[v]) * g[v];
         m = fmaxf(m, fabsf(c[v]));
     }
+    if (!beyond_f16_in_wave(m)) {     // the usual case: every exponent of the call is 0
+        if (!valid) return;
+        store_f16x4_scaled(C.f16() + (size_t)row * kI + n0, c, 0);
+        if ((n0 & (kGroup16 - 1)) == 0) C.f16_exp()[(size_t)row * (kI / kGroup16) + n0 / kGroup16] = 0;
+        return;
+    }
     const int e = group_exponent(m);
     if (!valid) return;
     store_f16x4_scaled(C.f16() + (size_t)row * kI + n0, c, e);

@@ -243,6 +243,13 @@ __device__ __forceinline__ int group_exponent(float m) {
     return k - 15;              // m 2^-e in [2^14, 2^15)
 }
 
+// Whether some lane's largest |x| (m) is a finite value beyond the fp16 range: the
+// only case in which a group exponent can differ from 0.  Uniform across the wave, so
+// the callers take group_exponent's lane exchanges only then.
+__device__ __forceinline__ bool beyond_f16_in_wave(float m) {
+    return __any(m > kF16Max && m < __builtin_inff());
+}
+
 // Four fp16 values of a group with exponent e (element offset `off` of a row-major
 // [rows, width] array of fp16 bits), written as one 8-byte store.
 __device__ __forceinline__ void store_f16x4_scaled(uint16_t* __restrict__ dst, const float (&x)[4], int e) {
@@ -284,6 +291,12 @@ __device__ __forceinline__ void store_rows4(const ExpertRows& rows, int* __restr
                                             int row, int col, const v4f& o, bool valid) {
     const float x[4] = {o[0], o[1], o[2], o[3]};
     const float m = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
+    if (!beyond_f16_in_wave(m)) {     // the usual case: every exponent of the call is 0
+        if (!valid) return;
+        store_f16x4_scaled(rows.f16 + (size_t)row * kH + col, x, 0);
+        if ((col & (kGroup16 - 1)) == 0) rows.exp[(size_t)row * (kH / kGroup16) + col / kGroup16] = 0;
+        return;
+    }
     const int e = group_exponent(m);
     if (!valid) return;
     store_f16x4_scaled(rows.f16 + (size_t)row * kH + col, x, e);
