@@ -62,9 +62,8 @@ constexpr int kMinTileM = 16;           // smallest row tile; sizes the tile lis
 // about 36 rows at T = 1152 and streams its weights about once.  From T = 705 the
 // streaming GEMM1 feeds the prefill GEMM2 (128-row tiles, FP8 MFMA on the hi/lo form),
 // the faster GEMM2 there; from T = 1537 both GEMMs are the MFMA-bound prefill kernels
-// on 256-row tiles (GEMM2 on the 128-row second list).  The 128-row prefill pair
-// (variants 3 / 4) stays reachable through MOE_MI355_FLAG_FORCE_PLAN.  The boundaries
-// come from wall-clock sweeps of the pairs at T = 64 .. 2560 on MI355X.
+// on 256-row tiles (GEMM2 on the 128-row second list).  The boundaries come from
+// wall-clock sweeps of the pairs at T = 64 .. 2560 on MI355X.
 struct Plan {
     int tm;        // tile height of the first list
     int tm2;       // tile height of the second list (0: none)
@@ -74,9 +73,9 @@ struct Plan {
     bool dispatch_in_gemm1;   // GEMM1 variant 5 computes the dispatch itself (no launch)
 };
 
-int g1_tile_m(int v) { return v == 1 || v == 5 ? 16 : v == 2 ? 32 : v == 3 ? 128 : 256; }
-bool g1_hilo(int v) { return v == 3 || v == 4; }   // GEMM1 writes the hi/lo form
-bool g2_hilo(int v) { return v >= 4; }        // GEMM2 reads the hi/lo form
+int g1_tile_m(int v) { return v == 1 || v == 5 ? 16 : v == 2 ? 32 : 256; }
+bool g1_hilo(int v) { return v == 4; }        // GEMM1 writes the hi/lo form
+bool g2_hilo(int v) { return v == 5; }        // GEMM2 reads the hi/lo form
 
 // The plan of a GEMM1 / GEMM2 pair, false when they cannot run together.  GEMM1
 // variant 5 is variant 1 with the dispatch folded in (T <= 64): every workgroup of a
@@ -88,15 +87,14 @@ bool make_plan(int g1, int g2, int32_t T, Plan* p) {
         *p = {16, 0, 5, g2, false, false, true};
         return true;
     }
-    if (g1 < 1 || g1 > 4 || g2 < 1 || g2 > 5) return false;
+    if ((g1 != 1 && g1 != 2 && g1 != 4) || g2 < 1 || g2 > 5 || g2 == 4) return false;
     const int tm = g1_tile_m(g1);
     if (g1_hilo(g1) && !g2_hilo(g2)) return false;      // the fp16 GEMM2s need fp16 C
     if (g2 == 5) {                                       // the second list, 128-row tiles
-        if (tm != 16 && tm != 32 && tm != 256) return false;
         *p = {tm, 128, g1, g2, !g1_hilo(g1), false, false};
         return true;
     }
-    const int tm_g2 = g2 <= 2 ? 16 : g2 == 3 ? 32 : 128;
+    const int tm_g2 = g2 <= 2 ? 16 : 32;
     if (tm_g2 != tm) return false;
     *p = {tm, 0, g1, g2, g1_hilo(g1) != g2_hilo(g2), false, false};
     return true;

@@ -163,173 +163,17 @@ __device__ __forceinline__ void store_c_hilo(const v4f (&acc)[4][8], float* xch,
 }
 
 // ---------------------------------------------------------------------------
-// Prefill GEMM1 (many tokens per expert): MFMA-bound tiling.
-//
-// Workgroup tile: 128 gathered token rows x 256 weight rows (128 gate rows
-// n0..n0+127 and the matching 128 up rows 2048+n0..), i.e. 128 x 128 SwiGLU
-// outputs.  Wave w (2 x 2 arrangement) computes 64 tokens x (64 gate + 64 up) rows:
-// per K block 32 MFMA 16x16x128 (4 token blocks x 8 weight blocks) whose fresh
-// partials are scaled by sa[token] * sb[block] into fp32 accumulators.
-//
-// Operands travel HBM/L2 -> LDS with global_load_lds_dwordx4 (8 rows x 128 B per
-// instruction, each wave moving 32 token rows and 64 weight rows; token scales with
-// one global_load_lds_dword), into NS stages of 49 KB; rows keep 16-byte chunk c
-// at c ^ swz128(r) so ds_read_b128 in the MFMA layout is conflict-free.  One workgroup barrier per K block both publishes
-// the stage every wave waited for and frees the stage about to be refilled.
-// Work items (row tile, 128-column group) are grouped up to 4 row tiles of one
-// expert x all column groups (column-major inside a group, see grouped_item) and
-// each XCD takes a contiguous run of 32 items of a round: up to 4 row tiles x 8
-// column groups share one L2, so each token row block is fetched about twice
-// instead of 16 times and each weight block once per group.
-// ---------------------------------------------------------------------------
-template <int NS>
-__global__ __launch_bounds__(256) void gemm1_prefill_kernel(
-    const uint8_t* __restrict__ hidden, TokenScales sa, int T,
-    const uint8_t* __restrict__ w1, const float* __restrict__ s1,
-    const int4* __restrict__ tiles, const int* __restrict__ num_tiles,
-    const int* __restrict__ exp_off, const int* __restrict__ sorted_tok, Intermediate C) {
-    constexpr int BM = 128;                     // token rows per tile
-    constexpr int NG = kI / 128;                // 16 column groups
-    constexpr int kA = BM * kBlk;               // 16 KB token stage
-    constexpr int kW = 256 * kBlk;              // 32 KB weight stage
-    constexpr int kStage = kA + kW + 4 * 256;   // + per-wave token-scale rows
-    constexpr int kVm = 13;                     // per K block: 4 + 8 + 1 DMA
-    static_assert((NS - 1) * kVm < 64, "ring too deep for vmcnt");
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * kStage];
-
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    const int r16 = lane & 15, kq = lane >> 4;
-    const int wm = wave >> 1, wn = wave & 1;   // token half, weight half
-    const v4f zero = {0.f, 0.f, 0.f, 0.f};
-    const int nitems = (*num_tiles) * NG;
-
-    // XCD-aware mapping: round r covers items [r*G, (r+1)*G); XCD x = blockIdx % 8
-    // takes the contiguous slice x*(G/8) .. of that round.
-    const int G = gridDim.x;
-    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, per = G >> 3;
-
-    const int drow = lane >> 3, dchunk = lane & 7;
-    const int swz = swz128(r16);
-    const int c0 = ((2 * kq) ^ swz) << 4, c1 = ((2 * kq + 1) ^ swz) << 4;
-
-    for (int round = 0; round * G < nitems; ++round) {
-        const int item = round * G + xcd * per + slot;
-        if (item >= nitems) continue;            // uniform per workgroup
-        int tix, ng;
-        grouped_item<BM>(item, NG, tiles, exp_off, tix, ng);
-        const int4 tile = tiles[tix];
-        const int le = tile.x, row0 = tile.y, nrows = tile.z;
-
-        // DMA sources: wave w moves token rows 32w..32w+31 and weight rows
-        // 64w..64w+63 of the stage (rows 0-127 gate, 128-255 up)
-        const uint8_t* asrc[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = 32 * wave + 8 * i + drow;
-            const int tok = sorted_tok[row0 + min(r, nrows - 1)];
-            asrc[i] = hidden + (size_t)tok * kH + ((dchunk ^ swz128(r)) << 4);
-        }
-        const uint8_t* wsrc[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int r = 64 * wave + 8 * i + drow;          // 0..255
-            const int n = (r < 128) ? ng * 128 + r : kI + ng * 128 + (r - 128);
-            wsrc[i] = w1 + (size_t)(le * kN1 + n) * kH + ((dchunk ^ swz128(r)) << 4);
-        }
-        // token scales: lane l of wave w fetches the scale of row 64*wm + l
-        const int srow = row0 + min(64 * wm + lane, nrows - 1);
-        const float* sap = sa.p + (sa.by_row ? srow : sorted_tok[srow]);
-        const float* sgp = s1 + (size_t)(le * kN1B + ng) * kHB;
-        const float* sup = sgp + (size_t)kIB * kHB;
-
-        auto issue = [&](int kb) {
-            uint8_t* st = lds + (kb % NS) * kStage;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) dma16(asrc[i] + kb * kBlk, st + (32 * wave + 8 * i) * kBlk);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) dma16(wsrc[i] + kb * kBlk, st + kA + (64 * wave + 8 * i) * kBlk);
-            dma4(sap + (size_t)kb * sa.stride, st + kA + kW + wave * 256);
-        };
-
-        v4f acc[4][8];
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) acc[s][j] = zero;
-
-        __syncthreads();   // previous item's reads of the ring are finished
-#pragma unroll
-        for (int kb = 0; kb < NS - 1; ++kb) {
-            issue(kb);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        // 16-row token blocks of this wave that exist: padding blocks skip their MFMAs
-        auto kloop = [&](auto live) {
-        constexpr int NLIVE = decltype(live)::value;
-#pragma unroll 1
-        for (int kb = 0; kb < kHB; ++kb) {
-            // wait for this wave's part of stage kb (younger stages stay in flight)
-            if (kb + NS - 1 <= kHB) {
-                static_assert(NS >= 2, "");
-                __builtin_amdgcn_s_waitcnt(vmcnt_imm((NS - 2) * kVm));
-            } else {
-                __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-            }
-            __syncthreads();
-            if (kb + NS - 1 < kHB) issue(kb + NS - 1);
-            __builtin_amdgcn_sched_barrier(0);
-
-            const uint8_t* st = lds + (kb % NS) * kStage;
-            const float fsg = sgp[kb], fsu = sup[kb];
-            if (NLIVE == 0) continue;
-            v8i bt[4];
-#pragma unroll
-            for (int s = 0; s < NLIVE; ++s) {
-                const uint8_t* rp = st + (64 * wm + 16 * s + r16) * kBlk;
-                const v4u x0 = *reinterpret_cast<const v4u*>(rp + c0);
-                const v4u x1 = *reinterpret_cast<const v4u*>(rp + c1);
-                bt[s] = v8i{(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
-            }
-            const float* sar = reinterpret_cast<const float*>(st + kA + kW + wave * 256);
-            float fs[4][2];
-#pragma unroll
-            for (int s = 0; s < NLIVE; ++s) {
-                const float sa = sar[16 * s + r16];
-                fs[s][0] = sa * fsg;
-                fs[s][1] = sa * fsu;
-            }
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                // weight block j: gate rows 64*wn + 16j (j < 4) or up rows (j >= 4)
-                const int r = (j < 4) ? (64 * wn + 16 * j) : (128 + 64 * wn + 16 * (j - 4));
-                const uint8_t* rp = st + kA + (r + r16) * kBlk;
-                const v4u x0 = *reinterpret_cast<const v4u*>(rp + c0);
-                const v4u x1 = *reinterpret_cast<const v4u*>(rp + c1);
-                const v8i bw = {(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
-#pragma unroll
-                for (int s = 0; s < NLIVE; ++s) {
-                    const v4f t = mfma_fp8(bw, bt[s], zero);
-                    const float f = fs[s][j >> 2];
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) acc[s][j][v] = __builtin_fmaf(t[v], f, acc[s][j][v]);
-                }
-            }
-        }
-        };
-        with_live_blocks(live_blocks(64 * wm, nrows), kloop);
-
-        // epilogue: lane holds D[n = 4*kq + v][token = r16] of each 16 x 16 block
-        store_c_hilo(acc, reinterpret_cast<float*>(lds), wm, wn, kq, r16, row0, nrows, ng, C);
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Prefill GEMM1, 8-wave variant: workgroup tile 256 token rows x 256 weight rows
-// (128 gate + 128 up -> 128 SwiGLU columns), waves 4 (tokens) x 2 (weights), each
-// 64 tokens x (64 gate + 64 up) as in gemm1_prefill_kernel.  Two waves per SIMD
-// let one wave's scale FMAs and LDS reads run under the other's MFMAs; registers
-// stay <= 256 per lane for that.  Two 66 KB stages.
+// Prefill GEMM1 (many tokens per expert), MFMA-bound tiling: workgroup tile 256
+// gathered token rows x 256 weight rows (128 gate rows n0..n0+127 and the matching
+// 128 up rows 2048+n0.., i.e. 256 x 128 SwiGLU outputs), waves 4 (tokens) x 2
+// (weights), each 64 tokens x (64 gate + 64 up) rows: per K block 32 MFMA 16x16x128
+// (4 token blocks x 8 weight blocks) whose fresh partials are scaled by
+// sa[token] * sb[block] into fp32 accumulators.  Two waves per SIMD let one wave's
+// scale FMAs and LDS reads run under the other's MFMAs; registers stay <= 256 per
+// lane for that.  Two 66 KB stages; rows keep 16-byte chunk c at c ^ swz128(r), so
+// ds_read_b128 in the MFMA layout is conflict-free.  Padding row blocks skip their
+// MFMAs.  Items (row tile, 128-column group) follow grouped_item with an
+// XCD-contiguous mapping of each round.
 //
 // Operand DMA is buffer_load ... lds (addresses in SGPR resources, 32-bit lane
 // offsets, the K step in the scalar offset), issued in two bursts per K block:
@@ -572,10 +416,10 @@ bool launch_gemm1_dispatch(const int* topk_ids, const float* topk_w, int T, int 
 }
 
 // Variants (the tile height of the dispatch they expect, and the form of C they write):
-//   1  register-staged streaming, 1 row block per item    16-row tiles   fp16 + bf16
-//   2  register-staged, 2 row blocks x 2 column groups   32-row tiles   fp16 + bf16
-//   3  prefill, 4 waves, 128 x 256 workgroup tile        128-row tiles  fp8 hi/lo
+//   1  register-staged streaming, 1 row block per item    16-row tiles   fp16 (+ exponents)
+//   2  register-staged, 2 row blocks x 2 column groups   32-row tiles   fp16 (+ exponents)
 //   4  prefill, 8 waves, 256 x 256 workgroup tile        256-row tiles  fp8 hi/lo
+// (variant 5, the dispatch folded into variant 1, has its own launcher)
 bool launch_gemm1(int variant, const uint8_t* hidden, const TokenScales& sa, int T,
                   const uint8_t* w1, const float* s1, const int4* tiles, const int* num_tiles,
                   const int* exp_off, int max_tiles, const int* sorted_tok, const Intermediate& C,
@@ -592,10 +436,6 @@ bool launch_gemm1(int variant, const uint8_t* hidden, const TokenScales& sa, int
         case 2:
             hipLaunchKernelGGL((gemm1_rstream_kernel<2, 2, 2, true>), dim3(grid_for(mt * G / 2)), dim3(256), 0, stream,
                                hidden, sa, T, w1, s1, tiles, num_tiles, sorted_tok, C, c_wide);
-            return true;
-        case 3:
-            hipLaunchKernelGGL(gemm1_prefill_kernel<3>, dim3(prefill_grid), dim3(256), 0, stream,
-                               hidden, sa, T, w1, s1, tiles, num_tiles, exp_off, sorted_tok, C);
             return true;
         case 4:
             hipLaunchKernelGGL(gemm1_prefill8_kernel, dim3(prefill_grid), dim3(512), 0, stream,

@@ -297,11 +297,11 @@ __global__ void e4m3_to_f16_kernel(const uint32_t* __restrict__ in, uint2* __res
 static int grid_for2(long long work) { return (int)(work < 4096 ? work : 4096); }
 
 // Variants (the tile height of the dispatch they expect, and the form of C they read):
-//   1  register-staged streaming, 32 columns x 1 row block per wave      16-row   bf16
-//   2  register-staged streaming, 64 columns x 1 row block per wave      16-row   bf16
-//   3  register-staged streaming, 64 columns x 2 row blocks per wave     32-row   bf16
-//   4  prefill, 8 waves, 128 x 256 workgroup tile                        128-row  hi/lo
-//   5  the same kernel over the 128-row second tile list of a 256-row dispatch    hi/lo
+//   1  register-staged streaming, 32 columns x 1 row block per wave      16-row   fp16
+//   2  register-staged streaming, 64 columns x 1 row block per wave      16-row   fp16
+//   3  register-staged streaming, 64 columns x 2 row blocks per wave     32-row   fp16
+//   5  prefill, 8 waves, 128 x 256 workgroup tile, over the 128-row second tile list
+//      of the dispatch (whatever the first list's height)                         hi/lo
 bool launch_gemm2(int variant, const Intermediate& C, const uint8_t* w2, const float* s2,
                   const int4* tiles, const int* num_tiles, const int* exp_off, int max_tiles,
                   const ExpertRows& rows, hipStream_t stream) {
@@ -321,7 +321,6 @@ bool launch_gemm2(int variant, const Intermediate& C, const uint8_t* w2, const f
             hipLaunchKernelGGL((gemm2_rstream_kernel<3, 4, 4, 2>), dim3(grid_for2(mt * G / 4)), dim3(256), 0,
                                stream, C, flags, w2, s2, tiles, num_tiles, rows);
             return true;
-        case 4:
         case 5:
             hipLaunchKernelGGL(gemm2_prefill8_kernel, dim3(256), dim3(512), 0, stream, C, w2, s2, tiles,
                                num_tiles, exp_off, rows, flags + 1);

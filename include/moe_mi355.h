@@ -107,11 +107,11 @@ typedef struct moe_mi355_args {
  *   MOE_MI355_FLAG_FORCE_PLAN      run the GEMM1 / GEMM2 variant pair in bits 8-11 /
  *                                  12-15 (MOE_MI355_FLAGS_PLAN(g1, g2)); for tuning
  *                                  sweeps and tests.  GEMM1: 1 streaming 16-row tiles,
- *                                  2 streaming 32-row tiles, 3 prefill 128-row tiles,
- *                                  4 prefill 256-row tiles; GEMM2: 1, 2 streaming 16-row,
- *                                  3 streaming 32-row, 4 prefill 128-row, 5 prefill on a
- *                                  second list of 128-row tiles.  A pair that cannot run
- *                                  together gives MOE_ERR_BAD_FLAGS.
+ *                                  2 streaming 32-row tiles, 4 prefill 256-row tiles;
+ *                                  GEMM2: 1, 2 streaming 16-row, 3 streaming 32-row,
+ *                                  5 prefill on a second list of 128-row tiles.  A pair
+ *                                  that cannot run together, or an unknown variant,
+ *                                  gives MOE_ERR_BAD_FLAGS.
  *                                  GEMM1 variant 5 is variant 1 with the dispatch
  *                                  computed inside it (T <= 64, the default there; pairs
  *                                  with GEMM2 variants 1 and 2): bit-identical output,

@@ -180,10 +180,11 @@ def _fake_args(k, T=4):
     return a
 
 
-@pytest.mark.parametrize("g1,g2", [(4, 1), (3, 3), (1, 4), (2, 2), (0, 1), (5, 5), (3, 5)])
+@pytest.mark.parametrize("g1,g2", [(4, 1), (3, 3), (1, 4), (2, 2), (0, 1), (5, 5), (3, 5), (3, 4), (4, 4)])
 def test_forced_plan_that_cannot_run_is_an_error(lib, g1, g2):
     """A GEMM pair that cannot run together (GEMM1 writes hi/lo C but GEMM2 reads fp16,
-    mismatched tile heights, unknown variants) is rejected before any launch with
+    mismatched tile heights, unknown variants: GEMM1 3 and GEMM2 4, the 128-row prefill
+    pair of earlier builds, are gone) is rejected before any launch with
     MOE_ERR_BAD_FLAGS, and the Python entry turns the status into a RuntimeError."""
     k = pkg("kernel")
     a = _fake_args(k)
