@@ -265,13 +265,38 @@ __global__ __launch_bounds__(512, 1) void gemm2_prefill8_kernel(
         with_live_blocks(live_blocks(64 * wm, cur.nrows), kloop);
 
         // lane holds D[h = 64 wn + 16 n + 4 kq + v][row = 64 wm + 16 s + r16]
+        float mx = 0.f;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const int rr = 64 * wm + 16 * s + r16;
+        for (int s = 0; s < 4; ++s)
 #pragma unroll
             for (int n = 0; n < 4; ++n)
-                store_rows4(rows, rows_wide, cur.row0 + rr, cur.hg * 256 + 64 * wn + 16 * n + 4 * kq, acc[s][n],
-                            rr < cur.nrows);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) mx = fmaxf(mx, fabsf(acc[s][n][v]));
+        if (!beyond_f16_in_wave(mx)) {
+            // the usual case: plain fp16, and the 4 zero exponents of a row's 64 columns
+            // as one 4-byte store (lane kq = 0 of the row)
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const int rr = 64 * wm + 16 * s + r16;
+                if (rr >= cur.nrows) continue;
+                const size_t row = (size_t)(cur.row0 + rr);
+                const int c0 = cur.hg * 256 + 64 * wn;
+#pragma unroll
+                for (int n = 0; n < 4; ++n) {
+                    const float x[4] = {acc[s][n][0], acc[s][n][1], acc[s][n][2], acc[s][n][3]};
+                    store_f16x4_scaled(rows.f16 + row * kH + c0 + 16 * n + 4 * kq, x, 0);
+                }
+                if (kq == 0) *reinterpret_cast<uint32_t*>(rows.exp + row * (kH / kGroup16) + c0 / kGroup16) = 0u;
+            }
+        } else {
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const int rr = 64 * wm + 16 * s + r16;
+#pragma unroll
+                for (int n = 0; n < 4; ++n)
+                    store_rows4(rows, rows_wide, cur.row0 + rr, cur.hg * 256 + 64 * wn + 16 * n + 4 * kq,
+                                acc[s][n], rr < cur.nrows);
+            }
         }
         cur = nxt;
     }
