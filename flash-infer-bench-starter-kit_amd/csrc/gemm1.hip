@@ -110,6 +110,10 @@ __global__ __launch_bounds__(256) void gemm1_rstream_dispatch_kernel(
 // through LDS (xch, 2 KB, reusing the operand ring: every wave must have left the
 // K loop, hence the first barrier).  Per row: s = amax/448 (1 for an all-zero row),
 // hi = e4m3(c * 448/amax), lo = e4m3((c - hi*s) * 16*448/amax).
+// A lane's 4 bytes of a row in each of the 4 column blocks are transposed across the
+// row's 4 lanes (lanes l, l+16, l+32, l+48) with v_permlane32_swap / v_permlane16_swap,
+// after which lane kq holds 16 consecutive bytes: one 16-byte store per form and row
+// block instead of four 4-byte ones, each row's 64 bytes written by one instruction.
 __device__ __forceinline__ void store_c_hilo(const v4f (&acc)[4][8], float* xch, int wm, int wn,
                                              int kq, int r16, int row0, int nrows, int ng,
                                              const Intermediate& C) {
@@ -134,30 +138,47 @@ __device__ __forceinline__ void store_c_hilo(const v4f (&acc)[4][8], float* xch,
         for (int s = 0; s < 4; ++s) xch[(wm * 2 + wn) * 64 + 16 * s + r16] = m[s];
     }
     __syncthreads();
+    // 4 x 4 transpose of 32-bit words over the 16-lane rows of the wave (word j of row kq
+    // -> word kq of row j): 32-lane then 16-lane swaps
+    auto transpose4 = [](uint32_t (&w)[4]) {
+        auto p = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
+        w[0] = p[0]; w[2] = p[1];
+        p = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
+        w[1] = p[0]; w[3] = p[1];
+        p = __builtin_amdgcn_permlane16_swap(w[0], w[1], false, false);
+        w[0] = p[0]; w[1] = p[1];
+        p = __builtin_amdgcn_permlane16_swap(w[2], w[3], false, false);
+        w[2] = p[0]; w[3] = p[1];
+    };
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
         const float amax = fmaxf(m[s], xch[(wm * 2 + (wn ^ 1)) * 64 + 16 * s + r16]);
         const int r = 64 * wm + 16 * s + r16;
-        if (r >= nrows) continue;
         const float sc = amax > 0.f ? amax / 448.f : 1.f;
         const float inv = amax > 0.f ? 448.f / amax : 1.f;
         const float inv16 = inv * 16.f;
-        const size_t off = (size_t)(row0 + r) * kI + ng * 128 + 64 * wn + 4 * kq;
+        uint32_t h[4], l[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const float* x = c[s][j];
-            const uint32_t h = e4m3x4_from_f32(clamp448(x[0] * inv), clamp448(x[1] * inv),
-                                               clamp448(x[2] * inv), clamp448(x[3] * inv));
-            const auto h01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)h, false);
-            const auto h23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)h, true);
+            h[j] = e4m3x4_from_f32(clamp448(x[0] * inv), clamp448(x[1] * inv),
+                                   clamp448(x[2] * inv), clamp448(x[3] * inv));
+            const auto h01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)h[j], false);
+            const auto h23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)h[j], true);
             const float hv[4] = {h01[0], h01[1], h23[0], h23[1]};
             float lq[4];
 #pragma unroll
             for (int v = 0; v < 4; ++v) lq[v] = clamp448(__builtin_fmaf(-hv[v], sc, x[v]) * inv16);
-            const uint32_t l = e4m3x4_from_f32(lq[0], lq[1], lq[2], lq[3]);
-            *reinterpret_cast<uint32_t*>(C.hi() + off + 16 * j) = h;
-            *reinterpret_cast<uint32_t*>(C.lo() + off + 16 * j) = l;
+            l[j] = e4m3x4_from_f32(lq[0], lq[1], lq[2], lq[3]);
         }
+        // every lane of the wave takes part in the swaps (the 4 lanes of a row share its
+        // validity); lane kq then holds bytes 16 kq .. 16 kq + 15 of the wave's 64
+        transpose4(h);
+        transpose4(l);
+        if (r >= nrows) continue;
+        const size_t off = (size_t)(row0 + r) * kI + ng * 128 + 64 * wn + 16 * kq;
+        *reinterpret_cast<v4u*>(C.hi() + off) = v4u{h[0], h[1], h[2], h[3]};
+        *reinterpret_cast<v4u*>(C.lo() + off) = v4u{l[0], l[1], l[2], l[3]};
         if (wn == 0 && kq == 0) C.scales[(size_t)ng * C.rows_cap + row0 + r] = sc;
     }
 }
