@@ -274,18 +274,44 @@ __global__ __launch_bounds__(512, 1) void gemm2_prefill8_kernel(
                 for (int v = 0; v < 4; ++v) mx = fmaxf(mx, fabsf(acc[s][n][v]));
         if (!beyond_f16_in_wave(mx)) {
             // the usual case: plain fp16, and the 4 zero exponents of a row's 64 columns
-            // as one 4-byte store (lane kq = 0 of the row)
+            // as one 4-byte store (lane kq = 0 of the row).  The fp16 pairs of column
+            // blocks (0, 1) and (2, 3) are exchanged across the row's 4 lanes (lanes l,
+            // l+16, l+32, l+48: a 32-lane then a 16-lane swap) so that lane kq holds
+            // columns 8 kq .. 8 kq + 7 of the pair: one 16-byte store writes 64
+            // consecutive bytes of the row.
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
                 const int rr = 64 * wm + 16 * s + r16;
-                if (rr >= cur.nrows) continue;
+                uint32_t w[4][2];
+#pragma unroll
+                for (int n = 0; n < 4; ++n)
+#pragma unroll
+                    for (int q = 0; q < 2; ++q)
+                        w[n][q] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)acc[s][n][2 * q]) |
+                                  ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)acc[s][n][2 * q + 1]) << 16);
+#pragma unroll
+                for (int pr = 0; pr < 2; ++pr) {
+                    const int a = 2 * pr, b = 2 * pr + 1;
+#pragma unroll
+                    for (int q = 0; q < 2; ++q) {
+                        const auto p = __builtin_amdgcn_permlane32_swap(w[a][q], w[b][q], false, false);
+                        w[a][q] = p[0];
+                        w[b][q] = p[1];
+                    }
+#pragma unroll
+                    for (int q = 0; q < 2; ++q) {
+                        const auto p = __builtin_amdgcn_permlane16_swap(w[a][q], w[b][q], false, false);
+                        w[a][q] = p[0];
+                        w[b][q] = p[1];
+                    }
+                }
+                if (rr >= cur.nrows) continue;   // after the swaps: every lane takes part
                 const size_t row = (size_t)(cur.row0 + rr);
                 const int c0 = cur.hg * 256 + 64 * wn;
 #pragma unroll
-                for (int n = 0; n < 4; ++n) {
-                    const float x[4] = {acc[s][n][0], acc[s][n][1], acc[s][n][2], acc[s][n][3]};
-                    store_f16x4_scaled(rows.f16 + row * kH + c0 + 16 * n + 4 * kq, x, 0);
-                }
+                for (int pr = 0; pr < 2; ++pr)
+                    *reinterpret_cast<v4u*>(rows.f16 + row * kH + c0 + 32 * pr + 8 * kq) =
+                        v4u{w[2 * pr][0], w[2 * pr][1], w[2 * pr + 1][0], w[2 * pr + 1][1]};
                 if (kq == 0) *reinterpret_cast<uint32_t*>(rows.exp + row * (kH / kGroup16) + c0 / kGroup16) = 0u;
             }
         } else {
