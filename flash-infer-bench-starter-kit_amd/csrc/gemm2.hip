@@ -66,8 +66,10 @@ __global__ __launch_bounds__(256) void gemm2_rstream_kernel(
 // Workgroup tile: 128 C rows x 256 output columns; waves 2 (rows) x 4 (columns),
 // each 64 rows x 64 columns, inside one W2 row block (one W2 scale per K block).
 // Stage (two, 64.5 KB each): C hi rows 16 KB | C lo rows 16 KB | W2 rows 32 KB |
-// C row scales 512 B, all by buffer_load ... lds in two bursts per K block (C after
-// the barrier, W2 after the second column block's MFMAs); rows keep 16-byte chunk c
+// C row scales 512 B, all by buffer_load ... lds in two bursts per K block (C right
+// after the barrier, W2 once this K block's operand reads are under way, ahead of its
+// first MFMAs; issuing W2 after the second column block's MFMAs was 4% slower at
+// T = 8192); rows keep 16-byte chunk c
 // at c ^ swz128(r).  Items (128-row piece, 256-column group) are grouped up to 4
 // pieces of one expert x all column groups with an XCD-contiguous mapping, as in
 // the prefill GEMM1.  A workgroup resolves the metadata of all its items at kernel
@@ -95,7 +97,7 @@ __global__ __launch_bounds__(512, 1) void gemm2_prefill8_kernel(
     constexpr int kC = BM * kBlk;               // 16 KB per C half
     constexpr int kW = 256 * kBlk;              // 32 KB of W2 rows
     constexpr int kStage = 2 * kC + kW + BM * 4;
-    constexpr int kWeightBurstAfter = 1;
+    constexpr int kWeightBurstAfter = 0;       // W2 burst in the first column block, before its MFMAs
     constexpr int kItemCap = 1024;              // per-workgroup item table (16 KB of LDS)
     static_assert(kIB % 2 == 0, "the next item's first stage must be stage 0");
     // one LDS object: the stages, then the item table
@@ -191,7 +193,7 @@ __global__ __launch_bounds__(512, 1) void gemm2_prefill8_kernel(
             __syncthreads();
             if (kb + 1 < kIB) {
                 issue_c(cur, kb + 1);
-                if (NLIVE == 0) issue_w(cur, kb + 1);
+                if (kWeightBurstAfter < 0 || NLIVE == 0) issue_w(cur, kb + 1);
             } else if (more) {
                 // stage 0 is free (every wave is past K block kIB - 2): the next item's first stage
                 nxt = make_item(r + 1);
