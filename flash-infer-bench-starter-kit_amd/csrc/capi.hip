@@ -57,13 +57,13 @@ constexpr int kMinTileM = 16;           // smallest row tile; sizes the tile lis
 // GEMM1's), an optional second list of 128-row tiles (GEMM2 variant 5), and whether the
 // fp16 C of a streaming GEMM1 is converted to the hi/lo form for a prefill GEMM2.
 // Small T streams weights with the register-staged kernels, C in fp16: 16-row tiles up
-// to T = 192 (GEMM2 with 32 output columns per wave up to T = 112, 64 beyond), 32-row
-// tiles (GEMM1 with two column groups per wave) beyond, where an expert gets up to
-// about 36 rows at T = 1152 and streams its weights about once.  From T = 705 the
-// streaming GEMM1 feeds the prefill GEMM2 (128-row tiles, FP8 MFMA on the hi/lo form),
-// the faster GEMM2 there; from T = 1537 both GEMMs are the MFMA-bound prefill kernels
-// on 256-row tiles (GEMM2 on the 128-row second list).  The boundaries come from
-// wall-clock sweeps of the pairs at T = 64 .. 2560 on MI355X.
+// to T = 88, 32-row tiles (GEMM1 with two column groups per wave, GEMM2 with two row
+// blocks per wave) beyond, where an expert gets up to about 36 rows at T = 1152 and
+// streams its weights about once.  From T = 433 the streaming GEMM1 feeds the prefill
+// GEMM2 (128-row tiles, FP8 MFMA on the hi/lo form), the faster GEMM2 there; from
+// T = 1089 both GEMMs are the MFMA-bound prefill kernels on 256-row tiles (GEMM2 on the
+// 128-row second list).  The boundaries come from wall-clock sweeps of the pairs at
+// T = 72 .. 2560 on MI355X over two routing seeds.
 struct Plan {
     int tm;        // tile height of the first list
     int tm2;       // tile height of the second list (0: none)
@@ -83,18 +83,18 @@ bool g2_hilo(int v) { return v == 5; }        // GEMM2 reads the hi/lo form
 // dispatch launch goes away.
 bool make_plan(int g1, int g2, int32_t T, Plan* p) {
     if (g1 == 5) {
-        if (g2 > 2 || T > moe::kDispatchInGemm1MaxT) return false;
+        if (g2 != 1 || T > moe::kDispatchInGemm1MaxT) return false;
         *p = {16, 0, 5, g2, false, false, true};
         return true;
     }
-    if ((g1 != 1 && g1 != 2 && g1 != 4) || g2 < 1 || g2 > 5 || g2 == 4) return false;
+    if ((g1 != 1 && g1 != 2 && g1 != 4) || (g2 != 1 && g2 != 3 && g2 != 5)) return false;
     const int tm = g1_tile_m(g1);
     if (g1_hilo(g1) && !g2_hilo(g2)) return false;      // the fp16 GEMM2s need fp16 C
     if (g2 == 5) {                                       // the second list, 128-row tiles
         *p = {tm, 128, g1, g2, !g1_hilo(g1), false, false};
         return true;
     }
-    const int tm_g2 = g2 <= 2 ? 16 : 32;
+    const int tm_g2 = g2 == 1 ? 16 : 32;
     if (tm_g2 != tm) return false;
     *p = {tm, 0, g1, g2, g1_hilo(g1) != g2_hilo(g2), false, false};
     return true;
@@ -117,10 +117,9 @@ int plan_for(int32_t T, int32_t flags, Plan* p) {
     // GEMM1 with the dispatch folded in reads the token scales by token: asking for the
     // gathered ones selects the separate dispatch there
     if (T <= moe::kDispatchInGemm1MaxT && !on) g1 = 5, g2 = 1;
-    else if (T <= 112) g1 = 1, g2 = 1;
-    else if (T <= 192) g1 = 1, g2 = 2;
-    else if (T <= 704) g1 = 2, g2 = 3;
-    else if (T <= 1536) g1 = 2, g2 = 5;
+    else if (T <= 88) g1 = 1, g2 = 1;
+    else if (T <= 432) g1 = 2, g2 = 3;
+    else if (T <= 1088) g1 = 2, g2 = 5;
     else g1 = 4, g2 = 5;
     if (flags & MOE_MI355_FLAG_FORCE_PLAN) {
         g1 = MOE_MI355_FLAGS_G1(flags);

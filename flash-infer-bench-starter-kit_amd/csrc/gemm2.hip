@@ -351,7 +351,6 @@ static int grid_for2(long long work) { return (int)(work < 4096 ? work : 4096); 
 
 // Variants (the tile height of the dispatch they expect, and the form of C they read):
 //   1  register-staged streaming, 32 columns x 1 row block per wave      16-row   fp16
-//   2  register-staged streaming, 64 columns x 1 row block per wave      16-row   fp16
 //   3  register-staged streaming, 64 columns x 2 row blocks per wave     32-row   fp16
 //   5  prefill, 8 waves, 128 x 256 workgroup tile, over the 128-row second tile list
 //      of the dispatch (whatever the first list's height)                         hi/lo
@@ -364,10 +363,6 @@ bool launch_gemm2(int variant, const Intermediate& C, const uint8_t* w2, const f
     switch (variant) {
         case 1:
             hipLaunchKernelGGL((gemm2_rstream_kernel<4, 4, 2, 1>), dim3(grid_for2(mt * G / 2)), dim3(256), 0,
-                               stream, C, flags, w2, s2, tiles, num_tiles, rows);
-            return true;
-        case 2:
-            hipLaunchKernelGGL((gemm2_rstream_kernel<3, 4, 4, 1>), dim3(grid_for2(mt * G / 4)), dim3(256), 0,
                                stream, C, flags, w2, s2, tiles, num_tiles, rows);
             return true;
         case 3:

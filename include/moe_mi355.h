@@ -108,13 +108,13 @@ typedef struct moe_mi355_args {
  *                                  12-15 (MOE_MI355_FLAGS_PLAN(g1, g2)); for tuning
  *                                  sweeps and tests.  GEMM1: 1 streaming 16-row tiles,
  *                                  2 streaming 32-row tiles, 4 prefill 256-row tiles;
- *                                  GEMM2: 1, 2 streaming 16-row, 3 streaming 32-row,
+ *                                  GEMM2: 1 streaming 16-row, 3 streaming 32-row,
  *                                  5 prefill on a second list of 128-row tiles.  A pair
  *                                  that cannot run together, or an unknown variant,
  *                                  gives MOE_ERR_BAD_FLAGS.
  *                                  GEMM1 variant 5 is variant 1 with the dispatch
  *                                  computed inside it (T <= 64, the default there; pairs
- *                                  with GEMM2 variants 1 and 2): bit-identical output,
+ *                                  with GEMM2 variant 1): bit-identical output,
  *                                  one launch fewer.
  *   MOE_MI355_FLAG_ROW_SCALES_ON / _OFF  GEMM1 reads the token scales gathered into row
  *                                  order / straight by token (default: gathered from

@@ -180,11 +180,12 @@ def _fake_args(k, T=4):
     return a
 
 
-@pytest.mark.parametrize("g1,g2", [(4, 1), (3, 3), (1, 4), (2, 2), (0, 1), (5, 5), (3, 5), (3, 4), (4, 4)])
+@pytest.mark.parametrize("g1,g2", [(4, 1), (3, 3), (1, 4), (2, 2), (0, 1), (5, 5), (3, 5), (3, 4), (4, 4),
+                                   (1, 2), (5, 2), (2, 6)])
 def test_forced_plan_that_cannot_run_is_an_error(lib, g1, g2):
     """A GEMM pair that cannot run together (GEMM1 writes hi/lo C but GEMM2 reads fp16,
-    mismatched tile heights, unknown variants: GEMM1 3 and GEMM2 4, the 128-row prefill
-    pair of earlier builds, are gone) is rejected before any launch with
+    mismatched tile heights, unknown variants: GEMM1 3, GEMM2 2 and 4, kernels of
+    earlier builds that no plan used, are gone) is rejected before any launch with
     MOE_ERR_BAD_FLAGS, and the Python entry turns the status into a RuntimeError."""
     k = pkg("kernel")
     a = _fake_args(k)
@@ -214,7 +215,7 @@ def test_layout_reports_the_forced_plan():
     # GEMM1 computes the dispatch itself up to T = 64, a dispatch launch from T = 65
     assert [k.workspace_layout(t).dispatch_in_gemm1 for t in (1, 8, 64, 65, 200, 9000)] == [1, 1, 1, 0, 0, 0]
     assert k.workspace_layout(64, k.plan_flags(1, 1)).dispatch_in_gemm1 == 0
-    assert k.workspace_layout(8, k.plan_flags(5, 2)).dispatch_in_gemm1 == 1
+    assert k.workspace_layout(8, k.plan_flags(5, 1)).dispatch_in_gemm1 == 1
     lay = k.WorkspaceLayout()
     lib = k._build_extension()
     assert lib.moe_mi355_get_workspace_layout(65, k.plan_flags(5, 1), ctypes.byref(lay)) == -7

@@ -18,8 +18,8 @@ def _bits(t):
     return t.view(torch.int16)
 
 
-@pytest.mark.parametrize("T,offset,g2", [(1, 0, 1), (5, 0, 1), (8, 0, 1), (13, 96, 2), (37, 224, 1),
-                                         (64, 0, 1), (64, 32, 2)])
+@pytest.mark.parametrize("T,offset,g2", [(1, 0, 1), (5, 0, 1), (8, 0, 1), (13, 96, 1), (37, 224, 1),
+                                         (64, 0, 1), (64, 32, 1)])
 def test_matches_separate_dispatch_bit_for_bit(T, offset, g2):
     k = pkg("kernel")
     d = first_tokens(config_inputs(3), T)
