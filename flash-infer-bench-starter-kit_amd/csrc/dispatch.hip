@@ -199,8 +199,8 @@ static void launch_dispatch_tm(const int* topk_ids, const float* topk_w, int T, 
 
 // chunk_cnt: int32 [ceil(T/256) * 32] scratch, needed when T > 1024.  tm2 > 0 (with
 // tiles2 / num_tiles2): a second tile list of tm2 rows over the same rows.  Tile
-// heights: tm in {16, 32, 64, 128, 256} alone, or the pairs (256, 128), (32, 128) and
-// (16, 128) the kernel plans use.
+// heights: tm in {16, 32, 64, 128, 256} alone, or the pairs (256, 128), (64, 128),
+// (32, 128) and (16, 128) the kernel plans use.
 bool launch_dispatch(const int* topk_ids, const float* topk_w, int T, int offset, int tm, int tm2,
                      int* exp_off, int* num_tiles, int4* tiles, int* sorted_tok,
                      float* sorted_w, int* inv, int* chunk_cnt, hipStream_t stream,
@@ -225,6 +225,7 @@ bool launch_dispatch(const int* topk_ids, const float* topk_w, int T, int offset
     switch (tm) {
         case 16: return run(IntC<16>{}, IntC<128>{});
         case 32: return run(IntC<32>{}, IntC<128>{});
+        case 64: return run(IntC<64>{}, IntC<128>{});
         case 256: return run(IntC<256>{}, IntC<128>{});
         default: return false;
     }

@@ -12,7 +12,8 @@
 // Kernels: register-staged weight streaming for small T (a work item is one row tile
 // of 16 or 32 rows x 16 gate + 16 up rows, its 56 K blocks split over the 4 waves of
 // a workgroup and reduced through LDS in a fixed order, so results do not depend on
-// scheduling), and MFMA-bound prefill kernels for large T (128- or 256-row tiles).
+// scheduling), the same streaming with a 64-row tile's token rows shared by the
+// workgroup for mid-size T, and MFMA-bound prefill kernels for large T (256-row tiles).
 //
 // MFMA: v_mfma_f32_16x16x128_f8f6f4 (e4m3 x e4m3), one instruction per 128-wide K
 // block, so the per-block scales multiply a fresh fp32 partial before it joins the
@@ -44,6 +45,206 @@ __global__ __launch_bounds__(256) void gemm1_rstream_kernel(
         gemm1_rstream_item<D, CB, NGRP, TL>(hidden, sa, w1, s1, tile.x, tile.y, tile.z,
                                             (work % S::kItems) * NGRP, sorted_tok, C, c_wide,
                                             slot_lds, red, wave);
+    }
+}
+
+// Streaming GEMM1 with the tile's token rows shared by the workgroup.  A work item is one
+// row tile of up to 64 rows x 16 NWV SwiGLU columns; each of the NWV waves streams its
+// own 16 gate + 16 up weight rows over all 56 K blocks through a register ring, as the
+// other streaming kernels do, while the token rows of a K block come once for the whole
+// workgroup by buffer_load ... lds into a ring of LDS stages (wave w moves rows
+// 64/NWV w .. 64/NWV (w + 1) - 1, wave 0 the 64 token scales).  With 8 waves the
+// workgroup requests 32 KB of weights and at most 8 KB of token rows per K block for
+// 64 x 128 outputs, where the 32-row kernel, whose waves split K and each load the
+// tile's rows, requests 12 KB for 32 x 32; and an expert of up to 64 rows streams its
+// weights once.  Each wave owns its columns over the whole K, so there is no cross-wave
+// reduction; one barrier per K block hands the token stage over.
+// D: register ring depth (K blocks of weights per wave); the token stages are one more,
+// so that the loads of block kb + D - 1 can go out before the barrier of block kb.
+template <int D, int NWV>
+struct Gemm1Shared {
+    static_assert(NWV == 4 || NWV == 8, "waves per workgroup");
+    static constexpr int kSlot = 32 * kBlk;                 // a wave's weight transpose slot
+    static constexpr int kTokStage = 64 * kBlk + 64 * 4;    // 64 token rows + their scales
+    static constexpr int kStages = D + 1;
+    static constexpr int kLds = NWV * kSlot + kStages * kTokStage;
+    static constexpr int kItems = kI / (16 * NWV);          // work items per tile
+    static constexpr int kRowsPerWave = 64 / NWV;           // token rows each wave moves
+};
+
+// Workgroup barrier that orders LDS only.  __syncthreads() is a release/acquire of all
+// memory at workgroup scope, which waits for every outstanding vector-memory load
+// (vmcnt(0)) and would drain the weight ring at every K block; here the caller has
+// already waited for its own LDS-DMA loads of the block the barrier hands over.
+__device__ __forceinline__ void lds_barrier() {
+    __asm__ volatile("" ::: "memory");   // no memory access moves across (compiler level)
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's LDS reads and writes are done
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    __asm__ volatile("" ::: "memory");
+}
+
+// vmcnt immediate for v = 0 .. 24 (uniform v; the switch keeps every wait an immediate)
+__device__ __forceinline__ void wait_vm_upto24(int v) {
+    switch (v) {
+#define MOE_WAIT_CASE(n) case n: __builtin_amdgcn_s_waitcnt(vmcnt_imm(n)); break;
+        MOE_WAIT_CASE(1) MOE_WAIT_CASE(2) MOE_WAIT_CASE(3) MOE_WAIT_CASE(4) MOE_WAIT_CASE(5)
+        MOE_WAIT_CASE(6) MOE_WAIT_CASE(7) MOE_WAIT_CASE(8) MOE_WAIT_CASE(9) MOE_WAIT_CASE(10)
+        MOE_WAIT_CASE(11) MOE_WAIT_CASE(12) MOE_WAIT_CASE(13) MOE_WAIT_CASE(14) MOE_WAIT_CASE(15)
+        MOE_WAIT_CASE(16) MOE_WAIT_CASE(17) MOE_WAIT_CASE(18) MOE_WAIT_CASE(19) MOE_WAIT_CASE(20)
+        MOE_WAIT_CASE(21) MOE_WAIT_CASE(22) MOE_WAIT_CASE(23) MOE_WAIT_CASE(24)
+#undef MOE_WAIT_CASE
+        default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
+    }
+}
+
+// One item of gemm1_shared_kernel with CB live 16-row blocks (the tile has 16 CB - 15 ..
+// 16 CB rows): wave `wave` computes SwiGLU columns 16 ng .. 16 ng + 15 of rows row0 ..
+// row0 + nrows - 1.
+template <int D, int NWV, int CB>
+__device__ __forceinline__ void gemm1_shared_item(
+    const uint8_t* __restrict__ hidden, const TokenScales& sa, __amdgpu_buffer_rsrc_t rs_h,
+    __amdgpu_buffer_rsrc_t rs_s, const uint8_t* __restrict__ w1, const float* __restrict__ s1,
+    int le, int row0, int nrows, int ng, const int* __restrict__ sorted_tok, const Intermediate& C,
+    int* __restrict__ c_wide, uint8_t* lds, int wave) {
+    using S = Gemm1Shared<D, NWV>;
+    static_assert(kHB % D == 0, "the K loop runs in steps of the ring depth");
+    const int lane = threadIdx.x & 63;
+    const int r16 = lane & 15, kq = lane >> 4;
+    const int drow = lane >> 3, dchunk = lane & 7;
+    const int swz = swz128(r16);
+    const int rd_g0 = r16 * kBlk + (((2 * kq) ^ swz) << 4);
+    const int rd_g1 = r16 * kBlk + (((2 * kq + 1) ^ swz) << 4);
+    const v4f zero = {0.f, 0.f, 0.f, 0.f};
+    uint8_t* const slot = lds + wave * S::kSlot;
+    uint8_t* const tok0 = lds + NWV * S::kSlot;
+
+    // weight rows of this wave: slot rows 0..15 gate rows of group ng, 16..31 its up rows,
+    // by buffer loads over the expert's W1 (32-bit offsets: one VGPR per load, the K block
+    // in the scalar offset)
+    const __amdgpu_buffer_rsrc_t rs_w = buffer_rsrc(w1 + (size_t)le * kN1 * kH, (uint32_t)kN1 * kH);
+    uint32_t woff[4];
+    int wr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = 8 * i + drow;
+        const int n = (r < 16) ? ng * 16 + r : kI + ng * 16 + (r - 16);
+        woff[i] = (uint32_t)n * kH + dchunk * 16;
+        wr[i] = r * kBlk + ((dchunk ^ swz128(r)) << 4);
+    }
+    // the NWV groups of a workgroup lie in one 128-column scale block
+    const float* sg = s1 + (size_t)(le * kN1B + (ng >> 3)) * kHB;
+    const float* su = sg + (size_t)kIB * kHB;
+    // token rows of this wave, 8 per instruction (clamped into the tile), for the live
+    // blocks: the stage rows of a live block are always written, so no stale row
+    // reaches an MFMA
+    constexpr int NT = S::kRowsPerWave / 8;
+    bool tlive[NT];
+    uint32_t toff[NT];
+    int ntok = 0;
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+        const int tr = S::kRowsPerWave * wave + 8 * i + drow;
+        tlive[i] = S::kRowsPerWave * wave + 8 * i < 16 * CB;
+        toff[i] = (uint32_t)sorted_tok[row0 + min(tr, nrows - 1)] * kH + ((dchunk ^ swz128(tr)) << 4);
+        ntok += tlive[i] ? 1 : 0;
+    }
+    const int sr = min(lane, nrows - 1);
+    const uint32_t soff = (uint32_t)(sa.by_row ? row0 + sr : sorted_tok[row0 + sr]) * 4;
+    const int nvm = 4 + ntok + (wave == 0 ? 1 : 0);   // loads per K block
+
+    // K block kb: weights in ring slot kb % D, token rows in stage kb % (D + 1)
+    v4u bw[D][4];
+    auto issue = [&](int kb, int ring) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)   // aux 2: nt, the weights are read once
+            bw[ring][i] = __builtin_amdgcn_raw_buffer_load_b128(rs_w, woff[i], (uint32_t)kb * kBlk, 2);
+        uint8_t* st = tok0 + (kb % S::kStages) * S::kTokStage;
+#pragma unroll
+        for (int i = 0; i < NT; ++i)
+            if (tlive[i]) bdma16(rs_h, toff[i], (uint32_t)kb * kBlk, st + (S::kRowsPerWave * wave + 8 * i) * kBlk);
+        if (wave == 0) bdma4(rs_s, soff, (uint32_t)kb * sa.stride * 4, st + 64 * kBlk);
+    };
+#pragma unroll
+    for (int k = 0; k < D - 1; ++k) issue(k, k);
+
+    v4f ag[CB], au[CB];
+#pragma unroll
+    for (int c = 0; c < CB; ++c) ag[c] = au[c] = zero;
+#pragma unroll 1
+    for (int kb0 = 0; kb0 < kHB; kb0 += D) {
+#pragma unroll
+        for (int j = 0; j < D; ++j) {
+            const int kb = kb0 + j;
+            // block kb + D - 1 goes to the ring slot block kb - 1 used (written to the LDS
+            // slot before) and to the stage of block kb - 2, which every wave finished
+            // reading before the barrier of block kb - 1
+            if (kb + D - 1 < kHB) issue(kb + D - 1, (j + D - 1) % D);
+            __builtin_amdgcn_sched_barrier(0);
+            // this wave's loads of block kb are in (those of the D - 1 blocks after it
+            // may stay in flight); after the barrier, every wave's (the token stage)
+            wait_vm_upto24(min(kHB - 1 - kb, D - 1) * nvm);
+            lds_barrier();
+#pragma unroll
+            for (int i = 0; i < 4; ++i) *reinterpret_cast<v4u*>(slot + wr[i]) = bw[j][i];
+            const uint8_t* st = tok0 + (kb % S::kStages) * S::kTokStage;
+            const float* ssc = reinterpret_cast<const float*>(st + 64 * kBlk);
+            const float wg = sg[kb], wu = su[kb];
+            const v4u g0 = *reinterpret_cast<const v4u*>(slot + rd_g0);
+            const v4u g1 = *reinterpret_cast<const v4u*>(slot + rd_g1);
+            const v4u u0 = *reinterpret_cast<const v4u*>(slot + 16 * kBlk + rd_g0);
+            const v4u u1 = *reinterpret_cast<const v4u*>(slot + 16 * kBlk + rd_g1);
+            const v8i bg = {(int)g0[0], (int)g0[1], (int)g0[2], (int)g0[3], (int)g1[0], (int)g1[1], (int)g1[2], (int)g1[3]};
+            const v8i bu = {(int)u0[0], (int)u0[1], (int)u0[2], (int)u0[3], (int)u1[0], (int)u1[1], (int)u1[2], (int)u1[3]};
+#pragma unroll
+            for (int c = 0; c < CB; ++c) {
+                __builtin_amdgcn_sched_barrier(0);   // one row block at a time: short live ranges
+                const uint8_t* ts = st + 16 * c * kBlk;
+                const v4u a0 = *reinterpret_cast<const v4u*>(ts + rd_g0);
+                const v4u a1 = *reinterpret_cast<const v4u*>(ts + rd_g1);
+                const v8i ba = {(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3], (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
+                const float sc = ssc[16 * c + r16];
+                const float fg = sc * wg, fu = sc * wu;
+                const v4f tg = mfma_fp8(bg, ba, zero);
+                const v4f tu = mfma_fp8(bu, ba, zero);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    ag[c][v] = __builtin_fmaf(tg[v], fg, ag[c][v]);
+                    au[c][v] = __builtin_fmaf(tu[v], fu, au[c][v]);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < CB; ++c)
+        store_swiglu4(C, c_wide, row0 + 16 * c + r16, ng * 16 + kq * 4, ag[c], au[c], 16 * c + r16 < nrows);
+}
+
+template <int D, int NWV>
+__global__ __launch_bounds__(64 * NWV) void gemm1_shared_kernel(
+    const uint8_t* __restrict__ hidden, TokenScales sa, int T,
+    const uint8_t* __restrict__ w1, const float* __restrict__ s1,
+    const int4* __restrict__ tiles, const int* __restrict__ num_tiles,
+    const int* __restrict__ sorted_tok, Intermediate C, int* __restrict__ c_wide) {
+    using S = Gemm1Shared<D, NWV>;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[S::kLds];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // token rows: T * 7168 < 2^32 (kMaxT); token scales: 56 x stride floats
+    const __amdgpu_buffer_rsrc_t rs_h = buffer_rsrc(hidden, (uint32_t)T * kH);
+    const __amdgpu_buffer_rsrc_t rs_s = buffer_rsrc(sa.p, (uint32_t)kHB * (uint32_t)sa.stride * 4);
+    const int nwork = (*num_tiles) * S::kItems;
+    for (int work = blockIdx.x; work < nwork; work += gridDim.x) {
+        const int4 tile = tiles[work / S::kItems];
+        const int ng = (work % S::kItems) * NWV + wave;
+        with_live_blocks(live_blocks(0, tile.z), [&](auto live) {
+            constexpr int CB = decltype(live)::value;
+            if constexpr (CB > 0)
+                gemm1_shared_item<D, NWV, CB>(hidden, sa, rs_h, rs_s, w1, s1, tile.x, tile.y, tile.z, ng,
+                                         sorted_tok, C, c_wide, lds, wave);
+        });
+        __syncthreads();   // the next item's first loads reuse the token stages
     }
 }
 
@@ -440,6 +641,7 @@ bool launch_gemm1_dispatch(const int* topk_ids, const float* topk_w, int T, int 
 //   1  register-staged streaming, 1 row block per item    16-row tiles   fp16 (+ exponents)
 //   2  register-staged, 2 row blocks x 2 column groups   32-row tiles   fp16 (+ exponents)
 //   4  prefill, 8 waves, 256 x 256 workgroup tile        256-row tiles  fp8 hi/lo
+//   7  register-staged weights, token rows shared in LDS  64-row tiles   fp16 (+ exponents)
 // (variant 5, the dispatch folded into variant 1, has its own launcher)
 bool launch_gemm1(int variant, const uint8_t* hidden, const TokenScales& sa, int T,
                   const uint8_t* w1, const float* s1, const int4* tiles, const int* num_tiles,
@@ -458,6 +660,12 @@ bool launch_gemm1(int variant, const uint8_t* hidden, const TokenScales& sa, int
             hipLaunchKernelGGL((gemm1_rstream_kernel<2, 2, 2, true>), dim3(grid_for(mt * G / 2)), dim3(256), 0, stream,
                                hidden, sa, T, w1, s1, tiles, num_tiles, sorted_tok, C, c_wide);
             return true;
+        case 7: {   // 4-wave workgroups, three resident per CU
+            const long long items = mt * Gemm1Shared<2, 4>::kItems;
+            hipLaunchKernelGGL((gemm1_shared_kernel<2, 4>), dim3((int)(items < 768 ? items : 768)), dim3(256), 0,
+                               stream, hidden, sa, T, w1, s1, tiles, num_tiles, sorted_tok, C, c_wide);
+            return true;
+        }
         case 4:
             hipLaunchKernelGGL(gemm1_prefill8_kernel, dim3(prefill_grid), dim3(512), 0, stream,
                                hidden, sa, T, w1, s1, tiles, num_tiles, exp_off, sorted_tok, C);

@@ -107,7 +107,9 @@ typedef struct moe_mi355_args {
  *   MOE_MI355_FLAG_FORCE_PLAN      run the GEMM1 / GEMM2 variant pair in bits 8-11 /
  *                                  12-15 (MOE_MI355_FLAGS_PLAN(g1, g2)); for tuning
  *                                  sweeps and tests.  GEMM1: 1 streaming 16-row tiles,
- *                                  2 streaming 32-row tiles, 4 prefill 256-row tiles;
+ *                                  2 streaming 32-row tiles, 4 prefill 256-row tiles,
+ *                                  7 streaming with shared token rows, 64-row tiles
+ *                                  (pairs with GEMM2 5 only);
  *                                  GEMM2: 1 streaming 16-row, 3 streaming 32-row,
  *                                  5 prefill on a second list of 128-row tiles.  A pair
  *                                  that cannot run together, or an unknown variant,

@@ -181,7 +181,7 @@ def _fake_args(k, T=4):
 
 
 @pytest.mark.parametrize("g1,g2", [(4, 1), (3, 3), (1, 4), (2, 2), (0, 1), (5, 5), (3, 5), (3, 4), (4, 4),
-                                   (1, 2), (5, 2), (2, 6)])
+                                   (1, 2), (5, 2), (2, 6), (7, 3), (7, 1), (8, 5)])
 def test_forced_plan_that_cannot_run_is_an_error(lib, g1, g2):
     """A GEMM pair that cannot run together (GEMM1 writes hi/lo C but GEMM2 reads fp16,
     mismatched tile heights, unknown variants: GEMM1 3, GEMM2 2 and 4, kernels of

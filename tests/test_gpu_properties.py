@@ -107,11 +107,11 @@ def test_small_odd_batches(T):
     assert st["frac_within"] == 1.0, st
 
 
-@pytest.mark.parametrize("T", [88, 89, 432, 433, 511, 512, 1024, 1025, 1088, 1089])
+@pytest.mark.parametrize("T", [88, 89, 432, 433, 511, 512, 576, 577, 1024, 1025, 1344, 1345])
 def test_plan_boundaries_match_oracle(T):
     """Token counts on both sides of every change of kernel plan (16-row streaming,
-    32-row streaming, 32-row streaming GEMM1 with the prefill GEMM2, 256-row prefill
-    tiles), of the token scales GEMM1 reads
+    32-row streaming, 32-row streaming GEMM1 with the prefill GEMM2, the token-sharing
+    GEMM1 on 64-row tiles, 256-row prefill tiles), of the token scales GEMM1 reads
     (by token, then gathered into row order from T = 512) and of the dispatch (one
     workgroup up to T = 1024, count and place kernels over 256-token chunks beyond)."""
     d = first_tokens(config_inputs(3), T)
@@ -125,7 +125,8 @@ def test_plan_boundaries_match_oracle(T):
 
 
 @pytest.mark.parametrize("T,g1,g2", [(64, 1, 1), (150, 1, 1), (64, 2, 3), (500, 2, 3),
-                                     (1000, 4, 5), (3000, 4, 5), (1500, 2, 5), (150, 1, 5)])
+                                     (1000, 4, 5), (3000, 4, 5), (1500, 2, 5), (150, 1, 5),
+                                     (1000, 7, 5), (300, 7, 5), (37, 7, 5), (2000, 7, 5)])
 def test_every_gemm_variant_matches_oracle(T, g1, g2):
     """Each GEMM1 / GEMM2 kernel variant (forced with the call's plan flags) stays
     within the tolerance."""
@@ -183,23 +184,25 @@ def test_row_order_token_scales_change_nothing(T):
     assert torch.equal(tab[:, :na], d["hidden_states_scale"][:, stok])
 
 
-@pytest.mark.parametrize("T", [64, 600, 2049])
-def test_all_local_routing_matches_oracle(T):
+@pytest.mark.parametrize("T,g1,g2", [(64, 0, 0), (600, 0, 0), (2049, 0, 0), (600, 7, 5)])
+def test_all_local_routing_matches_oracle(T, g1, g2):
     """Every token routed to 8 local experts (bias +3 on all 32 local experts, so group 0
     always wins and holds the whole top 8): N_a = 8T rows, the most the row-tile list
-    and the workspace are sized for, on a 16-row, a 32-row and a 256-row plan."""
+    and the workspace are sized for, on a 16-row, a 32-row and a 256-row plan, and with
+    the token-sharing GEMM1 forced (150 rows per expert: full and partial 64-row
+    tiles)."""
     k = pkg("kernel")
     wl = pkg("workloads")
     cfg = wl.Config("all_local", T, 0, hot_local_experts=tuple(range(32)), seed=20261111)
     d = dict(config_inputs(4))                   # offset 0: reuse its weights
     d.update(wl.make_activations(cfg, device="cuda"))
     d["output"] = torch.empty(T, 7168, dtype=torch.bfloat16, device="cuda")
-    note(f"[gpu] all-local routing T={T}")
+    note(f"[gpu] all-local routing T={T} g1={g1} g2={g2}")
     ids, w = k.route(d["routing_logits"], d["routing_bias"], d["routed_scaling_factor"])
     g = k.dispatch(ids, w, 0, 16)
     torch.cuda.synchronize()
     assert int(g["exp_off"][-1].item()) == 8 * T
-    out = run_forward(d)
+    out = run_forward(d, flags=k.plan_flags(g1, g2) if g1 else 0)
     rng = np.random.default_rng(T + 11)
     toks = sorted(rng.choice(T, min(T, 12), replace=False).tolist())
     st = compare_to_oracle(d, out, toks)
@@ -255,7 +258,7 @@ def _huge_inputs_check(d, c_flag, flags=0):
     k.forward(*wl.as_args({**d, "output": out2}), workspace=ws, flags=flags)
     torch.cuda.synchronize()
     assert _flags(ws, lay) == [0, 0]
-    ref = run_forward(d)
+    ref = run_forward(d, flags=flags)
     assert torch.equal(out2.view(torch.int16), ref.view(torch.int16))
 
 
@@ -282,6 +285,13 @@ def test_values_beyond_fp16_range_converted_plan():
     d = first_tokens(config_inputs(3), 1024)
     note("[gpu] values beyond the fp16 range, T=1024")
     _huge_inputs_check(d, c_flag=1)
+
+
+def test_values_beyond_fp16_range_token_sharing_gemm1():
+    """The same at T = 1024 with the token-sharing GEMM1 (64-row tiles) forced."""
+    d = first_tokens(config_inputs(3), 1024)
+    note("[gpu] values beyond the fp16 range, T=1024, GEMM1 variant 7")
+    _huge_inputs_check(d, c_flag=1, flags=pkg("kernel").plan_flags(7, 5))
 
 
 def test_values_beyond_fp16_range_prefill_plan():
