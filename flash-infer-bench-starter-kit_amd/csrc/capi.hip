@@ -101,7 +101,10 @@ bool make_plan(int g1, int g2, int32_t T, Plan* p) {
 }
 
 // GEMM1 reads the token scales gathered into row order (see gather_row_scales_kernel)
-// from T = kRowScalesMinT on; below, the gather costs more than it saves.
+// from T = kRowScalesMinT on; below, the gather costs more than it saves.  The
+// token-sharing GEMM1 (variant 7) moves a tile's 64 scales per K block with one gathering
+// DMA instruction either way, so it reads them by token and the gather launch goes away
+// (-1 us at T = 600 .. 1280).
 constexpr int32_t kRowScalesMinT = 512;
 constexpr int32_t kKnownFlags = MOE_MI355_FLAG_PROFILE | MOE_MI355_FLAG_FORCE_PLAN |
                                 MOE_MI355_FLAG_ROW_SCALES_ON | MOE_MI355_FLAG_ROW_SCALES_OFF |
@@ -130,7 +133,7 @@ int plan_for(int32_t T, int32_t flags, Plan* p) {
     }
     if (!make_plan(g1, g2, T, p)) return MOE_ERR_BAD_FLAGS;
     if (on && (off || p->dispatch_in_gemm1)) return MOE_ERR_BAD_FLAGS;
-    p->by_row = on ? true : off ? false : T >= kRowScalesMinT;
+    p->by_row = on ? true : off ? false : (T >= kRowScalesMinT && p->g1 != 7);
     return MOE_OK;
 }
 

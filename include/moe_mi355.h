@@ -120,7 +120,8 @@ typedef struct moe_mi355_args {
  *                                  one launch fewer.
  *   MOE_MI355_FLAG_ROW_SCALES_ON / _OFF  GEMM1 reads the token scales gathered into row
  *                                  order / straight by token (default: gathered from
- *                                  T = 512).  Bit-identical results either way.  GEMM1
+ *                                  T = 512, except under GEMM1 variant 7, which gathers
+ *                                  them itself).  Bit-identical results either way.  GEMM1
  *                                  variant 5 reads them by token: _ON selects the separate
  *                                  dispatch at T <= 64 (and is an error with variant 5
  *                                  forced).
