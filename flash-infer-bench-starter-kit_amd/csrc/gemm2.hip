@@ -187,10 +187,6 @@ __global__ __launch_bounds__(512, 1) void gemm2_prefill8_kernel(
         auto kloop = [&](auto live) {
         constexpr int NLIVE = decltype(live)::value;
         constexpr int NT = NLIVE > 0 ? NLIVE : 1;
-        // the W2 scale of a K block is loaded at the end of the block before (scalar loads
-        // complete out of order, so one still outstanding while the block's LDS reads return
-        // would make every LDS wait a full drain)
-        float sw_n = sbp[0];
 #pragma unroll 1
         for (int kb = 0; kb < kIB; ++kb) {
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
@@ -208,41 +204,30 @@ __global__ __launch_bounds__(512, 1) void gemm2_prefill8_kernel(
             if (NLIVE == 0) continue;
 
             const uint8_t* st = lds + (kb & 1) * kStage;
-            const float sw = sw_n;
+            const float sw = sbp[kb];
             const float* csr = reinterpret_cast<const float*>(st + 2 * kC + kW);
+            v8i ch[4], cl[4];
+            float f[4];
+#pragma unroll
+            for (int s = 0; s < NLIVE; ++s) {
+                const int rr = 64 * wm + 16 * s + r16;
+                const uint8_t* ph = st + rr * kBlk;
+                const uint8_t* pl = st + kC + rr * kBlk;
+                const v4u h0 = *reinterpret_cast<const v4u*>(ph + c0);
+                const v4u h1 = *reinterpret_cast<const v4u*>(ph + c1);
+                const v4u l0 = *reinterpret_cast<const v4u*>(pl + c0);
+                const v4u l1 = *reinterpret_cast<const v4u*>(pl + c1);
+                ch[s] = v8i{(int)h0[0], (int)h0[1], (int)h0[2], (int)h0[3], (int)h1[0], (int)h1[1], (int)h1[2], (int)h1[3]};
+                cl[s] = v8i{(int)l0[0], (int)l0[1], (int)l0[2], (int)l0[3], (int)l1[0], (int)l1[1], (int)l1[2], (int)l1[3]};
+                f[s] = csr[rr] * sw;
+            }
             auto read_w = [&](int n) {
                 const uint8_t* rp = st + 2 * kC + (64 * wn + 16 * n + r16) * kBlk;
                 const v4u x0 = *reinterpret_cast<const v4u*>(rp + c0);
                 const v4u x1 = *reinterpret_cast<const v4u*>(rp + c1);
                 return v8i{(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
             };
-            // the first MFMAs' operands first (W2 fragment 0 and the row scales, then the C hi
-            // fragments and the lo ones, in MFMA order): LDS reads complete in order, so the
-            // first MFMA waits for a few of them instead of all, and the rest overlap the MFMAs
             v8i w = read_w(0);
-            float f[4];
-#pragma unroll
-            for (int s = 0; s < NLIVE; ++s) f[s] = csr[64 * wm + 16 * s + r16];
-            __builtin_amdgcn_sched_barrier(0);
-            v8i ch[4], cl[4];
-#pragma unroll
-            for (int s = 0; s < NLIVE; ++s) {
-                const uint8_t* ph = st + (64 * wm + 16 * s + r16) * kBlk;
-                const v4u h0 = *reinterpret_cast<const v4u*>(ph + c0);
-                const v4u h1 = *reinterpret_cast<const v4u*>(ph + c1);
-                ch[s] = v8i{(int)h0[0], (int)h0[1], (int)h0[2], (int)h0[3], (int)h1[0], (int)h1[1], (int)h1[2], (int)h1[3]};
-            }
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int s = 0; s < NLIVE; ++s) {
-                const uint8_t* pl = st + kC + (64 * wm + 16 * s + r16) * kBlk;
-                const v4u l0 = *reinterpret_cast<const v4u*>(pl + c0);
-                const v4u l1 = *reinterpret_cast<const v4u*>(pl + c1);
-                cl[s] = v8i{(int)l0[0], (int)l0[1], (int)l0[2], (int)l0[3], (int)l1[0], (int)l1[1], (int)l1[2], (int)l1[3]};
-            }
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int s = 0; s < NLIVE; ++s) f[s] = f[s] * sw;
             v4f tp[NT];
 #pragma unroll
             for (int n = 0; n < 4; ++n) {
@@ -277,8 +262,6 @@ __global__ __launch_bounds__(512, 1) void gemm2_prefill8_kernel(
             for (int s = 0; s < NLIVE; ++s)
 #pragma unroll
                 for (int v = 0; v < 4; ++v) acc[s][3][v] = __builtin_fmaf(tp[s][v], f[s], acc[s][3][v]);
-            __builtin_amdgcn_sched_barrier(0);
-            if (kb + 1 < kIB) sw_n = sbp[kb + 1];
         }
         };
         with_live_blocks(live_blocks(64 * wm, cur.nrows), kloop);
