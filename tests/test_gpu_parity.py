@@ -59,7 +59,7 @@ def _route_both(lg: np.ndarray, bias: torch.Tensor, f: float):
     return ids.cpu().numpy(), w.cpu().numpy(), rids, rw
 
 
-@pytest.mark.parametrize("case", ["equal", "ties", "hot", "large", "odd_T", "one", "dup_max"])
+@pytest.mark.parametrize("case", ["equal", "ties", "hot", "large", "odd_T", "one", "dup_max", "extreme"])
 def test_route_edge_cases(case):
     rng = np.random.default_rng(42)
     zb = torch.zeros(256, dtype=torch.bfloat16)
@@ -83,6 +83,15 @@ def test_route_edge_cases(case):
     elif case == "one":
         lg = rng.standard_normal((1, 256)).astype(np.float32)
         b = zb
+    elif case == "extreme":
+        # logits at and beyond the +-700 clamp of the sigmoid's exp (exactly 0 / 1 there),
+        # up to +-inf, scattered over normal ones
+        lg = rng.standard_normal((16, 256)).astype(np.float32)
+        vals = np.array([700.0, -700.0, 699.9999, -699.9999, 700.0001, -700.0001, 701.0, -701.0, 1e4, -1e4,
+                         3e38, -3e38, np.inf, -np.inf, 88.0, -88.0, 104.0, -104.0], np.float32)
+        pos = rng.choice(256 * 16, 16 * 24, replace=False)
+        lg.reshape(-1)[pos] = vals[rng.integers(0, len(vals), len(pos))]
+        b = (torch.randn(256, generator=torch.Generator().manual_seed(3)) * 0.1).to(torch.bfloat16)
     else:
         lg = np.zeros((4, 256), np.float32)
         lg[:, 40] = lg[:, 41] = 2.0
