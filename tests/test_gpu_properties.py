@@ -159,6 +159,32 @@ def test_batch_sizes_between_plan_boundaries(T, offset):
     assert st["frac_within"] == 1.0, st
 
 
+_RNG_T = np.random.default_rng(20261202)
+_RANDOM_BATCHES = [(int(t), int(o)) for t, o in zip(_RNG_T.integers(1, 3000, 8),
+                                                    _RNG_T.choice([0, 32, 64, 96, 224], 8))]
+
+
+@pytest.mark.parametrize("T,offset", _RANDOM_BATCHES)
+def test_seeded_random_batches(T, offset):
+    """Seeded random token counts and offsets with their own activations and routing
+    logits (seed 1000 + T, not slices of a benchmark config) on config 3's weights:
+    sampled tokens match the oracle and a second call is bit-identical."""
+    wl = pkg("workloads")
+    cfg = wl.Config(f"random_t{T}", T, offset, seed=1000 + T)
+    d = dict(config_inputs(3))
+    d.update(wl.make_activations(cfg, device="cuda"))
+    d["local_expert_offset"] = offset
+    d["output"] = torch.empty(T, 7168, dtype=torch.bfloat16, device="cuda")
+    note(f"[gpu] random batch T={T} offset={offset}")
+    a = run_forward(d)
+    b = run_forward(d)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    toks = sorted(np.random.default_rng(T + 1).choice(T, min(T, 12), replace=False).tolist())
+    st = compare_to_oracle(d, a, toks)
+    note(f"[gpu] random T={T} offset={offset} stats {st}")
+    assert st["frac_within"] == 1.0, st
+
+
 @pytest.mark.parametrize("T", [64, 200, 1024, 3000])
 def test_row_order_token_scales_change_nothing(T):
     """GEMM1 reading the token scales gathered into row order (FLAG_ROW_SCALES_ON)
