@@ -58,12 +58,16 @@ constexpr int kMinTileM = 16;           // smallest row tile; sizes the tile lis
 // fp16 C of a streaming GEMM1 is converted to the hi/lo form for a prefill GEMM2.
 // Small T streams weights with the register-staged kernels, C in fp16: 16-row tiles up
 // to T = 88, 32-row tiles (GEMM1 with two column groups per wave, GEMM2 with two row
-// blocks per wave) beyond.  From T = 433 the streaming GEMM1 feeds the prefill GEMM2
-// (128-row tiles, FP8 MFMA on the hi/lo form), the faster GEMM2 there; from T = 577
-// GEMM1 is the token-sharing kernel on 64-row tiles (fewer requests per output once an
-// expert has dozens of rows); from T = 1345 both GEMMs are the MFMA-bound prefill
-// kernels on 256-row tiles (GEMM2 on the 128-row second list).  The boundaries come from
-// wall-clock sweeps of the pairs at T = 72 .. 2560 on MI355X over two routing seeds.
+// blocks per wave) beyond.  From T = 300 GEMM1 is the token-sharing kernel on 64-row
+// tiles (fewer requests per output once an expert has dozens of rows), feeding the
+// prefill GEMM2 (128-row tiles, FP8 MFMA on the hi/lo form): up to T = 960 with three
+// workgroups per CU (variant 8), then with two (variant 7), whose fewer resident
+// workgroups split the items of the larger tile lists into better-filled rounds; from
+// T = 1345 both GEMMs are the MFMA-bound prefill kernels on 256-row tiles (GEMM2 on the
+// 128-row second list).  The boundaries come from wall-clock sweeps of the pairs at
+// T = 72 .. 2560 on MI355X over three routing seeds (light, medium and heavy routing to
+// the local experts): between T = 960 and 1344 the best pair depends on the routing
+// (heavy routing prefers the prefill pair, light routing the token-sharing one).
 struct Plan {
     int tm;        // tile height of the first list
     int tm2;       // tile height of the second list (0: none)
@@ -73,7 +77,7 @@ struct Plan {
     bool dispatch_in_gemm1;   // GEMM1 variant 5 computes the dispatch itself (no launch)
 };
 
-int g1_tile_m(int v) { return v == 1 || v == 5 ? 16 : v == 2 ? 32 : v == 7 ? 64 : 256; }
+int g1_tile_m(int v) { return v == 1 || v == 5 ? 16 : v == 2 ? 32 : v == 7 || v == 8 ? 64 : 256; }
 bool g1_hilo(int v) { return v == 4; }        // GEMM1 writes the hi/lo form
 bool g2_hilo(int v) { return v == 5; }        // GEMM2 reads the hi/lo form
 
@@ -87,7 +91,7 @@ bool make_plan(int g1, int g2, int32_t T, Plan* p) {
         *p = {16, 0, 5, g2, false, false, true};
         return true;
     }
-    if ((g1 != 1 && g1 != 2 && g1 != 4 && g1 != 7) || (g2 != 1 && g2 != 3 && g2 != 5)) return false;
+    if ((g1 != 1 && g1 != 2 && g1 != 4 && g1 != 7 && g1 != 8) || (g2 != 1 && g2 != 3 && g2 != 5)) return false;
     const int tm = g1_tile_m(g1);
     if (g1_hilo(g1) && !g2_hilo(g2)) return false;      // the fp16 GEMM2s need fp16 C
     if (g2 == 5) {                                       // the second list, 128-row tiles
@@ -121,8 +125,8 @@ int plan_for(int32_t T, int32_t flags, Plan* p) {
     // gathered ones selects the separate dispatch there
     if (T <= moe::kDispatchInGemm1MaxT && !on) g1 = 5, g2 = 1;
     else if (T <= 88) g1 = 1, g2 = 1;
-    else if (T <= 432) g1 = 2, g2 = 3;
-    else if (T <= 576) g1 = 2, g2 = 5;
+    else if (T <= 299) g1 = 2, g2 = 3;
+    else if (T <= 960) g1 = 8, g2 = 5;
     else if (T <= 1344) g1 = 7, g2 = 5;
     else g1 = 4, g2 = 5;
     if (flags & MOE_MI355_FLAG_FORCE_PLAN) {
@@ -133,7 +137,7 @@ int plan_for(int32_t T, int32_t flags, Plan* p) {
     }
     if (!make_plan(g1, g2, T, p)) return MOE_ERR_BAD_FLAGS;
     if (on && (off || p->dispatch_in_gemm1)) return MOE_ERR_BAD_FLAGS;
-    p->by_row = on ? true : off ? false : (T >= kRowScalesMinT && p->g1 != 7);
+    p->by_row = on ? true : off ? false : (T >= kRowScalesMinT && p->g1 != 7 && p->g1 != 8);
     return MOE_OK;
 }
 

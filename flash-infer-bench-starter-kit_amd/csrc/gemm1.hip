@@ -222,8 +222,10 @@ __device__ __forceinline__ void gemm1_shared_item(
         store_swiglu4(C, c_wide, row0 + 16 * c + r16, ng * 16 + kq * 4, ag[c], au[c], 16 * c + r16 < nrows);
 }
 
-template <int D, int NWV>
-__global__ __launch_bounds__(64 * NWV) void gemm1_shared_kernel(
+// WPE: the waves per SIMD the register allocation is held to (1: the compiler's choice,
+// 172 registers, two workgroups per CU; 3: 153 registers, three).
+template <int D, int NWV, int WPE>
+__global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(WPE))) void gemm1_shared_kernel(
     const uint8_t* __restrict__ hidden, TokenScales sa, int T,
     const uint8_t* __restrict__ w1, const float* __restrict__ s1,
     const int4* __restrict__ tiles, const int* __restrict__ num_tiles,
@@ -642,6 +644,7 @@ bool launch_gemm1_dispatch(const int* topk_ids, const float* topk_w, int T, int 
 //   2  register-staged, 2 row blocks x 2 column groups   32-row tiles   fp16 (+ exponents)
 //   4  prefill, 8 waves, 256 x 256 workgroup tile        256-row tiles  fp8 hi/lo
 //   7  register-staged weights, token rows shared in LDS  64-row tiles   fp16 (+ exponents)
+//   8  variant 7 with three workgroups per CU (more loads in flight, more L2 pressure)
 // (variant 5, the dispatch folded into variant 1, has its own launcher)
 bool launch_gemm1(int variant, const uint8_t* hidden, const TokenScales& sa, int T,
                   const uint8_t* w1, const float* s1, const int4* tiles, const int* num_tiles,
@@ -660,9 +663,15 @@ bool launch_gemm1(int variant, const uint8_t* hidden, const TokenScales& sa, int
             hipLaunchKernelGGL((gemm1_rstream_kernel<2, 2, 2, true>), dim3(grid_for(mt * G / 2)), dim3(256), 0, stream,
                                hidden, sa, T, w1, s1, tiles, num_tiles, sorted_tok, C, c_wide);
             return true;
-        case 7: {   // 4-wave workgroups, three resident per CU
+        case 7: {   // 4-wave workgroups, two resident per CU (registers)
             const long long items = mt * Gemm1Shared<2, 4>::kItems;
-            hipLaunchKernelGGL((gemm1_shared_kernel<2, 4>), dim3((int)(items < 768 ? items : 768)), dim3(256), 0,
+            hipLaunchKernelGGL((gemm1_shared_kernel<2, 4, 1>), dim3((int)(items < 768 ? items : 768)), dim3(256), 0,
+                               stream, hidden, sa, T, w1, s1, tiles, num_tiles, sorted_tok, C, c_wide);
+            return true;
+        }
+        case 8: {   // the same held to three resident per CU
+            const long long items = mt * Gemm1Shared<2, 4>::kItems;
+            hipLaunchKernelGGL((gemm1_shared_kernel<2, 4, 3>), dim3((int)(items < 768 ? items : 768)), dim3(256), 0,
                                stream, hidden, sa, T, w1, s1, tiles, num_tiles, sorted_tok, C, c_wide);
             return true;
         }

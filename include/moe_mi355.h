@@ -109,7 +109,8 @@ typedef struct moe_mi355_args {
  *                                  sweeps and tests.  GEMM1: 1 streaming 16-row tiles,
  *                                  2 streaming 32-row tiles, 4 prefill 256-row tiles,
  *                                  7 streaming with shared token rows, 64-row tiles
- *                                  (pairs with GEMM2 5 only);
+ *                                  (pairs with GEMM2 5 only), 8 the same with three
+ *                                  workgroups per CU instead of two;
  *                                  GEMM2: 1 streaming 16-row, 3 streaming 32-row,
  *                                  5 prefill on a second list of 128-row tiles.  A pair
  *                                  that cannot run together, or an unknown variant,
@@ -120,7 +121,7 @@ typedef struct moe_mi355_args {
  *                                  one launch fewer.
  *   MOE_MI355_FLAG_ROW_SCALES_ON / _OFF  GEMM1 reads the token scales gathered into row
  *                                  order / straight by token (default: gathered from
- *                                  T = 512, except under GEMM1 variant 7, which gathers
+ *                                  T = 512, except under GEMM1 variants 7 and 8, which gather
  *                                  them itself).  Bit-identical results either way.  GEMM1
  *                                  variant 5 reads them by token: _ON selects the separate
  *                                  dispatch at T <= 64 (and is an error with variant 5

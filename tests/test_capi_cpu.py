@@ -181,7 +181,7 @@ def _fake_args(k, T=4):
 
 
 @pytest.mark.parametrize("g1,g2", [(4, 1), (3, 3), (1, 4), (2, 2), (0, 1), (5, 5), (3, 5), (3, 4), (4, 4),
-                                   (1, 2), (5, 2), (2, 6), (7, 3), (7, 1), (8, 5)])
+                                   (1, 2), (5, 2), (2, 6), (7, 3), (7, 1), (9, 5), (8, 1), (8, 3)])
 def test_forced_plan_that_cannot_run_is_an_error(lib, g1, g2):
     """A GEMM pair that cannot run together (GEMM1 writes hi/lo C but GEMM2 reads fp16,
     mismatched tile heights, unknown variants: GEMM1 3, GEMM2 2 and 4, kernels of
@@ -212,6 +212,11 @@ def test_unknown_flag_bits_are_an_error(lib, flags):
 def test_layout_reports_the_forced_plan():
     k = pkg("kernel")
     assert k.workspace_layout(64).tile_m == 16 and k.workspace_layout(64).intermediate_format == 0
+    # 32-row streaming tiles up to T = 299, then the token-sharing GEMM1 on 64-row tiles
+    # (C converted to the hi/lo form for the prefill GEMM2), then 256-row prefill tiles
+    assert [k.workspace_layout(t).tile_m for t in (89, 299, 300, 960, 961, 1344, 1345)] == \
+        [32, 32, 64, 64, 64, 64, 256]
+    assert [k.workspace_layout(t).intermediate_format for t in (299, 300, 1344, 1345)] == [0, 2, 2, 1]
     # GEMM1 computes the dispatch itself up to T = 64, a dispatch launch from T = 65
     assert [k.workspace_layout(t).dispatch_in_gemm1 for t in (1, 8, 64, 65, 200, 9000)] == [1, 1, 1, 0, 0, 0]
     assert k.workspace_layout(64, k.plan_flags(1, 1)).dispatch_in_gemm1 == 0

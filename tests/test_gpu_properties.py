@@ -107,13 +107,13 @@ def test_small_odd_batches(T):
     assert st["frac_within"] == 1.0, st
 
 
-@pytest.mark.parametrize("T", [88, 89, 432, 433, 511, 512, 576, 577, 1024, 1025, 1344, 1345])
+@pytest.mark.parametrize("T", [88, 89, 299, 300, 960, 961, 1024, 1025, 1344, 1345])
 def test_plan_boundaries_match_oracle(T):
     """Token counts on both sides of every change of kernel plan (16-row streaming,
-    32-row streaming, 32-row streaming GEMM1 with the prefill GEMM2, the token-sharing
-    GEMM1 on 64-row tiles, 256-row prefill tiles), of the token scales GEMM1 reads
-    (by token, then gathered into row order from T = 512) and of the dispatch (one
-    workgroup up to T = 1024, count and place kernels over 256-token chunks beyond)."""
+    32-row streaming, the token-sharing GEMM1 on 64-row tiles with three and then two
+    workgroups per CU feeding the prefill GEMM2, 256-row prefill tiles) and of the
+    dispatch (one workgroup up to T = 1024, count and place kernels over 256-token
+    chunks beyond)."""
     d = first_tokens(config_inputs(3), T)
     note(f"[gpu] plan boundary T={T}")
     out = run_forward(d)
@@ -126,7 +126,8 @@ def test_plan_boundaries_match_oracle(T):
 
 @pytest.mark.parametrize("T,g1,g2", [(64, 1, 1), (150, 1, 1), (64, 2, 3), (500, 2, 3),
                                      (1000, 4, 5), (3000, 4, 5), (1500, 2, 5), (150, 1, 5),
-                                     (1000, 7, 5), (300, 7, 5), (37, 7, 5), (2000, 7, 5)])
+                                     (1000, 7, 5), (300, 7, 5), (37, 7, 5), (2000, 7, 5),
+                                     (600, 8, 5), (150, 8, 5), (1500, 8, 5), (500, 2, 5)])
 def test_every_gemm_variant_matches_oracle(T, g1, g2):
     """Each GEMM1 / GEMM2 kernel variant (forced with the call's plan flags) stays
     within the tolerance."""
@@ -210,13 +211,13 @@ def test_row_order_token_scales_change_nothing(T):
     assert torch.equal(tab[:, :na], d["hidden_states_scale"][:, stok])
 
 
-@pytest.mark.parametrize("T,g1,g2", [(64, 0, 0), (600, 0, 0), (2049, 0, 0), (600, 7, 5)])
+@pytest.mark.parametrize("T,g1,g2", [(64, 0, 0), (600, 0, 0), (2049, 0, 0), (600, 7, 5), (1100, 0, 0)])
 def test_all_local_routing_matches_oracle(T, g1, g2):
     """Every token routed to 8 local experts (bias +3 on all 32 local experts, so group 0
     always wins and holds the whole top 8): N_a = 8T rows, the most the row-tile list
-    and the workspace are sized for, on a 16-row, a 32-row and a 256-row plan, and with
-    the token-sharing GEMM1 forced (150 rows per expert: full and partial 64-row
-    tiles)."""
+    and the workspace are sized for, on the 16-row plan, the 64-row token-sharing plans
+    (three workgroups per CU at T = 600, two at T = 1100, and two forced at T = 600:
+    150 rows per expert, full and partial 64-row tiles) and the 256-row plan."""
     k = pkg("kernel")
     wl = pkg("workloads")
     cfg = wl.Config("all_local", T, 0, hot_local_experts=tuple(range(32)), seed=20261111)
@@ -310,6 +311,13 @@ def test_values_beyond_fp16_range_converted_plan():
     range."""
     d = first_tokens(config_inputs(3), 1024)
     note("[gpu] values beyond the fp16 range, T=1024")
+    _huge_inputs_check(d, c_flag=1)
+
+
+def test_values_beyond_fp16_range_token_sharing_three_per_cu():
+    """T = 600 (the token-sharing GEMM1 at three workgroups per CU, the plan there)."""
+    d = first_tokens(config_inputs(3), 600)
+    note("[gpu] values beyond the fp16 range, T=600, GEMM1 variant 8")
     _huge_inputs_check(d, c_flag=1)
 
 
