@@ -44,7 +44,13 @@ __global__ __launch_bounds__(64 * kQuantRows) void quantize_fp8_blockwise_kernel
     float* __restrict__ scales) {
     __shared__ float sc[kQuantMaxCols / 128][kQuantRows];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int row0 = blockIdx.x * kQuantRows;
+    // workgroup b takes row group (b % 8) G/8 + b/8 (when 8 divides the grid): workgroup b
+    // runs on XCD b mod 8, so the four row groups whose scales share a 128-byte line of
+    // the column-major scale array run on one XCD, whose L2 assembles the whole line
+    // (-2% at 8192 rows, -4% at 32768)
+    const int G = gridDim.x;
+    const int gb = (G % 8 == 0) ? (blockIdx.x % 8) * (G / 8) + blockIdx.x / 8 : blockIdx.x;
+    const int row0 = gb * kQuantRows;
     const int row = row0 + wave;
     const int nb = cols >> 7;
     const int g = lane >> 4;
