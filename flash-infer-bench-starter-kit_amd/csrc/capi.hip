@@ -65,9 +65,9 @@ constexpr int kMinTileM = 16;           // smallest row tile; sizes the tile lis
 // workgroups split the items of the larger tile lists into better-filled rounds; from
 // T = 1345 both GEMMs are the MFMA-bound prefill kernels on 256-row tiles (GEMM2 on the
 // 128-row second list).  The boundaries come from wall-clock sweeps of the pairs at
-// T = 72 .. 2560 on MI355X over three routing seeds (light, medium and heavy routing to
-// the local experts): between T = 960 and 1344 the best pair depends on the routing
-// (heavy routing prefers the prefill pair, light routing the token-sharing one).
+// T = 72 .. 2560 on MI355X over five routing seeds (light to heavy routing to the local
+// experts): between T = 960 and 1344 the best pair depends on the routing (heavy routing
+// prefers the prefill pair, light routing the token-sharing one).
 struct Plan {
     int tm;        // tile height of the first list
     int tm2;       // tile height of the second list (0: none)
