@@ -13,8 +13,8 @@
 // expert: tiles[i] = (expert, first row, rows, 0).
 //
 // Placement is atomic-free: one token per thread; for each expert a wave ballot gives
-// every lane its rank inside the wave and the wave's count.  Up to 1024 tokens one
-// workgroup (sized to T) does everything in one pass; beyond that a count kernel
+// every lane its rank inside the wave and the wave's count.  Up to kDispatchSmallMaxT
+// tokens one workgroup (sized to T) does everything in one pass; beyond that a count kernel
 // writes per-chunk (256 tokens) expert counts and a place kernel (one workgroup per
 // chunk) turns them into each chunk's base and writes the permutation.
 
@@ -22,8 +22,12 @@
 
 namespace moe {
 
-// T <= 1024: one workgroup of NW waves (64 NW >= T), one token per thread, one pass
-// over the routes.
+constexpr int kDispatchSmallMaxT = 640;
+
+// T <= kDispatchSmallMaxT: one workgroup of NW waves (64 NW >= T), one token per thread, one
+// pass over the routes.  Beyond 640 tokens the two-kernel pass over 256-token chunks is
+// faster (-1.6 us at T = 1024, -0.8 us at 800; +0.4 us at 600): one workgroup's ballots and
+// scans serialise over T / 64 waves.
 template <int TM, int TM2, int NW>
 __global__ __launch_bounds__(64 * NW) void dispatch_small_kernel(
     const int* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int offset,
@@ -59,7 +63,7 @@ __global__ __launch_bounds__(64 * NW) void dispatch_small_kernel(
     place(r, rank, tid, T, wbase[wave], sorted_tok, sorted_w, inv);
 }
 
-// T > 1024, pass 1: chunk c (kChunk tokens) writes its per-expert counts.
+// T > kDispatchSmallMaxT, pass 1: chunk c (kChunk tokens) writes its per-expert counts.
 constexpr int kChunk = 256;
 constexpr int kChunkWaves = kChunk / 64;
 
@@ -80,7 +84,7 @@ __global__ __launch_bounds__(kChunk) void dispatch_count_kernel(
     }
 }
 
-// T > 1024, pass 2: every chunk derives the expert offsets and its own base from the
+// T > kDispatchSmallMaxT, pass 2: every chunk derives the expert offsets and its own base from the
 // chunk count table (thread t sums expert t % 32 over chunks = t / 32 mod 8, then the
 // eight partial sums are added in a fixed order), places its tokens; chunk 0 also
 // writes offsets and tiles.
@@ -178,7 +182,8 @@ static void launch_dispatch_tm(const int* topk_ids, const float* topk_w, int T, 
                                int* exp_off, int* num_tiles, int4* tiles, int* num_tiles2,
                                int4* tiles2, int* sorted_tok, float* sorted_w, int* inv,
                                int* chunk_cnt, hipStream_t stream) {
-    if (T <= 1024) {
+    // without chunk_cnt (allowed up to T = 1024 by the C ABI) the one-workgroup pass runs
+    if (T <= kDispatchSmallMaxT || (chunk_cnt == nullptr && T <= 1024)) {
 #define DISPATCH_SMALL(NW)                                                                        \
     hipLaunchKernelGGL((dispatch_small_kernel<TM, TM2, NW>), dim3(1), dim3(64 * NW), 0, stream,   \
                        topk_ids, topk_w, T, offset, exp_off, num_tiles, tiles, num_tiles2, tiles2, \
@@ -197,7 +202,7 @@ static void launch_dispatch_tm(const int* topk_ids, const float* topk_w, int T, 
                        num_tiles2, tiles2, sorted_tok, sorted_w, inv);
 }
 
-// chunk_cnt: int32 [ceil(T/256) * 32] scratch, needed when T > 1024.  tm2 > 0 (with
+// chunk_cnt: int32 [ceil(T/256) * 32] scratch, needed when T > kDispatchSmallMaxT.  tm2 > 0 (with
 // tiles2 / num_tiles2): a second tile list of tm2 rows over the same rows.  Tile
 // heights: tm in {16, 32, 64, 128, 256} alone, or the pairs (256, 128), (64, 128),
 // (32, 128) and (16, 128) the kernel plans use.

@@ -309,8 +309,10 @@ def route(routing_logits: torch.Tensor, routing_bias: torch.Tensor, routed_scali
 
 
 def dispatch(topk_ids: torch.Tensor, topk_weights: torch.Tensor, local_expert_offset: int,
-             tile_m: int = 64) -> dict:
-    """Dispatch only: the canonical permutation (see include/moe_mi355.h)."""
+             tile_m: int = 64, chunk_scratch: bool = True) -> dict:
+    """Dispatch only: the canonical permutation (see include/moe_mi355.h).  With
+    chunk_scratch False the chunk-count scratch is passed as NULL, which the C ABI
+    allows up to T = 1024 (the one-workgroup pass then runs)."""
     L = _build_extension()
     dev = topk_ids.device
     T = topk_ids.shape[0]
@@ -332,7 +334,8 @@ def dispatch(topk_ids: torch.Tensor, topk_weights: torch.Tensor, local_expert_of
                                   int(tile_m), out["exp_off"].data_ptr(),
                                   out["sorted_tok"].data_ptr(), out["sorted_w"].data_ptr(),
                                   out["inv"].data_ptr(), out["tiles"].data_ptr(),
-                                  out["num_tiles"].data_ptr(), out["chunk_counts"].data_ptr(),
+                                  out["num_tiles"].data_ptr(),
+                                  out["chunk_counts"].data_ptr() if chunk_scratch else None,
                                   ctypes.c_void_p(_stream_ptr(dev)))
     _check(rc, "moe_mi355_dispatch")
     return out

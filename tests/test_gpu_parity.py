@@ -124,6 +124,32 @@ def test_dispatch_bit_exact(idx, tile_m):
     assert np.array_equal(g["tiles"][:nt].cpu().numpy(), r["tiles"])
 
 
+@pytest.mark.parametrize("T", [640, 641, 1000, 1024])
+@pytest.mark.parametrize("chunk_scratch", [True, False])
+def test_dispatch_either_pass_bit_exact(T, chunk_scratch):
+    """Both dispatch passes around their switch point: with the chunk-count scratch the
+    count and place kernels run above T = 640; without it (allowed up to T = 1024) the
+    one-workgroup pass runs.  Each must equal the oracle's permutation."""
+    k = pkg("kernel")
+    o = oracle()
+    d = first_tokens(config_inputs(3), T)
+    rids, rw = o.route(d["routing_logits"], d["routing_bias"], d["routed_scaling_factor"])
+    off = d["local_expert_offset"]
+    note(f"[gpu] dispatch T={T} chunk_scratch={chunk_scratch}")
+    g = k.dispatch(torch.from_numpy(rids).cuda(), torch.from_numpy(rw).cuda(), off, 64,
+                   chunk_scratch=chunk_scratch)
+    torch.cuda.synchronize()
+    r = o.dispatch(rids, rw, off, 64)
+    na = int(r["exp_off"][-1])
+    nt = r["tiles"].shape[0]
+    assert np.array_equal(g["exp_off"].cpu().numpy(), r["exp_off"])
+    assert int(g["num_tiles"].item()) == nt
+    assert np.array_equal(g["sorted_tok"][:na].cpu().numpy(), r["sorted_tok"])
+    assert np.array_equal(g["sorted_w"][:na].cpu().numpy().view(np.uint32), r["sorted_w"].view(np.uint32))
+    assert np.array_equal(g["inv"].cpu().numpy(), r["inv"])
+    assert np.array_equal(g["tiles"][:nt].cpu().numpy(), r["tiles"])
+
+
 def _sample_tokens(T: int, n: int, seed: int):
     if T <= n:
         return list(range(T))

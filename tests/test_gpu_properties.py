@@ -107,12 +107,12 @@ def test_small_odd_batches(T):
     assert st["frac_within"] == 1.0, st
 
 
-@pytest.mark.parametrize("T", [88, 89, 299, 300, 960, 961, 1024, 1025, 1344, 1345])
+@pytest.mark.parametrize("T", [88, 89, 299, 300, 640, 641, 960, 961, 1344, 1345])
 def test_plan_boundaries_match_oracle(T):
     """Token counts on both sides of every change of kernel plan (16-row streaming,
     32-row streaming, the token-sharing GEMM1 on 64-row tiles with three and then two
     workgroups per CU feeding the prefill GEMM2, 256-row prefill tiles) and of the
-    dispatch (one workgroup up to T = 1024, count and place kernels over 256-token
+    dispatch (one workgroup up to T = 640, count and place kernels over 256-token
     chunks beyond)."""
     d = first_tokens(config_inputs(3), T)
     note(f"[gpu] plan boundary T={T}")
