@@ -30,7 +30,7 @@ bool launch_dispatch(const int*, const float*, int, int, int, int, int*, int*, i
 int dispatch_max_tiles(int T, int tm);
 bool launch_gemm1(int, const uint8_t*, const TokenScales&, int, const uint8_t*, const float*,
                   const int4*, const int*, const int*, int, const int*, const Intermediate&,
-                  hipStream_t);
+                  bool, hipStream_t);
 bool launch_gemm1_dispatch(const int*, const float*, int, int, const uint8_t*, const float*,
                            const uint8_t*, const float*, int*, int4*, int*, float*, int*,
                            const Intermediate&, hipStream_t);
@@ -110,9 +110,15 @@ bool make_plan(int g1, int g2, int32_t T, Plan* p) {
 // DMA instruction either way, so it reads them by token and the gather launch goes away
 // (-1 us at T = 600 .. 1280).
 constexpr int32_t kRowScalesMinT = 512;
+
+// The prefill GEMM1 takes its items ranked by expert rows (prefill_items_ranked) up to
+// T = kRankedMaxT and in tile-list order beyond.  Measured on three routings each at
+// T = 1400 .. 3500 the ranked order was 4-24 us faster on 17 of 21 (GEMM1 ~180-270 us)
+// and at most 6 us slower; at T = 4096 (skewed), 5000 and 8192 it was 4-19 us slower.
+constexpr int32_t kRankedMaxT = 3500;
 constexpr int32_t kKnownFlags = MOE_MI355_FLAG_PROFILE | MOE_MI355_FLAG_FORCE_PLAN |
                                 MOE_MI355_FLAG_ROW_SCALES_ON | MOE_MI355_FLAG_ROW_SCALES_OFF |
-                                (0xff << 8);
+                                MOE_MI355_FLAG_LIST_ORDER | (0xff << 8);
 
 // The plan of a call over T tokens: chosen from T alone, unless the caller's flags force
 // a GEMM pair or the token-scale form (tuning sweeps and the tests of every variant).
@@ -301,6 +307,7 @@ int forward_impl(const moe_mi355_args& a, void* workspace, size_t ws_bytes, hipS
     // HIP call left in this thread's last-error slot is cleared first.
     (void)hipGetLastError();
     const bool prof = (a.flags & MOE_MI355_FLAG_PROFILE) && g_prof.ev && g_prof.used < g_prof.slots;
+    const bool ranked = !(a.flags & MOE_MI355_FLAG_LIST_ORDER) && T <= kRankedMaxT;
     const int slot = prof ? g_prof.used++ : 0;
 
     if (prof) prof_record(slot, 0, s);
@@ -332,7 +339,7 @@ int forward_impl(const moe_mi355_args& a, void* workspace, size_t ws_bytes, hipS
     else
         ok = ok && moe::launch_gemm1(plan.g1, a.hidden_states, sa, T, a.gemm1_weights,
                                      a.gemm1_weights_scale, tiles, num_tiles, meta, max_tiles,
-                                     stok, inter, s);
+                                     stok, inter, ranked, s);
     if (prof) prof_record(slot, 3, s);
     if (ok && plan.convert) moe::launch_c_f16_to_hilo(inter, meta, s);   // in the GEMM2 stage
     if (ok && half)

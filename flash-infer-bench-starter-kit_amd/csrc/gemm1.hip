@@ -396,8 +396,8 @@ __device__ __forceinline__ void store_c_hilo(const v4f (&acc)[4][8], float* xch,
 // scale FMAs and LDS reads run under the other's MFMAs; registers stay <= 256 per
 // lane for that.  Two 66 KB stages; rows keep 16-byte chunk c at c ^ swz128(r), so
 // ds_read_b128 in the MFMA layout is conflict-free.  Padding row blocks skip their
-// MFMAs.  Items (row tile, 128-column group) follow grouped_item with an
-// XCD-contiguous mapping of each round.
+// MFMAs.  Items (row tile, 128-column group) follow prefill_items_ranked when `ranked`
+// is set, else grouped_item, with an XCD-contiguous mapping of each round.
 //
 // Operand DMA is buffer_load ... lds (addresses in SGPR resources, 32-bit lane
 // offsets, the K step in the scalar offset), issued in two bursts per K block:
@@ -422,7 +422,7 @@ __global__ __launch_bounds__(512, 1) void gemm1_prefill8_kernel(
     const uint8_t* __restrict__ hidden, TokenScales sa, int T,
     const uint8_t* __restrict__ w1, const float* __restrict__ s1,
     const int4* __restrict__ tiles, const int* __restrict__ num_tiles,
-    const int* __restrict__ exp_off, const int* __restrict__ sorted_tok, Intermediate C) {
+    const int* __restrict__ exp_off, const int* __restrict__ sorted_tok, Intermediate C, int ranked) {
     constexpr int NS = 2;
     constexpr int BM = 256;
     constexpr int NG = kI / 128;
@@ -460,7 +460,9 @@ __global__ __launch_bounds__(512, 1) void gemm1_prefill8_kernel(
         woff[i] = (uint32_t)n * kH + ((dchunk ^ swz128(r)) << 4);
     }
 
-    const int nr = prefill_items<BM>(s_items, kItemCap, nitems, NG, base, G, tiles, exp_off);
+    static_assert(kRankThreads == 512 && kRankScratch <= NS * kStage, "ranked order: threads, scratch");
+    int nr = ranked ? prefill_items_ranked<BM>(s_items, kItemCap, NG, base, G, exp_off, lds) : -1;
+    if (nr < 0) nr = prefill_items<BM>(s_items, kItemCap, nitems, NG, base, G, tiles, exp_off);
     if (nr == 0) return;   // uniform: the whole workgroup has no item
     __syncthreads();
 
@@ -649,7 +651,7 @@ bool launch_gemm1_dispatch(const int* topk_ids, const float* topk_w, int T, int 
 bool launch_gemm1(int variant, const uint8_t* hidden, const TokenScales& sa, int T,
                   const uint8_t* w1, const float* s1, const int4* tiles, const int* num_tiles,
                   const int* exp_off, int max_tiles, const int* sorted_tok, const Intermediate& C,
-                  hipStream_t stream) {
+                  bool ranked, hipStream_t stream) {
     int* c_wide = const_cast<int*>(exp_off) + kCWideFlag;   // meta word, cleared by the route kernel
     const int prefill_grid = 256;   // one resident workgroup per CU (LDS-bound)
     constexpr int G = kI / 16;      // 16-column groups
@@ -677,7 +679,8 @@ bool launch_gemm1(int variant, const uint8_t* hidden, const TokenScales& sa, int
         }
         case 4:
             hipLaunchKernelGGL(gemm1_prefill8_kernel, dim3(prefill_grid), dim3(512), 0, stream,
-                               hidden, sa, T, w1, s1, tiles, num_tiles, exp_off, sorted_tok, C);
+                               hidden, sa, T, w1, s1, tiles, num_tiles, exp_off, sorted_tok, C,
+                               ranked ? 1 : 0);
             return true;
         default: return false;
     }

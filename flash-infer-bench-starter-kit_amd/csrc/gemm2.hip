@@ -72,7 +72,8 @@ __global__ __launch_bounds__(256) void gemm2_rstream_kernel(
 // T = 8192); rows keep 16-byte chunk c
 // at c ^ swz128(r).  Items (128-row piece, 256-column group) are grouped up to 4
 // pieces of one expert x all column groups with an XCD-contiguous mapping, as in
-// the prefill GEMM1.  A workgroup resolves the metadata of all its items at kernel
+// the prefill GEMM1 (list order: the ranked order of the prefill GEMM1 was not faster
+// here, 83-90 us either way at T = 1024 .. 2600).  A workgroup resolves the metadata of all its items at kernel
 // start (prefill_items) and issues the first stage of its next item at the top of
 // the current item's last K block, so the next item's data arrives while the last
 // block computes and the epilogue stores.  In a K block, each 16 x 16 block's hi

@@ -143,6 +143,113 @@ __device__ __forceinline__ int4 prefill_item(const int4* tab, int cap, int r, in
                 __builtin_amdgcn_readfirstlane(m.z), __builtin_amdgcn_readfirstlane(m.w)};
 }
 
+// Ranked order of the same groups, the prefill GEMM1's default up to a few thousand
+// tokens.  The experts are ranked by rows (descending, ties by index), each expert's
+// groups staying together in list order, and round r gives slot p = base on even and
+// G - 1 - base on odd rounds the item r * G + p of that order: the first rounds take
+// the experts with the most rows (full tiles), the lighter ones fill the last rounds,
+// and those rounds alternate their direction over the slots, so a slot that took one of
+// the heaviest items in one round takes one of the lightest in the next instead of two
+// heavy ones.  An expert's items stay adjacent, so the items that read the same weight
+// columns still run together.  The whole workgroup (kRankThreads threads) computes it
+// from the expert offsets alone (tile j of expert e holds rows exp_off[e] + j TM .., as
+// the dispatch lists them) in `scr`, kRankScratch bytes of LDS (16-byte aligned) that
+// are free until the caller's next barrier.  Returns -1 when there are more than
+// kRankMaxGroups groups or `cap` rounds (the caller then uses list order), else the
+// number of rounds that have an item for this slot, their items in tab[0 ..).
+constexpr int kRankThreads = 512;
+constexpr int kRankMaxGroups = kRankThreads;
+constexpr int kRankScratch = kRankMaxGroups * 16 + 4 * (2 * 33 + 2 * kRankMaxGroups + 1 + kRankThreads / 64);
+
+template <int TM>
+__device__ int prefill_items_ranked(int4* tab, int cap, int ncol, int base, int G,
+                                    const int* __restrict__ exp_off, uint8_t* scr) {
+    int4* s_g = reinterpret_cast<int4*>(scr);        // [group] {expert, first tile, tiles, expert rows}
+    int* s_off = reinterpret_cast<int*>(s_g + kRankMaxGroups);   // [33] expert offsets
+    int* s_gs = s_off + 33;                           // [33] first group of each expert, total
+    int* s_pos = s_gs + 33;                           // [rank] group
+    int* s_start = s_pos + kRankMaxGroups;            // [rank + 1] first item of each rank
+    int* s_wsum = s_start + kRankMaxGroups + 1;       // [wave] scan totals
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid <= kEL) s_off[tid] = exp_off[tid];
+    __syncthreads();
+    if (wave == 0) {   // groups per expert, exclusive scan over the experts
+        int v = 0;
+        if (lane < kEL) v = ((s_off[lane + 1] - s_off[lane] + TM - 1) / TM + 3) / 4;
+        int incl = v;
+#pragma unroll
+        for (int d = 1; d < kEL; d <<= 1) {
+            const int u = __shfl_up(incl, d);
+            if (lane >= d) incl += u;
+        }
+        if (lane < kEL) s_gs[lane] = incl - v;
+        if (lane == kEL - 1) s_gs[kEL] = incl;
+    }
+    __syncthreads();
+    const int ngr = s_gs[kEL];
+    if (ngr > kRankMaxGroups) return -1;   // uniform
+    if (ngr == 0) return 0;
+    for (int j = tid; j < ngr; j += kRankThreads) {
+        int lo = 0, hi = kEL;   // s_gs[lo] <= j < s_gs[hi]: the expert owning group j
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (s_gs[mid] <= j) lo = mid;
+            else hi = mid;
+        }
+        const int rows = s_off[lo + 1] - s_off[lo];
+        const int t0 = 4 * (j - s_gs[lo]);
+        const int gm = min(4, (rows + TM - 1) / TM - t0);
+        s_g[j] = int4{lo, t0, gm, rows};
+    }
+    __syncthreads();
+    // rank of group j: the groups of experts with more rows, and those of equal rows
+    // before it in the list (the earlier experts', and the expert's own earlier groups)
+    for (int j = tid; j < ngr; j += kRankThreads) {
+        const int4 gj = s_g[j];
+        int rank = 0;
+        for (int i = 0; i < ngr; ++i) {
+            const int4 gi = s_g[i];
+            rank += (gi.w > gj.w || (gi.w == gj.w && i < j)) ? 1 : 0;
+        }
+        s_pos[rank] = j;
+    }
+    __syncthreads();
+    {   // first item of each rank: exclusive scan of tiles x ncol over the ranks
+        const int v = tid < ngr ? s_g[s_pos[tid]].z * ncol : 0;
+        int incl = v;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int u = __shfl_up(incl, d);
+            if (lane >= d) incl += u;
+        }
+        if (lane == 63) s_wsum[wave] = incl;
+        __syncthreads();
+        for (int w = 0; w < wave; ++w) incl += s_wsum[w];
+        if (tid < ngr) s_start[tid] = incl - v;
+        if (tid == ngr - 1) s_start[ngr] = incl;
+    }
+    __syncthreads();
+    const int nitems = s_start[ngr];
+    const int R = nitems / G, rem = nitems - R * G;
+    const int nr = R + ((((R & 1) ? G - 1 - base : base) < rem) ? 1 : 0);
+    if (nr > cap) return -1;   // uniform
+    for (int r = tid; r < nr; r += kRankThreads) {
+        const int i = r * G + ((r & 1) ? G - 1 - base : base);
+        int lo = 0, hi = ngr;   // s_start[lo] <= i < s_start[hi]
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (s_start[mid] <= i) lo = mid;
+            else hi = mid;
+        }
+        const int4 g = s_g[s_pos[lo]];
+        const int in = i - s_start[lo];
+        const int tix = g.y + in % g.z;
+        const int rows = s_off[g.x + 1] - s_off[g.x];
+        tab[r] = int4{g.x, s_off[g.x] + tix * TM, min(TM, rows - tix * TM), in / g.z};
+    }
+    return nr;
+}
+
 // Token scales as GEMM1 reads them: p[kb * stride + i], where i is the token (by_row 0:
 // the caller's hidden_states_scale [56, T], stride T) or the row of the permutation
 // (by_row 1: the gathered row scales [56, rows_cap], stride rows_cap, in which the rows

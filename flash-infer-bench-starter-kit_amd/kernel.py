@@ -73,6 +73,7 @@ FLAG_PROFILE = 1
 FLAG_FORCE_PLAN = 2
 FLAG_ROW_SCALES_ON = 4
 FLAG_ROW_SCALES_OFF = 8
+FLAG_LIST_ORDER = 16
 
 
 def plan_flags(g1: int, g2: int) -> int:

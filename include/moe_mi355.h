@@ -126,11 +126,18 @@ typedef struct moe_mi355_args {
  *                                  variant 5 reads them by token: _ON selects the separate
  *                                  dispatch at T <= 64 (and is an error with variant 5
  *                                  forced).
+ *   MOE_MI355_FLAG_LIST_ORDER      the prefill GEMM1 (variant 4) takes its work items in
+ *                                  tile-list order also at T <= 3500 (by default it
+ *                                  ranks them by expert rows there, which balances the
+ *                                  workgroups' loads); which workgroup computes an item
+ *                                  is all that changes, so the output is bit-identical
+ *                                  either way.
  * Every variant meets the same tolerance; the flags change speed only. */
 #define MOE_MI355_FLAG_PROFILE 1
 #define MOE_MI355_FLAG_FORCE_PLAN 2
 #define MOE_MI355_FLAG_ROW_SCALES_ON 4
 #define MOE_MI355_FLAG_ROW_SCALES_OFF 8
+#define MOE_MI355_FLAG_LIST_ORDER 16
 #define MOE_MI355_FLAGS_PLAN(g1, g2) \
     (MOE_MI355_FLAG_FORCE_PLAN | (((g1) & 15) << 8) | (((g2) & 15) << 12))
 #define MOE_MI355_FLAGS_G1(flags) (((flags) >> 8) & 15)

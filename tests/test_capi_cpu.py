@@ -199,7 +199,7 @@ def test_forced_plan_that_cannot_run_is_an_error(lib, g1, g2):
     assert lib.moe_mi355_get_workspace_layout(4, a.flags, ctypes.byref(lay)) == -7
 
 
-@pytest.mark.parametrize("flags", [1 << 20, 1 << 9, 4 | 8, 1 << 31])
+@pytest.mark.parametrize("flags", [1 << 20, 1 << 9, 4 | 8, 1 << 31, 1 << 5])
 def test_unknown_flag_bits_are_an_error(lib, flags):
     """Unknown bits, variant bits without the force bit, and both token-scale forms at
     once are rejected."""
@@ -207,6 +207,16 @@ def test_unknown_flag_bits_are_an_error(lib, flags):
     a = _fake_args(k)
     a.flags = flags - (1 << 32) if flags >= 1 << 31 else flags
     assert lib.moe_mi355_forward(ctypes.byref(a), None) == -7
+
+
+def test_list_order_flag_is_known_and_keeps_the_plan():
+    """FLAG_LIST_ORDER (16) only changes which workgroup takes a prefill GEMM1 item: it is
+    accepted alone and with a forced plan, and the layout is the same as without it."""
+    k = pkg("kernel")
+    assert k.FLAG_LIST_ORDER == 16
+    for T, base in ((2000, 0), (700, k.plan_flags(4, 5)), (64, 0)):
+        a, b = k.workspace_layout(T, base), k.workspace_layout(T, base | k.FLAG_LIST_ORDER)
+        assert (a.total, a.tile_m, a.intermediate_format) == (b.total, b.tile_m, b.intermediate_format)
 
 
 def test_layout_reports_the_forced_plan():

@@ -238,6 +238,34 @@ def test_row_order_token_scales_change_nothing(T):
     assert torch.equal(tab[:, :na], d["hidden_states_scale"][:, stok])
 
 
+@pytest.mark.parametrize("idx,T,g1,g2", [(3, 1500, 0, 0), (3, 3500, 0, 0), (4, 3500, 0, 0),
+                                         (3, 700, 4, 5), (3, 300, 4, 5), (1, None, 4, 5),
+                                         (0, None, 4, 5), (3, 3501, 0, 0)])
+def test_ranked_item_order_changes_nothing(idx, T, g1, g2):
+    """The prefill GEMM1's ranked item order (the default up to T = 3500: every case but
+    the last) and tile-list order (FLAG_LIST_ORDER) give bit-identical outputs over every
+    token.  Only which workgroup computes an item differs; the workspace is filled with
+    0xff (fp8 / fp16 NaN) before each call, so an item that either order computed never
+    would show as NaN."""
+    d = config_inputs(idx) if T is None else first_tokens(config_inputs(idx), T)
+    k = pkg("kernel")
+    wl = pkg("workloads")
+    T = d["routing_logits"].shape[0]
+    base = k.plan_flags(g1, g2) if g1 else 0
+    lay = k.workspace_layout(T, base)
+    outs = []
+    for flag in (0, k.FLAG_LIST_ORDER):
+        note(f"[gpu] item order config {idx} T={T} flags {base | flag}")
+        ws = torch.full((lay.total,), 255, dtype=torch.uint8, device="cuda")
+        out = torch.full_like(d["output"], float("nan"))
+        k.forward(*wl.as_args({**d, "output": out}), workspace=ws, flags=base | flag)
+        torch.cuda.synchronize()
+        assert not torch.isnan(out).any()
+        outs.append(out)
+        del ws
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+
+
 @pytest.mark.parametrize("T,g1,g2", [(64, 0, 0), (600, 0, 0), (2049, 0, 0), (600, 7, 5), (1100, 0, 0)])
 def test_all_local_routing_matches_oracle(T, g1, g2):
     """Every token routed to 8 local experts (bias +3 on all 32 local experts, so group 0
