@@ -68,15 +68,26 @@ def quantize_blocks_128(w: torch.Tensor):
     return q.view(R, C), scale
 
 
-def make_activations(cfg: Config, device="cpu", T: Optional[int] = None) -> dict:
-    """Logits, bias and quantised hidden states of a config (T may be overridden)."""
-    T = cfg.T if T is None else T
-    g = _gen(device, cfg.seed)
+def _draw_routing(cfg: Config, g: torch.Generator, device, T: int):
     logits = torch.randn(T, E_GLOBAL, generator=g, device=device, dtype=torch.float32)
     bias = (torch.randn(E_GLOBAL, generator=g, device=device, dtype=torch.float32) * 0.1)
     for le in cfg.hot_local_experts:
         bias[cfg.local_expert_offset + le] += 3.0
-    bias = bias.to(torch.bfloat16)
+    return logits, bias.to(torch.bfloat16)
+
+
+def make_routing_inputs(cfg: Config, device="cpu", T: Optional[int] = None):
+    """The config's (logits fp32 [T, 256], bias bf16 [256]) alone: the same values as
+    make_activations, without drawing and quantising the hidden states."""
+    T = cfg.T if T is None else T
+    return _draw_routing(cfg, _gen(device, cfg.seed), device, T)
+
+
+def make_activations(cfg: Config, device="cpu", T: Optional[int] = None) -> dict:
+    """Logits, bias and quantised hidden states of a config (T may be overridden)."""
+    T = cfg.T if T is None else T
+    g = _gen(device, cfg.seed)
+    logits, bias = _draw_routing(cfg, g, device, T)
     x = torch.randn(T, H, generator=g, device=device, dtype=torch.float32).to(torch.bfloat16)
     hs, hs_scale = quantize_rows_128(x)
     return dict(routing_logits=logits, routing_bias=bias, hidden_states=hs,
