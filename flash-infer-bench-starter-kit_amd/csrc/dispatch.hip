@@ -172,11 +172,6 @@ void launch_gather_row_scales(const float* hs_scale, int T, const int* sorted_to
                        sorted_tok, exp_off, row_scales, rows_cap);
 }
 
-int dispatch_max_tiles(int T, int tm) {
-    const long long rows = (long long)T * kTopK;
-    return (int)((rows + tm - 1) / tm) + kEL;
-}
-
 template <int TM, int TM2>
 static void launch_dispatch_tm(const int* topk_ids, const float* topk_w, int T, int offset,
                                int* exp_off, int* num_tiles, int4* tiles, int* num_tiles2,

@@ -258,8 +258,7 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(WPE)))
 // kernels after it read it.  The dispatch launch goes away; the dispatch itself costs a
 // workgroup about what the separate kernel's two dependent loads (tile list, then
 // permutation) cost before its first weight load.
-constexpr int kDispatchInGemm1MaxT = 64;
-constexpr int kDG1MaxTiles = kDispatchInGemm1MaxT * kTopK / 16 + kEL;   // 64
+constexpr int kDG1MaxTiles = dispatch_max_tiles(kDispatchInGemm1MaxT, 16);   // 64
 
 __global__ __launch_bounds__(256) void gemm1_rstream_dispatch_kernel(
     const int* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int offset,

@@ -6,22 +6,9 @@
 
 #include <utility>
 
-namespace moe {
+#include "moe_shape.h"
 
-// Geometry (reference solution/python/kernel.h:9-25).
-constexpr int kH = 7168;           // hidden
-constexpr int kI = 2048;           // intermediate
-constexpr int kN1 = 2 * kI;        // GEMM1 output width (gate rows | up rows)
-constexpr int kEG = 256;           // global experts
-constexpr int kEL = 32;            // local experts
-constexpr int kTopK = 8;
-constexpr int kNGroup = 8;
-constexpr int kGroupSize = 32;
-constexpr int kTopKGroup = 4;
-constexpr int kBlk = 128;          // quantisation block edge
-constexpr int kHB = kH / kBlk;     // 56 hidden blocks
-constexpr int kIB = kI / kBlk;     // 16 intermediate blocks
-constexpr int kN1B = kN1 / kBlk;   // 32 GEMM1 output blocks
+namespace moe {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
@@ -332,10 +319,9 @@ __device__ __forceinline__ void bdma4(__amdgpu_buffer_rsrc_t r, uint32_t voff, u
 // value beyond the fp16 range (then |x| 2^-e < 2^15 for every value of the group).
 // Readers that find the call's flag word raised apply the exponents; otherwise they
 // read the fp16 values as they are.
-constexpr int kCWideFlag = kEL + 3;    // meta word: C exceeds the fp16 range
-constexpr int kRowsWideFlag = kEL + 4; // meta word: an expert row exceeds the fp16 range
+// The flag words are kCWideFlag / kRowsWideFlag of the meta region, the exponent
+// groups kGroup16 columns wide (moe_shape.h).
 constexpr float kF16Max = 65504.f;
-constexpr int kGroup16 = 16;           // columns per exponent byte
 
 // Exponent of a 16-column group of which this lane holds 4 values (the other 12 are in
 // lanes l ^ 16, l ^ 32, l ^ 48: the same row, the other column quads of an MFMA 16x16
