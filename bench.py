@@ -6,8 +6,11 @@ experts) on one GPU.
 
 A step is one call of ``kernel(...)`` (route -> dispatch -> GEMM1+SwiGLU -> GEMM2 ->
 combine) over one batch of seeded synthetic inputs already resident in HBM.  Weights
-and activations rotate over ``--rotate`` copies so that consecutive steps do not find
-the previous step's weights in the 256 MB MALL.
+and activations rotate over copies so that a step does not find its weights in the
+256 MB MALL (Infinity Cache): by default as many copies as put at least twice the
+MALL's bytes between two uses of one copy (the algorithmic bytes of a call, from its
+routing, times the other copies), and at least 4; ``--rotate N`` fixes the count.  The
+copy count and that reuse distance are reported in the line.
 
 The headline (``value``) is configs[1] of BASELINE.json (decode, T=64): W untimed
 warmup steps, then exactly K timed steps between two ``torch.cuda.synchronize()``.
@@ -42,6 +45,8 @@ FP8_PEAK_TFLOPS = 5000.0
 BF16_PEAK_TFLOPS = 2500.0
 MIN_CONFIG_WARMUP = 20
 MIN_CONFIG_WARMUP_MS = 20.0
+MALL_BYTES = 256 << 20           # MI355X Infinity Cache
+MIN_ROTATE = 4
 
 
 def _load(name: str, path: str):
@@ -64,7 +69,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--config", type=int, default=None,
                     help="measure only this index of BASELINE.json configs (it becomes the headline)")
-    ap.add_argument("--rotate", type=int, default=4, help="input copies cycled over steps")
+    ap.add_argument("--rotate", type=int, default=0,
+                    help="input copies cycled over steps (0: enough for a reuse distance of "
+                         "twice the MALL, at least 4)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="skip the HIP-graph replay timing")
     ap.add_argument("--no-quantizer", action="store_true", help="skip the quantizer leg")
@@ -170,10 +177,6 @@ def measure_config(idx: int, a, k, wl, o, steps: int, warmup: int, quantizer: bo
     dev = torch.device("cuda:0")
     log(f"[bench] config {idx} {cfg.name} T={cfg.T}: generating inputs")
     base = wl.make_inputs(cfg, device=dev)
-    copies = [base]
-    for _ in range(max(0, a.rotate - 1)):
-        copies.append({kk: (v.clone() if isinstance(v, torch.Tensor) else v) for kk, v in base.items()})
-    arglists = [wl.as_args(c) for c in copies]
     T = cfg.T
     ws = torch.empty(k.workspace_bytes(T), dtype=torch.uint8, device=dev)
     torch.cuda.synchronize()
@@ -184,6 +187,20 @@ def measure_config(idx: int, a, k, wl, o, steps: int, warmup: int, quantizer: bo
     le = ids.to(torch.int64) - cfg.local_expert_offset
     touched = int(((le >= 0) & (le < 32)).any(dim=1).sum())
     n_a, e_a = work["N_a"], work["E_a"]
+
+    # input copies: between two uses of one copy, the other copies' calls touch at least
+    # twice the MALL's bytes (unless --rotate fixes the count)
+    ncopies = a.rotate if a.rotate > 0 else \
+        max(MIN_ROTATE, 1 + -(-2 * MALL_BYTES // max(1, work["bytes"])))
+    copies = [base]
+    for _ in range(ncopies - 1):
+        copies.append({kk: (v.clone() if isinstance(v, torch.Tensor) else v) for kk, v in base.items()})
+    arglists = [wl.as_args(c) for c in copies]
+    rotation = {"copies": ncopies, "bytes_per_call": work["bytes"],
+                "reuse_distance_bytes": (ncopies - 1) * work["bytes"], "mall_bytes": MALL_BYTES}
+    log(f"[bench] config {idx}: {ncopies} input copies, reuse distance "
+        f"{rotation['reuse_distance_bytes'] / 2**20:.0f} MiB")
+    torch.cuda.synchronize()
 
     for i in range(warmup):
         k.forward(*arglists[i % len(arglists)], workspace=ws)
@@ -321,6 +338,7 @@ def measure_config(idx: int, a, k, wl, o, steps: int, warmup: int, quantizer: bo
         "hbm_frac_whole_call": work["bytes"] / (lat_us * 1e-6) / (HBM_PEAK_GBS * 1e9),
         "stages_us": stages_us,
         "profiled_calls": n_prof,
+        "rotation": rotation,
         "roofline": roof,
         "cpu_baseline": cpu,
     }
@@ -377,7 +395,9 @@ def main() -> int:
         "config": {"workload": h["workload"], "T": h["T"],
                    "local_expert_offset": h["local_expert_offset"],
                    "routed_scaling_factor": wl.CONFIGS[head_idx].routed_scaling_factor,
-                   "hot_local_experts": h["hot_local_experts"], "rotate_copies": a.rotate,
+                   "hot_local_experts": h["hot_local_experts"],
+                   "rotate_copies": h["rotation"]["copies"],
+                   "reuse_distance_bytes": h["rotation"]["reuse_distance_bytes"],
                    "parallelism": "ep-rank (32 of 256 experts) on 1 GPU"},
         "latency_us": h["latency_us"],
         "eff_tflops": h["eff_tflops"],

@@ -8,8 +8,13 @@ Several processes may build at once (harness workers that each load the solution
 first use): a build holds an exclusive ``fcntl`` lock on ``libmoe_mi355.so.lock`` next
 to the library, compiles and links inside a private temporary directory, and installs
 the result with one atomic ``os.replace``, so no process ever loads a half-written
-library or links another process's objects.  ``ensure_built`` builds only when the
-library is missing, re-checking under the lock.
+library or links another process's objects.
+
+The library carries a hash of the sources it was built from (``csrc/*.hip``,
+``csrc/*.h`` and the C-ABI header) in its version string, ``moe_mi355_version()``.
+``ensure_built`` builds when the library is missing or its hash differs from the
+sources next to it (an edited kernel is never tested with the old binary), re-checking
+under the lock.
 """
 from __future__ import annotations
 
@@ -17,6 +22,7 @@ import argparse
 import concurrent.futures as cf
 import contextlib
 import fcntl
+import hashlib
 import os
 import shutil
 import subprocess
@@ -48,9 +54,43 @@ def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
-def _compile(src: str, outdir: str) -> str:
+# prefix of the source hash inside the library's version string (capi.hip)
+HASH_TAG = b"moe_mi355 src "
+
+
+def source_hash() -> str:
+    """Hash of everything the library is compiled from: every csrc/*.hip and csrc/*.h
+    file (name and bytes, in name order), then the C-ABI header."""
+    h = hashlib.sha256()
+    names = sorted(f for f in os.listdir(CSRC) if f.endswith((".hip", ".h")))
+    for path in [os.path.join(CSRC, f) for f in names] + [os.path.join(INCLUDE, "moe_mi355.h")]:
+        h.update(os.path.basename(path).encode() + b"\0")
+        with open(path, "rb") as f:
+            h.update(f.read())
+        h.update(b"\0")
+    return h.hexdigest()[:16]
+
+
+def library_hash(path: str = LIB):
+    """The source hash a built library carries (from its version string), or None."""
+    if not os.path.exists(path):
+        return None
+    with open(path, "rb") as f:
+        data = f.read()
+    i = data.find(HASH_TAG)
+    if i < 0:
+        return None
+    return data[i + len(HASH_TAG):i + len(HASH_TAG) + 16].decode("ascii", "replace")
+
+
+def is_current(path: str = LIB) -> bool:
+    """The library exists and was built from the sources next to it."""
+    return library_hash(path) == source_hash()
+
+
+def _compile(src: str, outdir: str, src_hash: str) -> str:
     obj = os.path.join(outdir, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
+    cmd = [HIPCC, *FLAGS, f'-DMOE_MI355_SRC_HASH="{src_hash}"', "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{r.stdout}\n{r.stderr}")
@@ -76,8 +116,9 @@ def _build_locked(jobs: int, verbose: bool) -> str:
     work = tempfile.mkdtemp(prefix="_build.", dir=HERE)
     try:
         srcs = sources()
+        src_hash = source_hash()
         with cf.ThreadPoolExecutor(max_workers=max(1, min(jobs, len(srcs)))) as ex:
-            objs = list(ex.map(lambda s: _compile(s, work), srcs))
+            objs = list(ex.map(lambda s: _compile(s, work, src_hash), srcs))
         tmp = os.path.join(work, os.path.basename(LIB))
         cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
         r = subprocess.run(cmd, capture_output=True, text=True)
@@ -98,11 +139,12 @@ def build(jobs: int = 8, verbose: bool = True) -> str:
 
 
 def ensure_built(jobs: int = 8, verbose: bool = False) -> str:
-    """Build the library only if it is missing (the first use of a packed solution)."""
-    if os.path.exists(LIB):
+    """Build the library if it is missing or was built from other sources (the first
+    use of a packed solution, or a kernel edited since the last build)."""
+    if is_current():
         return LIB
     with _build_lock():
-        if os.path.exists(LIB):       # another process built it while this one waited
+        if is_current():              # another process built it while this one waited
             return LIB
         return _build_locked(jobs, verbose)
 

@@ -198,7 +198,12 @@ int forward_impl(const moe_mi355_args& a, void* workspace, size_t ws_bytes, hipS
 
 extern "C" {
 
-const char* moe_mi355_version(void) { return "moe_mi355 0.1 gfx950"; }
+// The build passes a hash of the sources (build.py, source_hash) that the loader
+// compares with the sources next to the library before it loads it.
+#ifndef MOE_MI355_SRC_HASH
+#define MOE_MI355_SRC_HASH "0000000000000000"
+#endif
+const char* moe_mi355_version(void) { return "moe_mi355 0.1 gfx950; moe_mi355 src " MOE_MI355_SRC_HASH; }
 
 const char* moe_mi355_last_hip_error(void) { return g_hip_error; }
 

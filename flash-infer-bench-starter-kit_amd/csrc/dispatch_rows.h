@@ -1,7 +1,7 @@
 // dispatch_rows.h -- building blocks of the dispatch (per-expert ranks from wave
 // ballots, the scan of the counts, the tile list and the placement of rows), shared by
-// the dispatch kernels (dispatch.hip) and the fused decode kernel (decode.hip), which
-// computes the dispatch of its few tokens in every workgroup.
+// the dispatch kernels (dispatch.hip) and the GEMM1 that computes the dispatch of its
+// few tokens in every workgroup (gemm1_rstream_dispatch_kernel, gemm1.hip, T <= 64).
 #pragma once
 
 #include "moe_device.h"

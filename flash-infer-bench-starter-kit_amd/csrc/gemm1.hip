@@ -5,9 +5,10 @@
 // mainloop):
 //   G1[r, n] = sum_kb sa[kb, tok(r)] * sb[e, n/128, kb] * sum_{k in kb} A[tok(r), k] W1[e, n, k]
 //   C[r, i]  = silu(G1[r, 2048 + i]) * G1[r, i]        (kernel.cu:1104-1108 convention)
-// C is written as one row per routed assignment for GEMM2: fp16 plus a bf16 copy by
-// the streaming kernels, the fp8 hi/lo form by the prefill kernels (moe_device.h,
-// Intermediate).
+// C is written as one row per routed assignment for GEMM2: the fp16 form (fp16 values
+// with a power-of-two exponent byte per 16-column group, nonzero only where a group
+// holds a value beyond the fp16 range) by the streaming kernels, the fp8 hi/lo form by
+// the prefill kernels (moe_device.h, Intermediate).
 //
 // Kernels: register-staged weight streaming for small T (a work item is one row tile
 // of 16 or 32 rows x 16 gate + 16 up rows, its 56 K blocks split over the 4 waves of

@@ -7,8 +7,8 @@
 // moe_grouped_gemm_fp8.cu:274-322):
 //   O[r, h] = sum_kb sb2[e, h/128, kb] * sum_{i in kb} C[r, i] * W2[e, h, i]
 // Streaming kernels: C is the fp16 SwiGLU output of GEMM1; when GEMM1 flagged a value
-// beyond the fp16 range, C runs through bf16 instead, with the bf16 copy GEMM1 wrote
-// for exactly those values.  W2 e4m3 bytes are widened in registers to the same type
+// beyond the fp16 range, C runs through bf16 instead, rebuilt from the fp16 values and
+// their 16-column group exponents.  W2 e4m3 bytes are widened in registers to the same type
 // (exact: every e4m3 value is an fp16 and a bf16 value) for
 // v_mfma_f32_16x16x32_{f16,bf16}, operand A = 16 W2 rows, operand B = 16 C rows; lane l
 // supplies row l%16 and K elements 32*(l/16) + 8j..8j+7 of the block for MFMA j = 0..3

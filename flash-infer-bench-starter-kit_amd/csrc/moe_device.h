@@ -174,7 +174,7 @@ __device__ int prefill_items_ranked(int4* tab, int cap, int ncol, int base, int 
     }
     __syncthreads();
     const int ngr = s_gs[kEL];
-    if (ngr > kRankMaxGroups) return -1;   // uniform
+    if (ngr > kRankMaxGroups) return -1;   // the same in every workgroup (expert offsets only)
     if (ngr == 0) return 0;
     for (int j = tid; j < ngr; j += kRankThreads) {
         int lo = 0, hi = kEL;   // s_gs[lo] <= j < s_gs[hi]: the expert owning group j
@@ -217,9 +217,12 @@ __device__ int prefill_items_ranked(int4* tab, int cap, int ncol, int base, int 
     }
     __syncthreads();
     const int nitems = s_start[ngr];
+    // the same decision in every workgroup of the grid (it depends on nitems and G
+    // only): no slot gets more than ceil(nitems / G) rounds, so none overflows tab[cap]
+    // and either all workgroups take the ranked order or all take list order
+    if ((nitems + G - 1) / G > cap) return -1;
     const int R = nitems / G, rem = nitems - R * G;
     const int nr = R + ((((R & 1) ? G - 1 - base : base) < rem) ? 1 : 0);
-    if (nr > cap) return -1;   // uniform
     for (int r = tid; r < nr; r += kRankThreads) {
         const int i = r * G + ((r & 1) ? G - 1 - base : base);
         int lo = 0, hi = ngr;   // s_start[lo] <= i < s_start[hi]

@@ -13,7 +13,9 @@ ordered combine, all on the caller's current stream, no host synchronisation).
 
 Like the reference, which JIT-compiles its extension on first use
 (kernel.py:57-92), the first call builds ``libmoe_mi355.so`` with hipcc (gfx950)
-when it is not already next to this file (``build.py`` builds it ahead of time).
+when it is not already next to this file (``build.py`` builds it ahead of time), or
+when the library was built from other sources than the ``csrc/`` next to it (its
+version string carries a hash of them).
 Concurrent first calls from several processes are serialised by a file lock and
 install the library atomically.  If the library can neither be found nor built,
 ``kernel`` raises: there is no CPU or PyTorch fallback.
@@ -121,7 +123,9 @@ def _build_extension() -> ctypes.CDLL:
     with _lock:
         if _lib is not None:
             return _lib
-        if not os.path.exists(_LIB_PATH):
+        # the package's own library is (re)built when missing or stale; a library
+        # path set by the caller is loaded as it is
+        if os.path.abspath(_LIB_PATH) == os.path.join(_HERE, "libmoe_mi355.so"):
             import importlib.util
             spec = importlib.util.spec_from_file_location("_moe_mi355_build", os.path.join(_HERE, "build.py"))
             mod = importlib.util.module_from_spec(spec)
@@ -129,7 +133,7 @@ def _build_extension() -> ctypes.CDLL:
             try:
                 mod.ensure_built()
             except Exception as e:
-                raise RuntimeError(f"{_LIB_PATH} is missing and could not be built "
+                raise RuntimeError(f"{_LIB_PATH} is missing or stale and could not be built "
                                    f"(there is no fallback path): {e}") from e
         _lib = _declare(ctypes.CDLL(_LIB_PATH))
     return _lib

@@ -162,6 +162,10 @@ MOE_MI355_API int moe_mi355_forward(const moe_mi355_args* args, void* stream);
  *   - Calls on one GPU share the array: calls that overlap in time on one GPU (on
  *     different streams) race and must not be issued; calls on one stream are
  *     ordered and safe.  Nothing in the array needs clearing between calls.
+ *   - Under HIP graph capture: make one eager call on that device first.  The first
+ *     call on a device looks up the array's address (hipGetSymbolAddress) and, for
+ *     T <= 64, the launch grid (an occupancy query); after it, calls only enqueue
+ *     kernels and can be captured (tested for T = 8 and 256). 
  * Results are bit-identical to moe_mi355_forward's. */
 #define MOE_MI355_NOALLOC_MAX_TOKENS 256
 MOE_MI355_API int moe_mi355_forward_noalloc(const moe_mi355_args* args, void* stream);

@@ -300,8 +300,9 @@ def _flags(ws, lay):
 def _huge_inputs_check(d, c_flag, flags=0):
     """Hidden-state scales 2^10 times larger: |C| and the expert rows reach ~1e6, far
     beyond the fp16 range.  The call must raise the expert-row flag (meta[36]) and,
-    on the streaming plans, the C flag (meta[35]); the combine and GEMM2 then take the
-    fp32 / bf16 copies, and the output is finite and within 1e-2 of the largest output
+    on the streaming plans, the C flag (meta[35]); the combine and GEMM2 (or the
+    conversion to the hi/lo form) then apply the 16-column group exponents of the fp16
+    forms, and the output is finite and within 1e-2 of the largest output
     of the fp32 oracle (elementwise atol 1e-2 means nothing at this scale: where terms
     of 1e6 cancel, even exact fp32 staging leaves errors far above it).  A normal call
     on the same workspace afterwards finds both flags cleared and gives the same output
@@ -361,11 +362,21 @@ def test_values_beyond_fp16_range_separate_dispatch():
 
 
 def test_values_beyond_fp16_range_converted_plan():
-    """T = 1024 (streaming GEMM1, fp16 C converted to the hi/lo form for the prefill
-    GEMM2): the conversion takes GEMM1's bf16 copies of the values beyond the fp16
-    range."""
+    """T = 1024 with the 32-row streaming GEMM1 forced (GEMM1 variant 2, whose two
+    column groups per item write the group exponents of C) and its fp16 C converted to
+    the hi/lo form for the prefill GEMM2: the conversion applies the exponents."""
     d = first_tokens(config_inputs(3), 1024)
-    note("[gpu] values beyond the fp16 range, T=1024")
+    note("[gpu] values beyond the fp16 range, T=1024, plan 2/5")
+    _huge_inputs_check(d, c_flag=1, flags=pkg("kernel").plan_flags(2, 5))
+
+
+def test_values_beyond_fp16_range_32_row_streaming_plan():
+    """T = 200 (the default plan there: 32-row streaming GEMM1, variant 2, and the
+    32-row streaming GEMM2, variant 3, whose rare path reads C's group exponents)."""
+    d = first_tokens(config_inputs(3), 200)
+    note("[gpu] values beyond the fp16 range, T=200, plan 2/3")
+    lay = pkg("kernel").workspace_layout(200)
+    assert lay.tile_m == 32 and lay.intermediate_format == 0
     _huge_inputs_check(d, c_flag=1)
 
 

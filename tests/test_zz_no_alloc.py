@@ -82,3 +82,52 @@ def test_noalloc_matches_forward_on_consecutive_calls():
         assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), f"T={T}"
         assert bool(torch.isfinite(out.float()).all())
         note(f"[gpu] noalloc T={T} bit-identical, max |out| {float(out.float().abs().max()):.3g}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T", [8, MAX_T])
+def test_noalloc_under_graph_capture(T):
+    """After one eager call on the device (which looks up the array's address and the
+    launch grid), noalloc calls can be captured into a HIP graph: each replay, run
+    after eager forward calls on the same output and a device synchronisation, is
+    bit-identical to moe_mi355_forward with a fresh workspace; and a warm eager call
+    leaves the device's free memory (hipMemGetInfo) unchanged."""
+    from gpu_common import config_inputs, first_tokens, note
+    k = pkg("kernel")
+    wl = pkg("workloads")
+    L = k._build_extension()
+    dev = torch.device("cuda:0")
+    d = first_tokens(config_inputs(1 if T <= 64 else 3), T)
+    ref = torch.full_like(d["output"], float("nan"))
+    k.forward(*wl.as_args({**d, "output": ref}))
+    out = torch.full_like(d["output"], float("nan"))
+    a = _args(k, d, out)
+    side = torch.cuda.Stream(dev)
+
+    def call(stream):
+        return L.moe_mi355_forward_noalloc(ctypes.byref(a), ctypes.c_void_p(stream.cuda_stream))
+
+    note(f"[gpu] noalloc graph capture T={T}")
+    side.wait_stream(torch.cuda.current_stream(dev))
+    assert call(side) == 0                 # the warm call, on the capture stream
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info(dev)[0]
+    assert call(side) == 0
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info(dev)[0] == free0
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        rc = call(side)
+    assert rc == 0, L.moe_mi355_strerror(rc).decode()
+    torch.cuda.synchronize()
+    for rep in range(3):
+        out.fill_(float("nan"))
+        other = torch.full_like(out, float("nan"))
+        k.forward(*wl.as_args({**d, "output": other}))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), f"replay {rep}"
+    note(f"[gpu] noalloc graph T={T}: 3 replays bit-identical")
