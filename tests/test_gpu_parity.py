@@ -245,3 +245,17 @@ def test_prefill_intermediate_hilo_rows(T, g1, g2):
         bmax = ref.view(16, 128).abs().amax(dim=1).repeat_interleave(128)
         err = (got[i] - ref).abs()
         assert (err <= ref.abs() * 2.0 ** -7 + bmax * 2.0 ** -10).all(), (r, float(err.max()))
+
+
+def test_forward_every_token_of_config2():
+    """Config 2 (T = 1024, offset 64) with every token compared, not a sample: all
+    7,340,032 outputs within |gpu - ref| <= 1e-2 + 1e-2 |ref| of the fp32 oracle; the
+    error distribution is printed."""
+    d = config_inputs(2)
+    T = d["routing_logits"].shape[0]
+    note(f"[gpu] forward config 2, all {T} tokens")
+    out = run_forward(d)
+    st = compare_to_oracle(d, out, list(range(T)))
+    note(f"[gpu] config 2 every token: {st}")
+    assert st["n"] == T * 7168
+    assert st["frac_within"] == 1.0, st
