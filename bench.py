@@ -324,7 +324,8 @@ def measure_config(idx: int, a, k, wl, o, steps: int, warmup: int, quantizer: bo
                   1: "fp8_e4m3 GEMM1 + fp8 hi/lo GEMM2 (two FP8 MFMAs per product), fp32 accumulate",
                   2: "fp8_e4m3 GEMM1 (fp16 C, converted to fp8 hi/lo) + fp8 hi/lo GEMM2, "
                      "fp32 accumulate"}[lay.intermediate_format],
-        "plan": {"tile_m": lay.tile_m, "dispatch_in_gemm1": bool(lay.dispatch_in_gemm1)},
+        "plan": {"tile_m": lay.tile_m, "dispatch_in_gemm1": bool(lay.dispatch_in_gemm1),
+                 "combine_in_gemm2": bool(lay.combine_in_gemm2)},
         "latency_us": {"mean_wall": round(lat_us, 3), "median_event": float(np.median(ev_us)),
                        "p10_event": float(np.percentile(ev_us, 10)),
                        "p90_event": float(np.percentile(ev_us, 90)),

@@ -36,6 +36,8 @@ bool launch_gemm1_dispatch(const int*, const float*, int, int, const uint8_t*, c
                            const Intermediate&, hipStream_t);
 bool launch_gemm2(int, const Intermediate&, const uint8_t*, const float*, const int4*, const int*,
                   const int*, int, const ExpertRows&, hipStream_t);
+bool launch_gemm2_combine(const Intermediate&, const uint8_t*, const float*, const int4*, const int*,
+                          int*, const int*, const float*, int, uint16_t*, hipStream_t);
 void launch_combine(const ExpertRows&, const int*, const float*, const int*, int, uint16_t*, hipStream_t);
 void launch_e4m3_to_bf16(const uint8_t*, uint16_t*, int, hipStream_t);
 void launch_c_f16_to_hilo(const Intermediate&, const int*, hipStream_t);
@@ -180,14 +182,18 @@ int forward_impl(const moe_mi355_args& a, void* workspace, size_t ws_bytes, hipS
                                      stok, inter, ranked, s);
     if (prof) prof_record(slot, 3, s);
     if (ok && plan.convert) moe::launch_c_f16_to_hilo(inter, meta, s);   // in the GEMM2 stage
-    if (ok && half)
+    if (ok && plan.combine_in_gemm2)      // GEMM2 writes the output (timed as the GEMM2 stage)
+        ok = moe::launch_gemm2_combine(inter, a.gemm2_weights, a.gemm2_weights_scale, tiles,
+                                       num_tiles, meta, inv, sw, T, a.output, s);
+    else if (ok && half)
         ok = moe::launch_gemm2(plan.g2, inter, a.gemm2_weights, a.gemm2_weights_scale, tiles2,
                                num_tiles2, meta, moe::dispatch_max_tiles(T, plan.tm2), rows, s);
     else if (ok)
         ok = moe::launch_gemm2(plan.g2, inter, a.gemm2_weights, a.gemm2_weights_scale, tiles,
                                num_tiles, meta, max_tiles, rows, s);
     if (prof) prof_record(slot, 4, s);
-    if (ok) moe::launch_combine(rows, meta + moe::kRowsWideFlag, sw, inv, T, a.output, s);
+    if (ok && !plan.combine_in_gemm2)
+        moe::launch_combine(rows, meta + moe::kRowsWideFlag, sw, inv, T, a.output, s);
     if (prof) prof_record(slot, 5, s);
     const int hst = hip_status(hipGetLastError());
     if (hst != MOE_OK) return hst;

@@ -73,19 +73,6 @@ struct Gemm1Shared {
     static constexpr int kRowsPerWave = 64 / NWV;           // token rows each wave moves
 };
 
-// Workgroup barrier that orders LDS only.  __syncthreads() is a release/acquire of all
-// memory at workgroup scope, which waits for every outstanding vector-memory load
-// (vmcnt(0)) and would drain the weight ring at every K block; here the caller has
-// already waited for its own LDS-DMA loads of the block the barrier hands over.
-__device__ __forceinline__ void lds_barrier() {
-    __asm__ volatile("" ::: "memory");   // no memory access moves across (compiler level)
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's LDS reads and writes are done
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-    __asm__ volatile("" ::: "memory");
-}
-
 // vmcnt immediate for v = 0 .. 24 (uniform v; the switch keeps every wait an immediate)
 __device__ __forceinline__ void wait_vm_upto24(int v) {
     switch (v) {

@@ -203,22 +203,20 @@ __device__ __forceinline__ void gemm2_rstream_item(
     reduce_store<KSPLIT, HF, CB>(acc, red, wave, lane, ks, row0, nrows, hg, rows, rows_wide);
 }
 
-// The same work items when C went beyond the fp16 range somewhere (rare): bf16 MFMAs on
-// C rebuilt from its fp16 form and group exponents.  Plain loads in
-// the MFMA layout, one K block at a time: slow, but light on registers, so the normal
-// path keeps its occupancy.
+// The K partial of one wave of a work item when C went beyond the fp16 range somewhere
+// (rare): bf16 MFMAs on C rebuilt from its fp16 form and group exponents, over K blocks
+// ks KB .. ks KB + KB - 1 of the HF groups of 16 output columns from hg, for the CB
+// 16-row blocks of the tile from row0.  Plain loads in the MFMA layout, one K block at a
+// time: slow, but light on registers, so the normal path keeps its occupancy.
 template <int KSPLIT, int HF, int CB>
-__device__ __forceinline__ void gemm2_rstream_rare_item(
+__device__ __forceinline__ void gemm2_rare_partial(
     const uint16_t* __restrict__ inter, const uint8_t* __restrict__ inter_exp,
     const uint8_t* __restrict__ w2, const float* __restrict__ s2, int le, int row0, int nrows,
-    int hg0, const ExpertRows& rows, int* __restrict__ rows_wide, v4f (*red)[HF][CB][64], int wave) {
+    int hg, int ks, v4f (&acc)[HF][CB]) {
     constexpr int KB = kIB / KSPLIT;
     const int lane = threadIdx.x & 63;
     const int r16 = lane & 15, kq = lane >> 4;
-    const int ngl = wave / KSPLIT, ks = wave % KSPLIT;
     const v4f zero = {0.f, 0.f, 0.f, 0.f};
-    const int hg = hg0 + ngl * HF;
-    v4f acc[HF][CB];
 #pragma unroll
     for (int hf = 0; hf < HF; ++hf)
 #pragma unroll
@@ -255,6 +253,20 @@ __device__ __forceinline__ void gemm2_rstream_rare_item(
                 for (int v = 0; v < 4; ++v) acc[hf][c][v] = __builtin_fmaf(t[c][v], sb, acc[hf][c][v]);
         }
     }
+}
+
+// The work items of gemm2_rstream_item when C went beyond the fp16 range: each wave's K
+// partial on the rare path, reduced and stored as the normal path does.
+template <int KSPLIT, int HF, int CB>
+__device__ __forceinline__ void gemm2_rstream_rare_item(
+    const uint16_t* __restrict__ inter, const uint8_t* __restrict__ inter_exp,
+    const uint8_t* __restrict__ w2, const float* __restrict__ s2, int le, int row0, int nrows,
+    int hg0, const ExpertRows& rows, int* __restrict__ rows_wide, v4f (*red)[HF][CB][64], int wave) {
+    const int lane = threadIdx.x & 63;
+    const int ngl = wave / KSPLIT, ks = wave % KSPLIT;
+    const int hg = hg0 + ngl * HF;
+    v4f acc[HF][CB];
+    gemm2_rare_partial<KSPLIT, HF, CB>(inter, inter_exp, w2, s2, le, row0, nrows, hg, ks, acc);
     reduce_store<KSPLIT, HF, CB>(acc, red, wave, lane, ks, row0, nrows, hg, rows, rows_wide);
 }
 

@@ -47,6 +47,7 @@ struct Plan {
     bool convert;  // fp16 C converted to the hi/lo form between the GEMMs
     bool by_row;   // GEMM1 reads the token scales gathered into row order
     bool dispatch_in_gemm1;   // GEMM1 variant 5 computes the dispatch itself (no launch)
+    bool combine_in_gemm2;    // GEMM2 variant 6 writes the output itself (no combine launch)
 };
 
 inline int g1_tile_m(int v) { return v == 1 || v == 5 ? 16 : v == 2 ? 32 : v == 7 || v == 8 ? 64 : 256; }
@@ -58,21 +59,28 @@ inline bool g2_hilo(int v) { return v == 5; }        // GEMM2 reads the hi/lo fo
 // persistent grid computes the call's dispatch from the routing ids, and the separate
 // dispatch launch goes away.
 inline bool make_plan(int g1, int g2, int32_t T, Plan* p) {
+    // GEMM2 variant 6 is variant 1 (16-row tiles, fp16 C) with the combine folded in,
+    // for T <= kFusedCombineMaxT
+    if (g2 == 6 && (T > kFusedCombineMaxT || (g1 != 1 && g1 != 5))) return false;
     if (g1 == 5) {
-        if (g2 != 1 || T > kDispatchInGemm1MaxT) return false;
-        *p = {16, 0, 5, g2, false, false, true};
+        if ((g2 != 1 && g2 != 6) || T > kDispatchInGemm1MaxT) return false;
+        *p = {16, 0, 5, g2, false, false, true, g2 == 6};
+        return true;
+    }
+    if (g1 == 1 && g2 == 6) {
+        *p = {16, 0, 1, 6, false, false, false, true};
         return true;
     }
     if ((g1 != 1 && g1 != 2 && g1 != 4 && g1 != 7 && g1 != 8) || (g2 != 1 && g2 != 3 && g2 != 5)) return false;
     const int tm = g1_tile_m(g1);
     if (g1_hilo(g1) && !g2_hilo(g2)) return false;      // the fp16 GEMM2s need fp16 C
     if (g2 == 5) {                                       // the second list, 128-row tiles
-        *p = {tm, 128, g1, g2, !g1_hilo(g1), false, false};
+        *p = {tm, 128, g1, g2, !g1_hilo(g1), false, false, false};
         return true;
     }
     const int tm_g2 = g2 == 1 ? 16 : 32;
     if (tm_g2 != tm) return false;
-    *p = {tm, 0, g1, g2, g1_hilo(g1) != g2_hilo(g2), false, false};
+    *p = {tm, 0, g1, g2, g1_hilo(g1) != g2_hilo(g2), false, false, false};
     return true;
 }
 
@@ -101,7 +109,8 @@ inline int plan_for(int32_t T, int32_t flags, Plan* p) {
     int g1, g2;
     // GEMM1 with the dispatch folded in reads the token scales by token: asking for the
     // gathered ones selects the separate dispatch there
-    if (T <= kDispatchInGemm1MaxT && !on) g1 = 5, g2 = 1;
+    if (T <= kFusedCombineMaxT && !on) g1 = 5, g2 = 6;
+    else if (T <= kDispatchInGemm1MaxT && !on) g1 = 5, g2 = 1;
     else if (T <= 88) g1 = 1, g2 = 1;
     else if (T <= 299) g1 = 2, g2 = 3;
     else if (T <= 960) g1 = 8, g2 = 5;
@@ -164,6 +173,7 @@ inline int fill_layout(int32_t T, int32_t flags, moe_mi355_workspace_layout* L) 
     L->tile_m = plan.tm;
     L->intermediate_format = g1_hilo(plan.g1) ? 1 : plan.convert ? 2 : 0;
     L->dispatch_in_gemm1 = plan.dispatch_in_gemm1 ? 1 : 0;
+    L->combine_in_gemm2 = plan.combine_in_gemm2 ? 1 : 0;
     return MOE_OK;
 }
 

@@ -269,6 +269,20 @@ __device__ __forceinline__ constexpr int vmcnt_imm(int v) {
     return (v & 15) | ((v >> 4) << 14) | (7 << 4) | (15 << 8);
 }
 
+// Workgroup barrier that orders LDS only.  __syncthreads() is a release/acquire of all
+// memory at workgroup scope, which waits for every outstanding vector-memory load
+// (vmcnt(0)) and would drain the weight ring at every K block; here the caller has
+// already waited for whatever global loads the barrier hands over (its own LDS-DMA
+// loads of a K block), and register-staged loads stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+    __asm__ volatile("" ::: "memory");   // no memory access moves across (compiler level)
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's LDS reads and writes are done
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    __asm__ volatile("" ::: "memory");
+}
+
 // Compile-time int for generic lambdas (kernels specialise their K loop on the number
 // of 16-row blocks of a tile a wave actually has to compute).
 template <int N>

@@ -30,6 +30,10 @@ constexpr int kGroup16 = 16;       // columns per fp16-form exponent byte
 // keeps that call's permutation and tile list in LDS, sized by this bound.
 constexpr int kDispatchInGemm1MaxT = 64;
 
+// Largest T whose GEMM2 runs with the combine folded in (GEMM2 variant 6): the kernel
+// keeps every expert row of the call (8 T rows) for its 32 output columns in LDS.
+constexpr int kFusedCombineMaxT = 32;
+
 // Upper bound on the row tiles of tm rows a call over T tokens can have: every local
 // expert's last tile may be partial.
 constexpr int dispatch_max_tiles(int T, int tm) {

@@ -64,7 +64,8 @@ class WorkspaceLayout(ctypes.Structure):
         "sorted_weights", "chunk_counts", "row_scales", "intermediate", "intermediate_scales", "expert_out", "expert_out_exp",
         "total")] + [
         ("tile_m", ctypes.c_int32), ("max_tiles", ctypes.c_int32),
-        ("intermediate_format", ctypes.c_int32), ("dispatch_in_gemm1", ctypes.c_int32)]
+        ("intermediate_format", ctypes.c_int32), ("dispatch_in_gemm1", ctypes.c_int32),
+        ("combine_in_gemm2", ctypes.c_int32)]
 
 
 MAX_TOKENS = 1 << 19    # MOE_MI355_MAX_TOKENS

@@ -117,8 +117,11 @@ typedef struct moe_mi355_args {
  *                                  gives MOE_ERR_BAD_FLAGS.
  *                                  GEMM1 variant 5 is variant 1 with the dispatch
  *                                  computed inside it (T <= 64, the default there; pairs
- *                                  with GEMM2 variant 1): bit-identical output,
- *                                  one launch fewer.
+ *                                  with GEMM2 variants 1 and 6): bit-identical output,
+ *                                  one launch fewer.  GEMM2 variant 6 is variant 1 with
+ *                                  the combine computed inside it (T <= 32, the default
+ *                                  there, after GEMM1 variant 5 or 1): bit-identical
+ *                                  output, one launch fewer.
  *   MOE_MI355_FLAG_ROW_SCALES_ON / _OFF  GEMM1 reads the token scales gathered into row
  *                                  order / straight by token (default: gathered from
  *                                  T = 512, except under GEMM1 variants 7 and 8, which gather
@@ -256,6 +259,8 @@ typedef struct moe_mi355_workspace_layout {
     int32_t max_tiles;
     int32_t intermediate_format;
     int32_t dispatch_in_gemm1;  /* 1: GEMM1 computes the dispatch (no dispatch launch) */
+    int32_t combine_in_gemm2;   /* 1: GEMM2 writes the output itself (no combine launch;
+                                   the expert_out rows are not written) */
 } moe_mi355_workspace_layout;
 
 /* The layout of a call over T tokens with the given call flags: the regions do not

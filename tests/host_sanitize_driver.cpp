@@ -22,7 +22,7 @@ static int g_fail = 0;
         }                                                                      \
     } while (0)
 
-static const int32_t kTs[] = {INT32_MIN, -1, 0, 1, 2, 8, 16, 63, 64, 65, 88, 89, 299, 300, 511,
+static const int32_t kTs[] = {INT32_MIN, -1, 0, 1, 2, 8, 16, 32, 33, 63, 64, 65, 88, 89, 299, 300, 511,
                               512, 960, 961, 1024, 1344, 1345, 3500, 3501, 8192,
                               (1 << 19) - 1, 1 << 19, (1 << 19) + 1, INT32_MAX};
 
@@ -77,6 +77,8 @@ static unsigned long long sweep_plans() {
                 CHECK(p.tm == L.tile_m);
                 CHECK(p.tm2 == 0 || p.tm2 == 128);
                 CHECK(!p.dispatch_in_gemm1 || T <= moe::kDispatchInGemm1MaxT);
+                CHECK(!p.combine_in_gemm2 || (T <= moe::kFusedCombineMaxT && p.tm == 16));
+                CHECK(L.combine_in_gemm2 == (p.combine_in_gemm2 ? 1 : 0));
                 check_layout(T, L);
                 sum = sum * 1000003ull + (unsigned)(p.g1 * 16 + p.g2) + (p.by_row ? 1000 : 0) +
                       (p.convert ? 2000 : 0) + (unsigned long long)L.total;
@@ -96,8 +98,9 @@ static void default_plans() {
             printf("T %d status %d\n", T, st);
             continue;
         }
-        printf("T %d plan g1 %d g2 %d tm %d tm2 %d convert %d by_row %d dispatch_in_gemm1 %d\n", T,
-               p.g1, p.g2, p.tm, p.tm2, (int)p.convert, (int)p.by_row, (int)p.dispatch_in_gemm1);
+        printf("T %d plan g1 %d g2 %d tm %d tm2 %d convert %d by_row %d dispatch_in_gemm1 %d combine_in_gemm2 %d\n",
+               T, p.g1, p.g2, p.tm, p.tm2, (int)p.convert, (int)p.by_row, (int)p.dispatch_in_gemm1,
+               (int)p.combine_in_gemm2);
     }
 }
 
