@@ -22,7 +22,8 @@ the five configs is measured the same way (K steps after W warmup; the other con
 warm up for at least 20 steps and 20 ms of calls, so the GPU reaches steady clocks) and
 reported in ``per_config``, in config order: latency, effective TFLOP/s, the fraction of the
 whole call's roofline, the roofline of the dominant kernel measured with HIP events
-on the library's stream, and the CPU baseline (the reference's CPU-shaped path,
+that the runtime stamps at that kernel's own start and end on the library's stream
+(the library's stage profiler, hipExtLaunchKernelGGL), and the CPU baseline (the reference's CPU-shaped path,
 moe.cu:137-240, restated in torch-CPU) timed on this host on a bounded sample.
 
 Prints ONE JSON line.
@@ -235,7 +236,8 @@ def measure_config(idx: int, a, k, wl, o, steps: int, warmup: int, quantizer: bo
     torch.cuda.synchronize()
     ev_us = np.array([s.elapsed_time(e) * 1e3 for s, e in zip(starts, ends)])
 
-    # per-kernel durations: HIP events recorded by the library on its launch stream
+    # per-stage kernel durations: the library times each kernel with a pair of HIP events
+    # stamped at the kernel's start and end (launch gaps excluded), summed per stage
     k.profile_begin(steps)
     for i in range(steps):
         k.forward(*arglists[i % len(arglists)], workspace=ws, flags=k.FLAG_PROFILE)

@@ -46,6 +46,10 @@ void launch_e4m3_to_f16(const uint8_t*, uint16_t*, int, hipStream_t);
 void launch_quantize_fp8_blockwise(const void*, int, int, int, uint8_t*, float*, hipStream_t);
 }  // namespace moe
 
+namespace moe {
+thread_local KernelTimer* g_kernel_timer = nullptr;
+}  // namespace moe
+
 namespace {
 
 using moe::host::aligned16;
@@ -66,16 +70,17 @@ int hip_status(hipError_t e) {
 }
 
 // ---- stage profiler ------------------------------------------------------------
+// One record per profiled call: a start and a stop event for each of its kernels
+// (launch_kernel fills them) and the stage of each kernel.
+constexpr int kMaxTimedLaunches = 8;   // kernels of one forward call
 struct Profiler {
-    hipEvent_t* ev = nullptr;   // [slots][kNumStages + 1]
+    hipEvent_t* ev = nullptr;          // [slots][2 kMaxTimedLaunches]
+    int* stage = nullptr;              // [slots][kMaxTimedLaunches]
+    moe::KernelTimer* rec = nullptr;   // [slots]
     int slots = 0;
     int used = 0;
 };
 Profiler g_prof;
-
-void prof_record(int slot, int stage, hipStream_t s) {
-    (void)hipEventRecord(g_prof.ev[slot * (MOE_MI355_NUM_STAGES + 1) + stage], s);
-}
 
 // ---- the library's own workspace (moe_mi355_forward_noalloc) ---------------------
 // A workspace for calls of up to MOE_MI355_NOALLOC_MAX_TOKENS tokens in a file-scope
@@ -146,14 +151,19 @@ int forward_impl(const moe_mi355_args& a, void* workspace, size_t ws_bytes, hipS
     // The status reports this call's launches only: an error some earlier, unrelated
     // HIP call left in this thread's last-error slot is cleared first.
     (void)hipGetLastError();
-    const bool prof = (a.flags & MOE_MI355_FLAG_PROFILE) && g_prof.ev && g_prof.used < g_prof.slots;
+    const bool prof = (a.flags & MOE_MI355_FLAG_PROFILE) && g_prof.rec && g_prof.used < g_prof.slots;
     const bool ranked = !(a.flags & MOE_MI355_FLAG_LIST_ORDER) && T <= kRankedMaxT;
-    const int slot = prof ? g_prof.used++ : 0;
+    moe::KernelTimer* timer = prof ? &g_prof.rec[g_prof.used++] : nullptr;
+    if (timer) timer->n = 0;
+    auto stage = [timer](int st) {
+        if (timer) timer->cur_stage = st;
+    };
+    moe::g_kernel_timer = timer;   // the launches below time themselves (cleared before return)
 
-    if (prof) prof_record(slot, 0, s);
+    stage(0);
     moe::launch_route(a.routing_logits, a.routing_bias, T, (float)a.routed_scaling_factor, ids,
                       wts, meta + moe::kCWideFlag, s);
-    if (prof) prof_record(slot, 1, s);
+    stage(1);
     const int max_tiles = moe::dispatch_max_tiles(T, plan.tm);
     const bool half = plan.tm2 > 0;   // GEMM2 walks the second (128-row) tile list
     int4* tiles2 = tiles + max_tiles;
@@ -170,7 +180,7 @@ int forward_impl(const moe_mi355_args& a, void* workspace, size_t ws_bytes, hipS
                                       T * moe::kTopK, s);
     const moe::TokenScales sa = plan.by_row ? moe::TokenScales{row_scales, T * moe::kTopK, 1}
                                             : moe::TokenScales{a.hidden_states_scale, T, 0};
-    if (prof) prof_record(slot, 2, s);
+    stage(2);
     if (plan.dispatch_in_gemm1)
         ok = ok && moe::launch_gemm1_dispatch(ids, wts, T, clamp_offset(a.local_expert_offset),
                                               a.hidden_states, a.hidden_states_scale,
@@ -180,7 +190,7 @@ int forward_impl(const moe_mi355_args& a, void* workspace, size_t ws_bytes, hipS
         ok = ok && moe::launch_gemm1(plan.g1, a.hidden_states, sa, T, a.gemm1_weights,
                                      a.gemm1_weights_scale, tiles, num_tiles, meta, max_tiles,
                                      stok, inter, ranked, s);
-    if (prof) prof_record(slot, 3, s);
+    stage(3);
     if (ok && plan.convert) moe::launch_c_f16_to_hilo(inter, meta, s);   // in the GEMM2 stage
     if (ok && plan.combine_in_gemm2)      // GEMM2 writes the output (timed as the GEMM2 stage)
         ok = moe::launch_gemm2_combine(inter, a.gemm2_weights, a.gemm2_weights_scale, tiles,
@@ -191,10 +201,10 @@ int forward_impl(const moe_mi355_args& a, void* workspace, size_t ws_bytes, hipS
     else if (ok)
         ok = moe::launch_gemm2(plan.g2, inter, a.gemm2_weights, a.gemm2_weights_scale, tiles,
                                num_tiles, meta, max_tiles, rows, s);
-    if (prof) prof_record(slot, 4, s);
+    stage(4);
     if (ok && !plan.combine_in_gemm2)
         moe::launch_combine(rows, meta + moe::kRowsWideFlag, sw, inv, T, a.output, s);
-    if (prof) prof_record(slot, 5, s);
+    moe::g_kernel_timer = nullptr;
     const int hst = hip_status(hipGetLastError());
     if (hst != MOE_OK) return hst;
     return ok ? MOE_OK : MOE_ERR_BAD_PLAN;
@@ -319,7 +329,7 @@ size_t moe_mi355_noalloc_scratch_bytes(void) { return kScratchBytes; }
 int moe_mi355_profile_begin(int32_t max_calls) {
     moe_mi355_profile_end();
     if (max_calls <= 0) return MOE_ERR_BAD_SIZE;
-    const int n = max_calls * (MOE_MI355_NUM_STAGES + 1);
+    const int n = max_calls * 2 * kMaxTimedLaunches;
     g_prof.ev = new hipEvent_t[n];
     for (int i = 0; i < n; ++i) {
         const hipError_t e = hipEventCreate(&g_prof.ev[i]);
@@ -330,25 +340,32 @@ int moe_mi355_profile_begin(int32_t max_calls) {
             return hip_status(e);
         }
     }
+    g_prof.stage = new int[max_calls * kMaxTimedLaunches];
+    g_prof.rec = new moe::KernelTimer[max_calls];
+    for (int c = 0; c < max_calls; ++c)
+        g_prof.rec[c] = {g_prof.ev + c * 2 * kMaxTimedLaunches, g_prof.stage + c * kMaxTimedLaunches,
+                         kMaxTimedLaunches, 0, 0};
     g_prof.slots = max_calls;
     g_prof.used = 0;
     return MOE_OK;
 }
 
+// Average over the recorded calls of each stage's time: the sum of its kernels' times,
+// each from the HIP events stamped at that kernel's start and end.
 int moe_mi355_profile_read(float* stage_ms, int32_t n) {
     if (!stage_ms) return MOE_ERR_NULL_POINTER;
-    if (!g_prof.ev || g_prof.used == 0) return 0;
+    if (!g_prof.rec || g_prof.used == 0) return 0;
     const int ns = MOE_MI355_NUM_STAGES;
     double sum[MOE_MI355_NUM_STAGES] = {0};
     for (int c = 0; c < g_prof.used; ++c) {
-        hipEvent_t* ev = g_prof.ev + c * (ns + 1);
-        const hipError_t e = hipEventSynchronize(ev[ns]);
-        if (e != hipSuccess) return hip_status(e);
-        for (int st = 0; st < ns; ++st) {
+        const moe::KernelTimer& r = g_prof.rec[c];
+        for (int i = 0; i < r.n; ++i) {
+            const hipError_t e = hipEventSynchronize(r.ev[2 * i + 1]);
+            if (e != hipSuccess) return hip_status(e);
             float ms = 0.f;
-            const hipError_t e2 = hipEventElapsedTime(&ms, ev[st], ev[st + 1]);
+            const hipError_t e2 = hipEventElapsedTime(&ms, r.ev[2 * i], r.ev[2 * i + 1]);
             if (e2 != hipSuccess) return hip_status(e2);
-            sum[st] += ms;
+            if (r.stage[i] >= 0 && r.stage[i] < ns) sum[r.stage[i]] += ms;
         }
     }
     for (int st = 0; st < ns && st < n; ++st) stage_ms[st] = (float)(sum[st] / g_prof.used);
@@ -357,13 +374,12 @@ int moe_mi355_profile_read(float* stage_ms, int32_t n) {
 
 int moe_mi355_profile_end(void) {
     if (g_prof.ev) {
-        for (int i = 0; i < g_prof.slots * (MOE_MI355_NUM_STAGES + 1); ++i)
-            (void)hipEventDestroy(g_prof.ev[i]);
+        for (int i = 0; i < g_prof.slots * 2 * kMaxTimedLaunches; ++i) (void)hipEventDestroy(g_prof.ev[i]);
         delete[] g_prof.ev;
     }
-    g_prof.ev = nullptr;
-    g_prof.slots = 0;
-    g_prof.used = 0;
+    delete[] g_prof.stage;
+    delete[] g_prof.rec;
+    g_prof = Profiler{};
     return MOE_OK;
 }
 

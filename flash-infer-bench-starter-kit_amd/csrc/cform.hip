@@ -63,7 +63,7 @@ __global__ __launch_bounds__(256) void c_f16_to_hilo_kernel(Intermediate C, cons
 void launch_c_f16_to_hilo(const Intermediate& C, const int* meta, hipStream_t stream) {
     const int grid = C.rows_cap < 2048 ? C.rows_cap : 2048;
     if (grid <= 0) return;
-    hipLaunchKernelGGL(c_f16_to_hilo_kernel, dim3(grid), dim3(256), 0, stream, C, meta);
+    launch_kernel(c_f16_to_hilo_kernel, dim3(grid), dim3(256), 0, stream, C, meta);
 }
 
 }  // namespace moe

@@ -34,7 +34,7 @@ void launch_combine(const ExpertRows& rows, const int* rows_wide, const float* s
                     int T, uint16_t* out, hipStream_t stream) {
     if (T <= 0) return;
     constexpr int kParts = kH / (128 * 8);
-    hipLaunchKernelGGL(combine_kernel, dim3((unsigned)T * kParts), dim3(128), 0, stream, rows,
+    launch_kernel(combine_kernel, dim3((unsigned)T * kParts), dim3(128), 0, stream, rows,
                        rows_wide, sorted_w, inv, T, out);
 }
 

@@ -168,7 +168,7 @@ void launch_gather_row_scales(const float* hs_scale, int T, const int* sorted_to
                               hipStream_t stream) {
     if (rows_cap <= 0) return;
     const int gx = min((rows_cap + 255) / 256, 64);
-    hipLaunchKernelGGL(gather_row_scales_kernel, dim3(gx, kHB), dim3(256), 0, stream, hs_scale, T,
+    launch_kernel(gather_row_scales_kernel, dim3(gx, kHB), dim3(256), 0, stream, hs_scale, T,
                        sorted_tok, exp_off, row_scales, rows_cap);
 }
 
@@ -180,7 +180,7 @@ static void launch_dispatch_tm(const int* topk_ids, const float* topk_w, int T, 
     // without chunk_cnt (allowed up to T = 1024 by the C ABI) the one-workgroup pass runs
     if (T <= kDispatchSmallMaxT || (chunk_cnt == nullptr && T <= 1024)) {
 #define DISPATCH_SMALL(NW)                                                                        \
-    hipLaunchKernelGGL((dispatch_small_kernel<TM, TM2, NW>), dim3(1), dim3(64 * NW), 0, stream,   \
+    launch_kernel((dispatch_small_kernel<TM, TM2, NW>), dim3(1), dim3(64 * NW), 0, stream,   \
                        topk_ids, topk_w, T, offset, exp_off, num_tiles, tiles, num_tiles2, tiles2, \
                        sorted_tok, sorted_w, inv)
         if (T <= 64) DISPATCH_SMALL(1);
@@ -190,9 +190,9 @@ static void launch_dispatch_tm(const int* topk_ids, const float* topk_w, int T, 
         return;
     }
     const int nchunks = (T + kChunk - 1) / kChunk;
-    hipLaunchKernelGGL(dispatch_count_kernel, dim3(nchunks), dim3(kChunk), 0, stream, topk_ids, topk_w,
+    launch_kernel(dispatch_count_kernel, dim3(nchunks), dim3(kChunk), 0, stream, topk_ids, topk_w,
                        T, offset, chunk_cnt);
-    hipLaunchKernelGGL((dispatch_place_kernel<TM, TM2>), dim3(nchunks), dim3(kChunk), 0, stream, topk_ids,
+    launch_kernel((dispatch_place_kernel<TM, TM2>), dim3(nchunks), dim3(kChunk), 0, stream, topk_ids,
                        topk_w, T, offset, chunk_cnt, nchunks, exp_off, num_tiles, tiles,
                        num_tiles2, tiles2, sorted_tok, sorted_w, inv);
 }

@@ -622,7 +622,7 @@ bool launch_gemm1_dispatch(const int* topk_ids, const float* topk_w, int T, int 
     }
     const long long items = (long long)(((long long)T * kTopK + 15) / 16 + kEL) * Gemm1Stream<1, 1, false>::kItems;
     const int grid = (int)(items < resident ? items : resident);
-    hipLaunchKernelGGL(gemm1_rstream_dispatch_kernel, dim3(grid), dim3(256), 0, stream, topk_ids,
+    launch_kernel(gemm1_rstream_dispatch_kernel, dim3(grid), dim3(256), 0, stream, topk_ids,
                        topk_w, T, offset, hidden, hs_scale, w1, s1, meta, tiles, sorted_tok, sorted_w,
                        inv, C);
     return true;
@@ -645,27 +645,27 @@ bool launch_gemm1(int variant, const uint8_t* hidden, const TokenScales& sa, int
     const long long mt = max_tiles;
     switch (variant) {
         case 1:
-            hipLaunchKernelGGL((gemm1_rstream_kernel<4, 1, 1, false>), dim3(grid_for(mt * G)), dim3(256), 0, stream,
+            launch_kernel((gemm1_rstream_kernel<4, 1, 1, false>), dim3(grid_for(mt * G)), dim3(256), 0, stream,
                                hidden, sa, T, w1, s1, tiles, num_tiles, sorted_tok, C, c_wide);
             return true;
         case 2:
-            hipLaunchKernelGGL((gemm1_rstream_kernel<2, 2, 2, true>), dim3(grid_for(mt * G / 2)), dim3(256), 0, stream,
+            launch_kernel((gemm1_rstream_kernel<2, 2, 2, true>), dim3(grid_for(mt * G / 2)), dim3(256), 0, stream,
                                hidden, sa, T, w1, s1, tiles, num_tiles, sorted_tok, C, c_wide);
             return true;
         case 7: {   // 4-wave workgroups, two resident per CU (registers)
             const long long items = mt * Gemm1Shared<2, 4>::kItems;
-            hipLaunchKernelGGL((gemm1_shared_kernel<2, 4, 1>), dim3((int)(items < 768 ? items : 768)), dim3(256), 0,
+            launch_kernel((gemm1_shared_kernel<2, 4, 1>), dim3((int)(items < 768 ? items : 768)), dim3(256), 0,
                                stream, hidden, sa, T, w1, s1, tiles, num_tiles, sorted_tok, C, c_wide);
             return true;
         }
         case 8: {   // the same held to three resident per CU
             const long long items = mt * Gemm1Shared<2, 4>::kItems;
-            hipLaunchKernelGGL((gemm1_shared_kernel<2, 4, 3>), dim3((int)(items < 768 ? items : 768)), dim3(256), 0,
+            launch_kernel((gemm1_shared_kernel<2, 4, 3>), dim3((int)(items < 768 ? items : 768)), dim3(256), 0,
                                stream, hidden, sa, T, w1, s1, tiles, num_tiles, sorted_tok, C, c_wide);
             return true;
         }
         case 4:
-            hipLaunchKernelGGL(gemm1_prefill8_kernel, dim3(prefill_grid), dim3(512), 0, stream,
+            launch_kernel(gemm1_prefill8_kernel, dim3(prefill_grid), dim3(512), 0, stream,
                                hidden, sa, T, w1, s1, tiles, num_tiles, exp_off, sorted_tok, C,
                                ranked ? 1 : 0);
             return true;

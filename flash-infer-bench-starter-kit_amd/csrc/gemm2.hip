@@ -363,15 +363,15 @@ bool launch_gemm2(int variant, const Intermediate& C, const uint8_t* w2, const f
     constexpr int G = kH / 16;      // 16-column groups
     switch (variant) {
         case 1:
-            hipLaunchKernelGGL((gemm2_rstream_kernel<4, 4, 2, 1>), dim3(grid_for2(mt * G / 2)), dim3(256), 0,
+            launch_kernel((gemm2_rstream_kernel<4, 4, 2, 1>), dim3(grid_for2(mt * G / 2)), dim3(256), 0,
                                stream, C, flags, w2, s2, tiles, num_tiles, rows);
             return true;
         case 3:
-            hipLaunchKernelGGL((gemm2_rstream_kernel<3, 4, 4, 2>), dim3(grid_for2(mt * G / 4)), dim3(256), 0,
+            launch_kernel((gemm2_rstream_kernel<3, 4, 4, 2>), dim3(grid_for2(mt * G / 4)), dim3(256), 0,
                                stream, C, flags, w2, s2, tiles, num_tiles, rows);
             return true;
         case 5:
-            hipLaunchKernelGGL(gemm2_prefill8_kernel, dim3(256), dim3(512), 0, stream, C, w2, s2, tiles,
+            launch_kernel(gemm2_prefill8_kernel, dim3(256), dim3(512), 0, stream, C, w2, s2, tiles,
                                num_tiles, exp_off, rows, flags + 1);
             return true;
         default: return false;

@@ -250,7 +250,7 @@ bool launch_gemm2_combine(const Intermediate& C, const uint8_t* w2, const float*
                           const int4* tiles, const int* num_tiles, int* meta, const int* inv,
                           const float* sorted_w, int T, uint16_t* out, hipStream_t stream) {
     if (T <= 0 || T > kFusedCombineMaxT) return false;
-    hipLaunchKernelGGL((gemm2_combine_kernel<2>), dim3(kH / kFusedCols), dim3(512), 0, stream, C,
+    launch_kernel((gemm2_combine_kernel<2>), dim3(kH / kFusedCols), dim3(512), 0, stream, C,
                        meta + kCWideFlag, w2, s2, tiles, num_tiles, inv, sorted_w, T, out);
     return true;
 }

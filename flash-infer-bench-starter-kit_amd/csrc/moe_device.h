@@ -1,6 +1,7 @@
 // moe_device.h -- shared constants and device helpers of the gfx950 fused-MoE kernels.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -16,6 +17,31 @@ typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef short v8s __attribute__((ext_vector_type(8)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+
+// Kernel timing of the stage profiler (MOE_MI355_FLAG_PROFILE).  While a profiled
+// forward call enqueues its kernels, g_kernel_timer points at that call's record: every
+// launch made through launch_kernel takes the next pair of HIP events, which the runtime
+// stamps when the kernel itself starts and ends (hipExtLaunchKernelGGL), so a kernel's
+// time excludes the launch gap before it; the record keeps the stage of each launch.
+// Outside profiled calls the pointer is null and launch_kernel is a plain launch.
+struct KernelTimer {
+    hipEvent_t* ev;   // [2 cap]: start, stop of launch i at 2 i, 2 i + 1
+    int* stage;       // [cap]
+    int cap, n, cur_stage;
+};
+extern thread_local KernelTimer* g_kernel_timer;
+
+template <typename K, typename... Args>
+inline void launch_kernel(K kernel, dim3 grid, dim3 block, uint32_t shmem, hipStream_t s, Args... args) {
+    KernelTimer* t = g_kernel_timer;
+    if (t != nullptr && t->n < t->cap) {
+        const int i = t->n++;
+        t->stage[i] = t->cur_stage;
+        hipExtLaunchKernelGGL(kernel, grid, block, shmem, s, t->ev[2 * i], t->ev[2 * i + 1], 0, args...);
+    } else {
+        hipLaunchKernelGGL(kernel, grid, block, shmem, s, args...);
+    }
+}
 
 // Round-to-nearest-even fp32 -> bf16 bits (NaN -> quiet NaN).
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {

@@ -192,7 +192,7 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
 void launch_route(const float* logits, const uint16_t* bias, int T, float factor,
                   int* topk_ids, float* topk_w, int* clear_word, hipStream_t stream) {
     if (T <= 0) return;
-    hipLaunchKernelGGL(route_kernel, dim3((T + 3) / 4), dim3(256), 0, stream, logits, bias,
+    launch_kernel(route_kernel, dim3((T + 3) / 4), dim3(256), 0, stream, logits, bias,
                        T, factor, topk_ids, topk_w, clear_word);
 }
 

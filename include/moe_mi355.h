@@ -103,7 +103,7 @@ typedef struct moe_mi355_args {
 
 /* Call flags (moe_mi355_args.flags).  Without any, the library picks its kernel plan
  * from T alone; nothing else (no environment variable) changes it.
- *   MOE_MI355_FLAG_PROFILE         record per-stage HIP events (moe_mi355_profile_*)
+ *   MOE_MI355_FLAG_PROFILE         time each kernel with HIP events (moe_mi355_profile_*)
  *   MOE_MI355_FLAG_FORCE_PLAN      run the GEMM1 / GEMM2 variant pair in bits 8-11 /
  *                                  12-15 (MOE_MI355_FLAGS_PLAN(g1, g2)); for tuning
  *                                  sweeps and tests.  GEMM1: 1 streaming 16-row tiles,
@@ -269,12 +269,15 @@ typedef struct moe_mi355_workspace_layout {
 MOE_MI355_API int moe_mi355_get_workspace_layout(int32_t T, int32_t flags,
                                                  moe_mi355_workspace_layout* out);
 
-/* Stage profiler: with MOE_MI355_FLAG_PROFILE set, each forward call records HIP
- * events around each of its kernels into a ring of `max_calls` slots.
- * moe_mi355_profile_read synchronises those events and writes the average
- * duration in milliseconds of each stage over the recorded calls into
- * stage_ms[0..n) (stage order: route, dispatch, gemm1, gemm2, combine) and
- * returns the number of calls averaged. */
+/* Stage profiler: with MOE_MI355_FLAG_PROFILE set, each forward call (up to
+ * `max_calls` of them) times each of its kernels with a pair of HIP events that the
+ * runtime stamps at the kernel's own start and end (hipExtLaunchKernelGGL), so the
+ * gaps between kernels are not counted.  moe_mi355_profile_read synchronises those
+ * events and writes, for each stage, the sum of its kernels' durations in
+ * milliseconds averaged over the recorded calls into stage_ms[0..n) (stage order:
+ * route, dispatch (with the token-scale gather), gemm1, gemm2 (with the conversion of
+ * C, and the combine when GEMM2 computes it), combine) and returns the number of
+ * calls averaged.  A stage without a kernel in the call's plan reads 0. */
 MOE_MI355_API int moe_mi355_profile_begin(int32_t max_calls);
 MOE_MI355_API int moe_mi355_profile_read(float* stage_ms, int32_t n);
 MOE_MI355_API int moe_mi355_profile_end(void);
