@@ -2,17 +2,20 @@
 // the launch sequence and a small stage profiler.
 //
 // Replaces the host orchestration of the reference (solution/python/main.cpp:66-266):
-// there ~16 launches and ~20 torch allocations per call; here five launches on the
-// caller's stream over one caller-provided workspace, no host synchronisation and no
+// there ~16 launches and ~20 torch allocations per call; here three to eight launches on
+// the caller's stream over one caller-provided workspace, no host synchronisation and no
 // allocation:
 //   route    (T/4 workgroups)      -> topk ids / weights
-//   dispatch (1 workgroup)         -> expert offsets, row tiles, permutation, inverse map
+//   dispatch (1 workgroup, or count + place kernels; inside GEMM1 for T <= 64)
+//                                  -> expert offsets, row tiles, permutation, inverse map
+//   (gather  -> token scales in row order, for the plans that read them so)
 //   gemm1    (persistent)          -> SwiGLU rows C      [N_a, 2048] (fp16 or fp8 hi/lo)
 //   (cform   (persistent)          -> fp16 C as hi/lo, for the plans that need it)
 //   gemm2    (persistent)          -> fp16 expert rows   [N_a, 7168]
-//   combine  (7 T workgroups)      -> bf16 output        [T, 7168]
+//   combine  (7 T workgroups; inside GEMM2 for T <= 32) -> bf16 output [T, 7168]
 // The GEMM grids are sized from the host-known bound on the tile count; each
-// workgroup reads the real count written by dispatch and exits when it runs out.
+// workgroup reads the real count written by dispatch and exits when it runs out.  The
+// plan, the workspace layout and the argument checks are host_plan.h's.
 
 #include <stdio.h>
 #include <stdlib.h>
