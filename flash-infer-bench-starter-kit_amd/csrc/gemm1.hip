@@ -212,6 +212,13 @@ __device__ __forceinline__ void gemm1_shared_item(
 
 // WPE: the waves per SIMD the register allocation is held to (1: the compiler's choice,
 // 172 registers, two workgroups per CU; 3: 153 registers, three).
+// With three per CU the kernel chooses, from the call's tile count, how many of its 768
+// workgroups work: items are equal (an item streams 128 weight rows over all of K), so the
+// rounds decide the time, and 768 < items <= 1024 takes two rounds either way, where two
+// workgroups per CU run each item faster; then workgroups 512 .. 767 exit at once and the
+// other 512 (two per CU, the workgroups being spread over the CUs in launch order) take
+// the items.  Otherwise all 768 work (fewer rounds).  Which workgroup computes an item
+// changes nothing in the result.
 template <int D, int NWV, int WPE>
 __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(WPE))) void gemm1_shared_kernel(
     const uint8_t* __restrict__ hidden, TokenScales sa, int T,
@@ -225,7 +232,10 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(WPE)))
     const __amdgpu_buffer_rsrc_t rs_h = buffer_rsrc(hidden, (uint32_t)T * kH);
     const __amdgpu_buffer_rsrc_t rs_s = buffer_rsrc(sa.p, (uint32_t)kHB * (uint32_t)sa.stride * 4);
     const int nwork = (*num_tiles) * S::kItems;
-    for (int work = blockIdx.x; work < nwork; work += gridDim.x) {
+    int G = gridDim.x;
+    if (WPE == 3 && G == 768 && nwork > 768 && nwork <= 1024) G = 512;
+    if ((int)blockIdx.x >= G) return;   // uniform: the whole workgroup
+    for (int work = blockIdx.x; work < nwork; work += G) {
         const int4 tile = tiles[work / S::kItems];
         const int ng = (work % S::kItems) * NWV + wave;
         with_live_blocks(live_blocks(0, tile.z), [&](auto live) {

@@ -31,15 +31,14 @@ constexpr int kMinTileM = 16;           // smallest row tile; sizes the tile lis
 // Small T streams weights with the register-staged kernels, C in fp16: 16-row tiles up
 // to T = 88, 32-row tiles (GEMM1 with two column groups per wave, GEMM2 with two row
 // blocks per wave) beyond.  From T = 300 GEMM1 is the token-sharing kernel on 64-row
-// tiles (fewer requests per output once an expert has dozens of rows), feeding the
-// prefill GEMM2 (128-row tiles, FP8 MFMA on the hi/lo form): up to T = 960 with three
-// workgroups per CU (variant 8), then with two (variant 7), whose fewer resident
-// workgroups split the items of the larger tile lists into better-filled rounds; from
-// T = 1345 both GEMMs are the MFMA-bound prefill kernels on 256-row tiles (GEMM2 on the
-// 128-row second list).  The boundaries come from wall-clock sweeps of the pairs at
-// T = 72 .. 2560 on MI355X over five routing seeds (light to heavy routing to the local
-// experts): between T = 960 and 1344 the best pair depends on the routing (heavy routing
-// prefers the prefill pair, light routing the token-sharing one).
+// tiles (fewer requests per output once an expert has dozens of rows; variant 8, which
+// runs three or two workgroups per CU as the call's tile count makes best), feeding the
+// prefill GEMM2 (128-row tiles, FP8 MFMA on the hi/lo form); from T = 1345 both GEMMs are
+// the MFMA-bound prefill kernels on 256-row tiles (GEMM2 on the 128-row second list).  The
+// boundaries come from wall-clock sweeps of the pairs at T = 72 .. 2560 on MI355X over
+// routing seeds from light to heavy routing to the local experts.  Between T = 961 and
+// 1344 variant 8 was 6-25 us faster than variant 7 (always two per CU) on three routings
+// and 4-10 us slower on three; heavier routing there can prefer the prefill pair.
 struct Plan {
     int tm;        // tile height of the first list
     int tm2;       // tile height of the second list (0: none)
@@ -113,8 +112,7 @@ inline int plan_for(int32_t T, int32_t flags, Plan* p) {
     else if (T <= kDispatchInGemm1MaxT && !on) g1 = 5, g2 = 1;
     else if (T <= 88) g1 = 1, g2 = 1;
     else if (T <= 299) g1 = 2, g2 = 3;
-    else if (T <= 960) g1 = 8, g2 = 5;
-    else if (T <= 1344) g1 = 7, g2 = 5;
+    else if (T <= 1344) g1 = 8, g2 = 5;
     else g1 = 4, g2 = 5;
     if (flags & MOE_MI355_FLAG_FORCE_PLAN) {
         g1 = MOE_MI355_FLAGS_G1(flags);

@@ -109,8 +109,10 @@ typedef struct moe_mi355_args {
  *                                  sweeps and tests.  GEMM1: 1 streaming 16-row tiles,
  *                                  2 streaming 32-row tiles, 4 prefill 256-row tiles,
  *                                  7 streaming with shared token rows, 64-row tiles
- *                                  (pairs with GEMM2 5 only), 8 the same with three
- *                                  workgroups per CU instead of two;
+ *                                  (pairs with GEMM2 5 only), two workgroups per CU,
+ *                                  8 the same held to three per CU, of which it runs
+ *                                  three or two by the call's tile count (the default
+ *                                  for 300 <= T <= 1344);
  *                                  GEMM2: 1 streaming 16-row, 3 streaming 32-row,
  *                                  5 prefill on a second list of 128-row tiles.  A pair
  *                                  that cannot run together, or an unknown variant,
