@@ -143,9 +143,19 @@ __device__ __forceinline__ void gemm1_rstream_item(
         const int n = (rr < 16) ? (ng + gi) * 16 + rr : kI + (ng + gi) * 16 + (rr - 16);
         wsrc[i] = w1 + (size_t)(le * kN1 + n) * kH + dchunk * 16;
     }
-    // the NGRP groups lie in one 128-column scale block (16 NGRP divides 128)
+    // the NGRP groups lie in one 128-column scale block (16 NGRP divides 128).  The
+    // wave's KB gate and up scales are loaded here, ahead of its first weight loads:
+    // loaded in the K loop, the first of them would come due at the first K block's LDS
+    // accesses, which wait for every scalar load in flight.
     const float* sg = s1 + (size_t)(le * kN1B + (ng >> 3)) * kHB;
     const float* su = sg + (size_t)kIB * kHB;
+    float wgv[KB], wuv[KB];
+#pragma unroll
+    for (int k = 0; k < KB; ++k) {
+        wgv[k] = sg[kb0 + k];
+        wuv[k] = su[kb0 + k];
+    }
+    __builtin_amdgcn_sched_barrier(0);
 
     v4u bw[D][NW];
     v4u bt[D][2 * CB];
@@ -208,8 +218,7 @@ __device__ __forceinline__ void gemm1_rstream_item(
                 ba[c] = v8i{(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3], (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
             }
         }
-        const int kb = kb0 + k;
-        const float wg = sg[kb], wu = su[kb];
+        const float wg = wgv[k], wu = wuv[k];
 #pragma unroll
         for (int gi = 0; gi < NGRP; ++gi) {
             const uint8_t* gs = slot + gi * 32 * kBlk;

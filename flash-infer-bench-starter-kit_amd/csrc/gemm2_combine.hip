@@ -16,8 +16,10 @@
 // moved to the MFMA layout through the wave's LDS slot, and fp16 C fragments), so the
 // loads of the next tile are in flight while this one computes.  After every 4 tiles the
 // waves add the 4 K partials of a tile each (waves 0, 1, 2, 3 in that order) and keep
-// the rows in LDS.  The token's routing weights and inverse row map come in by LDS DMA
-// at kernel start.  224 workgroups stream the same bytes per CU as the separate GEMM2
+// the rows in LDS.  The token's routing weights, the inverse row map and the tile list
+// come in by LDS DMA at kernel start, and each step's W2 block scale with the step's
+// loads, so the loop issues no scalar load (an LDS access waits for every scalar load
+// in flight, as both count on one counter).  224 workgroups stream the same bytes per CU as the separate GEMM2
 // (448 items of 32 columns over 256 CUs); the LDS holds the rows of up to
 // kFusedCombineMaxT tokens.  Two groups of 4 waves take alternate tiles, so the
 // workgroup has as many waves in flight as two of the separate GEMM2's.
@@ -42,13 +44,15 @@ __global__ __launch_bounds__(256 * NG, 1) void gemm2_combine_kernel(
     constexpr int HF = 2, KSPLIT = 4, KB = kIB / KSPLIT, D = KB;
     constexpr int NW = KSPLIT * NG;           // waves
     constexpr int CH = 4 * NG;                // tiles per reduction round (4 per group)
-    constexpr int kVmPerStep = 2 * HF + 4;    // W2 loads, C loads of one (tile, K block)
+    constexpr int kVmPerStep = 2 * HF + 5;    // W2 loads, C loads, block scale of one (tile, K block)
+    static_assert(HF == 2, "the HF column groups of a workgroup share one W2 scale block");
     // flags[0]: C beyond the fp16 range (set by GEMM1); flags[1]: an expert row beyond it
     __shared__ __attribute__((aligned(1024))) uint8_t slot_lds[NW][16 * HF * kBlk];
     __shared__ v4f red[KSPLIT][CH][HF][64];          // K partials of one round of tiles
     __shared__ float o_lds[kFusedRows][kFusedCols];  // expert rows (as the combine reads them)
     __shared__ int s_inv[kFusedRows];
     __shared__ float s_w[kFusedRows];
+    __shared__ int4 s_tiles[64];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -57,12 +61,13 @@ __global__ __launch_bounds__(256 * NG, 1) void gemm2_combine_kernel(
     const int drow = lane >> 3, dchunk = lane & 7;
     const int hg = blockIdx.x * HF;                  // first 16-column group
     const v4f zero = {0.f, 0.f, 0.f, 0.f};
-    const int nt = __builtin_amdgcn_readfirstlane(*num_tiles);
     const int R = T * kTopK;
 
-    // the routing weights of the rows and the inverse map, straight into LDS (they are
-    // read by the combine at the end; the waits of the K loop or the barrier before
-    // the combine cover them)
+    // Straight into LDS: the routing weights of the rows and the inverse map (read by
+    // the combine at the end; the waits of the K loop or the barrier before the combine
+    // cover them), and the whole tile list as far as the workspace holds it (the last
+    // wave; waited for below).  A tile read from LDS keeps the K loop free of scalar
+    // loads, whose completion every LDS access after them would wait for.
     {
         const __amdgpu_buffer_rsrc_t rs_inv = buffer_rsrc(inv, (uint32_t)R * 4);
         const __amdgpu_buffer_rsrc_t rs_w = buffer_rsrc(sorted_w, (uint32_t)R * 4);
@@ -70,11 +75,18 @@ __global__ __launch_bounds__(256 * NG, 1) void gemm2_combine_kernel(
             bdma4(rs_inv, (uint32_t)(b + lane) * 4, 0, s_inv + b);
             bdma4(rs_w, (uint32_t)(b + lane) * 4, 0, s_w + b);
         }
+        if (wave == NW - 1) {
+            const __amdgpu_buffer_rsrc_t rs_t = buffer_rsrc(tiles, (uint32_t)dispatch_max_tiles(T, 16) * 16);
+            bdma16(rs_t, (uint32_t)lane * 16, 0, s_tiles);
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        }
     }
+    const int nt = __builtin_amdgcn_readfirstlane(*num_tiles);
+    __syncthreads();   // the tile list is in LDS
 
-    // tile t: local expert, first row, rows (scalar loads of the dispatch's list)
+    // tile t: local expert, first row, rows
     auto tile_of = [&](int t) {
-        const int4 tl = tiles[t];
+        const int4 tl = s_tiles[t];
         return int4{__builtin_amdgcn_readfirstlane(tl.x), __builtin_amdgcn_readfirstlane(tl.y),
                     __builtin_amdgcn_readfirstlane(tl.z), 0};
     };
@@ -132,6 +144,10 @@ __global__ __launch_bounds__(256 * NG, 1) void gemm2_combine_kernel(
         }
         v4u bw[D][2 * HF];
         v4u bc[D][4];
+        float bsc[D];
+        // the W2 block scale of a step comes with its loads (a vector load: it is waited
+        // for with them), so the loop reads no scale through the scalar cache
+        const __amdgpu_buffer_rsrc_t rs_s2 = buffer_rsrc(s2, (uint32_t)(kEL * kHB * kIB * 4));
         auto issue = [&](const int4& tl, int j) {   // tile tl, K block 4 ks + j -> slot j
             const int kb = ks * KB + j;
 #pragma unroll
@@ -142,6 +158,8 @@ __global__ __launch_bounds__(256 * NG, 1) void gemm2_combine_kernel(
             const uint8_t* cp = reinterpret_cast<const uint8_t*>(C.f16() + (size_t)(tl.y + min(r16, tl.z - 1)) * kI) + kq * 64;
 #pragma unroll
             for (int q = 0; q < 4; ++q) bc[j][q] = *reinterpret_cast<const v4u*>(cp + kb * 2 * kBlk + 16 * q);
+            bsc[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                rs_s2, (uint32_t)(((tl.x * kHB + (hg >> 3)) * kIB + kb) * 4), 0, 0));
         };
         const int nsteps = nt_g * D;
         int4 cur = nt_g > 0 ? tile_of(grp) : int4{0, 0, 1, 0};
@@ -172,7 +190,6 @@ __global__ __launch_bounds__(256 * NG, 1) void gemm2_combine_kernel(
                     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                     for (int q = 0; q < 2 * HF; ++q) *reinterpret_cast<v4u*>(slot + wr[q]) = bw[j][q];
-                    const int kb = ks * KB + j;
 #pragma unroll
                     for (int hf = 0; hf < HF; ++hf) {
                         const v4u x0 = *reinterpret_cast<const v4u*>(slot + hf * 16 * kBlk + rd0);
@@ -181,9 +198,8 @@ __global__ __launch_bounds__(256 * NG, 1) void gemm2_combine_kernel(
                         v4f tp = zero;
 #pragma unroll
                         for (int q = 0; q < 4; ++q) tp = mfma_w2_c<true>(ww[2 * q], ww[2 * q + 1], bc[j][q], tp);
-                        const float sb = s2[(size_t)(cur.x * kHB + ((hg + hf) >> 3)) * kIB + kb];
 #pragma unroll
-                        for (int v = 0; v < 4; ++v) acc[hf][v] = __builtin_fmaf(tp[v], sb, acc[hf][v]);
+                        for (int v = 0; v < 4; ++v) acc[hf][v] = __builtin_fmaf(tp[v], bsc[j], acc[hf][v]);
                     }
                     __builtin_amdgcn_sched_barrier(0);
                 }

@@ -136,9 +136,17 @@ __device__ __forceinline__ void gemm2_rstream_item(
 #pragma unroll
     for (int i = 0; i < 2 * HF; ++i)
         wsrc[i] = w2 + (size_t)(le * kH + hg * 16 + 8 * i + drow) * kI + dchunk * 16;
-    const float* sp[HF];
+    // the wave's block scales, loaded ahead of its first W2 loads (in the K loop the first
+    // would come due at the first K block's LDS accesses, which wait for every scalar
+    // load in flight)
+    float sbv[HF][KB];
 #pragma unroll
-    for (int hf = 0; hf < HF; ++hf) sp[hf] = s2 + (size_t)(le * kHB + ((hg + hf) >> 3)) * kIB;
+    for (int hf = 0; hf < HF; ++hf) {
+        const float* sp = s2 + (size_t)(le * kHB + ((hg + hf) >> 3)) * kIB;
+#pragma unroll
+        for (int k = 0; k < KB; ++k) sbv[hf][k] = sp[kb0 + k];
+    }
+    __builtin_amdgcn_sched_barrier(0);
 
     v4u bw[D][2 * HF];
     v4u bc[D][CB][4];
@@ -191,7 +199,7 @@ __device__ __forceinline__ void gemm2_rstream_item(
             for (int j = 0; j < 4; ++j)
 #pragma unroll
                 for (int c = 0; c < CB; ++c) t[c] = mfma_w2_c<true>(ww[2 * j], ww[2 * j + 1], bc[k % D][c][j], t[c]);
-            const float sb = sp[hf][kb0 + k];
+            const float sb = sbv[hf][k];
 #pragma unroll
             for (int c = 0; c < CB; ++c)
 #pragma unroll
