@@ -56,13 +56,11 @@ __device__ __forceinline__ TokenRoutes load_routes(const int* __restrict__ topk_
     return r;
 }
 
-// For each expert e: the wave's count into wcnt[wave][e]; returns in rank[k] this
-// lane's rank among the wave's lanes holding expert lek[k].  One ballot per expert;
-// lane e keeps expert e's ballot and writes it to the wave's table bal[kEL] in LDS,
-// from which every lane reads the ballots of its own experts.  The table is written
-// and read by the same wave only (LDS operations of a wave complete in order).
-__device__ __forceinline__ void wave_ranks(const TokenRoutes& r, int wave, int lane,
-                                           int (*wcnt)[kEL], uint64_t* bal, int* rank) {
+// For each expert e: the wave's ballot of the lanes routed to it into bal[e] and their
+// count into wcnt[wave][e] (LDS).  One ballot per expert; lane e keeps expert e's
+// ballot and writes it.
+__device__ __forceinline__ void wave_ballots(const TokenRoutes& r, int wave, int lane,
+                                             int (*wcnt)[kEL], uint64_t* bal) {
     uint64_t mine = 0;
 #pragma unroll
     for (int e = 0; e < kEL; ++e) {
@@ -73,6 +71,16 @@ __device__ __forceinline__ void wave_ranks(const TokenRoutes& r, int wave, int l
         bal[lane] = mine;
         wcnt[wave][lane] = __popcll(mine);
     }
+}
+
+// For each expert e: the wave's count into wcnt[wave][e]; returns in rank[k] this
+// lane's rank among the wave's lanes holding expert lek[k].  The wave's ballot table
+// bal[kEL] (wave_ballots, LDS) is written and read by the same wave only (LDS
+// operations of a wave complete in order): every lane reads the ballots of its own
+// experts.
+__device__ __forceinline__ void wave_ranks(const TokenRoutes& r, int wave, int lane,
+                                           int (*wcnt)[kEL], uint64_t* bal, int* rank) {
+    wave_ballots(r, wave, lane, wcnt, bal);
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int k = 0; k < kTopK; ++k) {

@@ -44,7 +44,8 @@ __global__ __launch_bounds__(256) void gemm1_rstream_kernel(
     for (int work = blockIdx.x; work < nwork; work += gridDim.x) {
         const int4 tile = tiles[work / S::kItems];
         gemm1_rstream_item<D, CB, NGRP, TL>(hidden, sa, w1, s1, tile.x, tile.y, tile.z,
-                                            (work % S::kItems) * NGRP, sorted_tok, C, c_wide,
+                                            (work % S::kItems) * NGRP,
+                                            [&](int row) { return sorted_tok[row]; }, C, c_wide,
                                             slot_lds, red, wave);
     }
 }
@@ -249,13 +250,18 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(WPE)))
 }
 
 // The streaming GEMM1 of variant 1 with the dispatch folded in, for T <= 64: every
-// workgroup of a persistent grid computes the call's dispatch from the routing ids
-// (dispatch_wave: one wave, a token per lane, into LDS) and takes its work items from
-// that tile list; workgroup 0 also writes the dispatch (offsets, tile count and list,
-// permutation, row weights, inverse map) to the workspace, where the GEMM2 and combine
-// kernels after it read it.  The dispatch launch goes away; the dispatch itself costs a
-// workgroup about what the separate kernel's two dependent loads (tile list, then
-// permutation) cost before its first weight load.
+// workgroup of a persistent grid computes the part of the call's dispatch its items need,
+// into LDS.  Wave 0 takes one ballot per local expert over the tokens (lane = token),
+// which gives each expert's row count, the tile list, and each row's rank among the
+// expert's rows (rows follow token order); then all four waves place the tokens of the
+// rows, two of each token's eight routes per wave.  The last workgroup, which has the
+// fewest items (none up to T = 32), also writes the whole dispatch to the workspace
+// (expert offsets, tile count and list, permutation, row weights, inverse map), where
+// the GEMM2 and combine kernels after this one read it.  Workgroup b takes items b,
+// b + G, ..., so the items of an expert's consecutive tiles that read the same weight
+// rows (128 items apart) run on one XCD.  The dispatch launch goes away; the part of the
+// dispatch before the first weight load costs a workgroup about what the separate
+// kernel's two dependent loads (tile list, then permutation) cost.
 constexpr int kDG1MaxTiles = dispatch_max_tiles(kDispatchInGemm1MaxT, 16);   // 64
 
 __global__ __launch_bounds__(256) void gemm1_rstream_dispatch_kernel(
@@ -272,34 +278,59 @@ __global__ __launch_bounds__(256) void gemm1_rstream_dispatch_kernel(
     __shared__ int s_num_tiles;
     __shared__ int4 s_tiles[kDG1MaxTiles];
     __shared__ int s_stok[R];
-    __shared__ float s_sw[R];
-    __shared__ int s_inv[R];
+    __shared__ int8_t s_lek[kDispatchInGemm1MaxT][kTopK];
+    __shared__ float s_wk[kDispatchInGemm1MaxT][kTopK];
     __shared__ DispatchWaveLds s_dw;
     const int tid = threadIdx.x;
+    const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    if (wave == 0)
-        dispatch_wave<16>(topk_ids, topk_w, T, offset, tid & 63, s_dw, s_exp_off, &s_num_tiles,
-                          s_tiles, s_stok, s_sw, s_inv);
+    const bool writer = blockIdx.x == gridDim.x - 1;
+    if (wave == 0) {
+        const TokenRoutes r = load_routes(topk_ids, topk_w, lane, T, offset);
+        wave_ballots(r, 0, lane, s_dw.wcnt, s_dw.bal);
+#pragma unroll
+        for (int k = 0; k < kTopK; ++k) {
+            s_lek[lane][k] = (int8_t)r.lek[k];
+            s_wk[lane][k] = r.wk[k];
+        }
+        __builtin_amdgcn_wave_barrier();
+        write_offsets_and_tiles<16, 0>(lane < kEL ? s_dw.wcnt[0][lane] : 0, lane, s_dw.off,
+                                       s_exp_off, &s_num_tiles, s_tiles, nullptr, nullptr);
+    }
     __syncthreads();
     const int ntiles = s_num_tiles;
-    if (blockIdx.x == 0) {
-        const int na = s_exp_off[kEL];
+    if (lane < T) {   // token lane: its routes 2 wave and 2 wave + 1
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            const int k = 2 * wave + kk;
+            const int le = s_lek[lane][k];
+            int row = -1;
+            if (le >= 0) {
+                const uint64_t b = s_dw.bal[le];
+                row = s_exp_off[le] + (int)__builtin_amdgcn_mbcnt_hi(
+                                          (uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+                s_stok[row] = lane;
+                if (writer) {
+                    sorted_tok[row] = lane;
+                    sorted_w[row] = s_wk[lane][k];
+                }
+            }
+            if (writer) inv[lane * kTopK + k] = row;
+        }
+    }
+    if (writer) {
         for (int i = tid; i <= kEL; i += 256) meta[i] = s_exp_off[i];
         if (tid == 0) meta[kEL + 1] = ntiles;
         for (int i = tid; i < ntiles; i += 256) tiles[i] = s_tiles[i];
-        for (int i = tid; i < na; i += 256) {
-            sorted_tok[i] = s_stok[i];
-            sorted_w[i] = s_sw[i];
-        }
-        for (int i = tid; i < T * kTopK; i += 256) inv[i] = s_inv[i];
     }
+    __syncthreads();
     const TokenScales sa{hs_scale, T, 0};
     const int nwork = ntiles * S::kItems;
     for (int work = blockIdx.x; work < nwork; work += gridDim.x) {
         const int4 tile = s_tiles[work / S::kItems];
         gemm1_rstream_item<4, 1, 1, false>(hidden, sa, w1, s1, tile.x, tile.y, tile.z,
-                                           work % S::kItems, s_stok, C, meta + kCWideFlag,
-                                           slot_lds, red, wave);
+                                           work % S::kItems, [&](int row) { return s_stok[row]; },
+                                           C, meta + kCWideFlag, slot_lds, red, wave);
     }
 }
 

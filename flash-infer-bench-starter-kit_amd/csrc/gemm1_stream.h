@@ -79,14 +79,14 @@ struct Gemm1Stream {
 };
 
 // One work item of the streaming GEMM1: row tile (local expert le, rows row0 ..
-// row0 + nrows - 1, whose tokens sorted_tok[row] gives) x the NGRP groups of 16 SwiGLU
+// row0 + nrows - 1, whose tokens tok_of(row) gives) x the NGRP groups of 16 SwiGLU
 // columns from ng on.  The 4 waves of the workgroup take 14 K blocks each and reduce
 // through red[] in a fixed order; wave 0 writes the rows of C.
-template <int D, int CB, int NGRP, bool TL>
+template <int D, int CB, int NGRP, bool TL, class TokOf>
 __device__ __forceinline__ void gemm1_rstream_item(
     const uint8_t* __restrict__ hidden, const TokenScales& sa, const uint8_t* __restrict__ w1,
     const float* __restrict__ s1, int le, int row0, int nrows, int ng,
-    const int* __restrict__ sorted_tok, const Intermediate& C, int* __restrict__ c_wide,
+    const TokOf& tok_of, const Intermediate& C, int* __restrict__ c_wide,
     uint8_t (*slot_lds)[Gemm1Stream<CB, NGRP, TL>::kSlot], v4f (*red)[2][NGRP * CB][64], int wave) {
     constexpr int KSPLIT = 4;
     constexpr int KB = kHB / KSPLIT;                  // 14 K blocks per wave
@@ -125,14 +125,14 @@ __device__ __forceinline__ void gemm1_rstream_item(
     uint32_t toff[2 * CB];
 #pragma unroll
     for (int i = 0; i < 2 * CB; ++i) {
-        if (TL) toff[i] = (uint32_t)sorted_tok[row0 + min(8 * i + drow, nrows - 1)] * kH + dchunk * 16;
-        else if (i < CB) toff[i] = (uint32_t)sorted_tok[row0 + min(16 * i + r16, nrows - 1)] * kH + kq * 32;
+        if (TL) toff[i] = (uint32_t)tok_of(row0 + min(8 * i + drow, nrows - 1)) * kH + dchunk * 16;
+        else if (i < CB) toff[i] = (uint32_t)tok_of(row0 + min(16 * i + r16, nrows - 1)) * kH + kq * 32;
     }
     const float* sp[CB];
 #pragma unroll
     for (int c = 0; c < CB; ++c) {
         const int row = row0 + min(16 * c + r16, nrows - 1);
-        sp[c] = sa.p + (sa.by_row ? row : sorted_tok[row]);
+        sp[c] = sa.p + (sa.by_row ? row : tok_of(row));
     }
     // slot rows 32 gi + 0..15: gate rows of group ng + gi, 32 gi + 16..31: its up rows
     const uint8_t* wsrc[NW];
