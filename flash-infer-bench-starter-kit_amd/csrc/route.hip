@@ -7,8 +7,9 @@
 //
 // Layout on the wave: lane l owns experts 4l..4l+3, so group g = l/8 lives on
 // lanes 8g..8g+7.  Scores travel as order-preserving 32-bit images of fp32;
-// reductions use DPP (quad permutes and row shifts), and ties between equal scores
-// are broken toward the lower expert with a ballot.
+// reductions and exchanges use DPP (quad permutes, row rotations) and the lane-swap
+// instructions v_permlane16_swap / v_permlane32_swap, so every lane holds their results,
+// and ties between equal scores are broken toward the lower expert with a ballot.
 //
 // The sigmoid is evaluated in binary64 with an exp built from IEEE operations only
 // (Cody-Waite reduction, degree-13 Taylor polynomial, explicit fma) and rounded
@@ -58,18 +59,6 @@ __device__ __forceinline__ float canon_sigmoid(float x) {
 
 // ---- cross-lane helpers (DPP; identity 0 for unsigned max) ------------------
 
-// max over the whole wave, result uniform (in an SGPR)
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, false));  // row_shr:1
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, false));  // row_shr:2
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x113, 0xf, 0xf, false));  // row_shr:3
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xe, false));  // row_shr:4
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xc, false));  // row_shr:8
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false));  // row_bcast:15
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false));  // row_bcast:31
-    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
-}
-
 // value of lane i^1, i^2 (quad permutes) and i^4 (swap of the two quads of an octet)
 __device__ __forceinline__ uint32_t xor1(uint32_t v) {
     return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xb1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
@@ -81,6 +70,36 @@ __device__ __forceinline__ uint32_t xor4(uint32_t v) {
     // banks 0,2 (lanes 0-3, 8-11 of a row) read lane+4; banks 1,3 read lane-4
     const int a = __builtin_amdgcn_update_dpp((int)v, (int)v, 0x104, 0xf, 0x5, false);  // row_shl:4
     return (uint32_t)__builtin_amdgcn_update_dpp(a, (int)v, 0x114, 0xf, 0xa, false);     // row_shr:4
+}
+
+// value of lane i^8 (rotation by 8 inside each row of 16 lanes)
+__device__ __forceinline__ uint32_t xor8(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xf, 0xf, false);  // row_ror:8
+}
+// value of lane i^16 and i^32: v_permlane16_swap / v_permlane32_swap of v with itself
+// leave the value of the partner row (half) in the second result for even rows (the
+// lower half) and in the first for odd rows (the upper half)
+__device__ __forceinline__ uint32_t xor16(uint32_t v, int lane) {
+    const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return ((lane >> 4) & 1) ? p[0] : p[1];
+}
+__device__ __forceinline__ uint32_t xor32(uint32_t v, int lane) {
+    const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (lane >> 5) ? p[0] : p[1];
+}
+
+// max over the whole wave, held in every lane: quad exchanges, rotations by 4 and 8
+// inside each row, then the row and half swaps (each lane meets every other lane's
+// value; no lane reads past its row)
+__device__ __forceinline__ uint32_t wave_max_all(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xb1, 0xf, 0xf, false));   // quad_perm [1,0,3,2]
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4e, 0xf, 0xf, false));   // quad_perm [2,3,0,1]
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x124, 0xf, 0xf, false));  // row_ror:4
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xf, 0xf, false));  // row_ror:8
+    auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    v = max((uint32_t)p[0], (uint32_t)p[1]);
+    p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return max((uint32_t)p[0], (uint32_t)p[1]);
 }
 
 // merge (a1 >= a2) with the pair of another lane: the two largest of the four
@@ -125,56 +144,71 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
     top2_merge(a1, a2, xor4(a1), xor4(a2));
     const float gscore = order_bits_inv(a1) + order_bits_inv(a2);
 
-    // keep the 4 best groups, ties to the lower group (kernel.cu:96-115); the group
-    // scores are wave-uniform after the read-lanes
+    // keep the 4 best groups, ties to the lower group (kernel.cu:96-115): every lane of
+    // the octet of group g holds its score; an xor butterfly over the octets gives each
+    // lane all eight (gk[j]: group g ^ j), and the lane ranks its own group against them
+    // (a group beats it with a larger score, or an equal one at a lower index).  The kept
+    // groups are those ranked 0..3, the set that four picks of the best remaining group,
+    // ties to the lower, select.
+    const int g = lane >> 3;
     uint32_t gk[kNGroup];
+    gk[0] = order_bits(gscore);
+    gk[1] = xor8(gk[0]);
+    gk[2] = xor16(gk[0], lane);
+    gk[3] = xor16(gk[1], lane);
 #pragma unroll
-    for (int g = 0; g < kNGroup; ++g)
-        gk[g] = order_bits(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(gscore), 8 * g)));
-    // lane l ranks group l % 8 against all eight (a group beats it with a larger score,
-    // or an equal one at a lower index); the kept groups are those ranked 0..3, which is
-    // the set that four picks of the best remaining group, ties to the lower, select
-    const int mg = lane & (kNGroup - 1);
-    uint32_t mine = gk[0];
-#pragma unroll
-    for (int g = 1; g < kNGroup; ++g) mine = (mg == g) ? gk[g] : mine;
+    for (int j = 0; j < 4; ++j) gk[4 + j] = xor32(gk[j], lane);
     int rank = 0;
 #pragma unroll
-    for (int g = 0; g < kNGroup; ++g) rank += (gk[g] > mine || (gk[g] == mine && g < mg)) ? 1 : 0;
-    const uint32_t keep = (uint32_t)__ballot(lane < kNGroup && rank < kTopKGroup) & ((1u << kNGroup) - 1u);
+    for (int j = 1; j < kNGroup; ++j)
+        rank += (gk[j] > gk[0] || (gk[j] == gk[0] && (g ^ j) < g)) ? 1 : 0;
+    const bool kept = rank < kTopKGroup;
 
     // top-8 (moe.cu:198-200): candidate key = orderable score + 1 for kept experts,
-    // 1 for pruned ones, 0 once taken.  Per round the wave maximum is found with DPP,
-    // the lowest lane holding it with a ballot, and that lane's lowest slot with it;
-    // lane l holds experts 4l..4l+3, so this is the lowest expert index.
-    const bool kept = ((keep >> (lane >> 3)) & 1u) != 0u;
+    // 1 for pruned ones, 0 once taken.  Per round the wave maximum is found with DPP and
+    // lane swaps (held in every lane), the lowest lane holding it with a ballot, and that
+    // lane's lowest slot with it; lane l holds experts 4l..4l+3, so this is the lowest
+    // expert index.  The owner notes the round in the slot; the picks are gathered in
+    // round order through LDS afterwards.
     uint32_t ck[4];
+    int round_of[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) ck[j] = kept ? key[j] + 1u : 1u;
-
-    int my_id = 0;
-    float my_s = 0.0f;
-    float ssel[kTopK];
+    for (int j = 0; j < 4; ++j) {
+        ck[j] = kept ? key[j] + 1u : 1u;
+        round_of[j] = -1;
+    }
 #pragma unroll
     for (int j = 0; j < kTopK; ++j) {
         const uint32_t lm = max(max(ck[0], ck[1]), max(ck[2], ck[3]));
-        const uint32_t m = wave_max_u32(lm);
-        const uint64_t holders = __ballot(lm == m);
-        const int owner = (int)__builtin_ctzll(holders);
+        const uint32_t m = wave_max_all(lm);
+        const int owner = (int)__builtin_ctzll(__ballot(lm == m));
         int sub = 3;
 #pragma unroll
         for (int q = 2; q >= 0; --q) sub = (ck[q] == m) ? q : sub;
-        float sp = s[0];
+        const bool own = lane == owner;
 #pragma unroll
-        for (int q = 1; q < 4; ++q) sp = (sub == q) ? s[q] : sp;
-        const int osub = __builtin_amdgcn_readlane(sub, owner);
-        const float se = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sp), owner));
-#pragma unroll
-        for (int q = 0; q < 4; ++q) ck[q] = (lane == owner && q == osub) ? 0u : ck[q];
-        ssel[j] = se;
-        my_id = (lane == j) ? 4 * owner + osub : my_id;
-        my_s = (lane == j) ? se : my_s;
+        for (int q = 0; q < 4; ++q) {
+            const bool take = own && q == sub;
+            ck[q] = take ? 0u : ck[q];
+            round_of[q] = take ? j : round_of[q];
+        }
     }
+    __shared__ float s_sel[4][kTopK];
+    __shared__ int s_sel_id[4][kTopK];
+    const int wv = threadIdx.x >> 6;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        if (round_of[q] >= 0) {
+            s_sel[wv][round_of[q]] = s[q];
+            s_sel_id[wv][round_of[q]] = 4 * lane + q;
+        }
+    }
+    __builtin_amdgcn_wave_barrier();   // the wave's LDS writes before its reads (in order)
+    float ssel[kTopK];
+#pragma unroll
+    for (int j = 0; j < kTopK; ++j) ssel[j] = s_sel[wv][j];
+    const int my_id = lane < kTopK ? s_sel_id[wv][lane] : 0;
+    const float my_s = lane < kTopK ? s_sel[wv][lane] : 0.0f;
 
     // w = s / (sum + 1e-20) * factor, summed in selection order
     float sum = 0.0f;
