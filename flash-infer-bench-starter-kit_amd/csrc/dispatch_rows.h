@@ -56,17 +56,28 @@ __device__ __forceinline__ TokenRoutes load_routes(const int* __restrict__ topk_
     return r;
 }
 
+// The ballot of expert BASE + (lane & (2^(BIT+1) - 1)) for this lane: a selection tree
+// over the bits of the lane index, whose leaves are the ballots of experts BASE ..
+// BASE + 2^(BIT+1) - 1.
+template <int BIT, int BASE>
+__device__ __forceinline__ uint64_t ballot_for_lane(uint32_t mask, int lane) {
+    if constexpr (BIT < 0) {
+        return __ballot((mask >> BASE) & 1u);
+    } else {
+        const uint64_t lo = ballot_for_lane<BIT - 1, BASE>(mask, lane);
+        const uint64_t hi = ballot_for_lane<BIT - 1, BASE + (1 << BIT)>(mask, lane);
+        return ((lane >> BIT) & 1) ? hi : lo;
+    }
+}
+
 // For each expert e: the wave's ballot of the lanes routed to it into bal[e] and their
 // count into wcnt[wave][e] (LDS).  One ballot per expert; lane e keeps expert e's
-// ballot and writes it.
+// ballot, picked by a selection tree over the bits of the lane index (five levels of
+// independent selects; a select per expert in turn made a 32-step dependent chain).
 __device__ __forceinline__ void wave_ballots(const TokenRoutes& r, int wave, int lane,
                                              int (*wcnt)[kEL], uint64_t* bal) {
-    uint64_t mine = 0;
-#pragma unroll
-    for (int e = 0; e < kEL; ++e) {
-        const uint64_t b = __ballot((r.mask >> e) & 1u);
-        mine = (lane == e) ? b : mine;
-    }
+    static_assert(kEL == 32, "the selection tree covers 32 experts");
+    const uint64_t mine = ballot_for_lane<4, 0>(r.mask, lane);
     if (lane < kEL) {
         bal[lane] = mine;
         wcnt[wave][lane] = __popcll(mine);
