@@ -1,8 +1,10 @@
 """Compile the gfx950 HIP sources of this directory into ``libmoe_mi355.so``.
 
-Usage: ``python build.py [--jobs N]``.  Each ``csrc/*.hip`` file is compiled to an
-object (in parallel), then linked into ``libmoe_mi355.so`` next to this file, where
-``kernel.py`` loads it.  hipcc cross-compiles for gfx950 without a GPU.
+Usage: ``python build.py [--jobs N] [--stamps]``.  Each ``csrc/*.hip`` file is compiled
+to an object (in parallel), then linked into ``libmoe_mi355.so`` next to this file, where
+``kernel.py`` loads it.  hipcc cross-compiles for gfx950 without a GPU.  ``--stamps``
+builds ``libmoe_mi355_stamps.so`` instead: the same library with the decode chain's
+in-kernel timeline stamps compiled in (``csrc/stamps.h``, read by ``stamp_timeline.py``).
 
 Several processes may build at once (harness workers that each load the solution on
 first use): a build holds an exclusive ``fcntl`` lock on ``libmoe_mi355.so.lock`` next
@@ -33,6 +35,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 REPO = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libmoe_mi355.so")
+STAMPS_LIB = os.path.join(HERE, "libmoe_mi355_stamps.so")
 LOCK = LIB + ".lock"
 # the C-ABI header: include/ next to this file in a packed solution, else the repo's
 INCLUDE = os.path.join(HERE, "include") if os.path.isdir(os.path.join(HERE, "include")) \
@@ -88,9 +91,10 @@ def is_current(path: str = LIB) -> bool:
     return library_hash(path) == source_hash()
 
 
-def _compile(src: str, outdir: str, src_hash: str) -> str:
+def _compile(src: str, outdir: str, src_hash: str, stamps: bool = False) -> str:
     obj = os.path.join(outdir, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *FLAGS, f'-DMOE_MI355_SRC_HASH="{src_hash}"', "-c", src, "-o", obj]
+    cmd = [HIPCC, *FLAGS, f'-DMOE_MI355_SRC_HASH="{src_hash}"',
+           *(["-DMOE_MI355_STAMPS"] if stamps else []), "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{r.stdout}\n{r.stderr}")
@@ -112,44 +116,50 @@ def _build_lock():
         os.close(fd)
 
 
-def _build_locked(jobs: int, verbose: bool) -> str:
+def _build_locked(jobs: int, verbose: bool, stamps: bool = False) -> str:
+    out = STAMPS_LIB if stamps else LIB
     work = tempfile.mkdtemp(prefix="_build.", dir=HERE)
     try:
         srcs = sources()
         src_hash = source_hash()
         with cf.ThreadPoolExecutor(max_workers=max(1, min(jobs, len(srcs)))) as ex:
-            objs = list(ex.map(lambda s: _compile(s, work, src_hash), srcs))
-        tmp = os.path.join(work, os.path.basename(LIB))
+            objs = list(ex.map(lambda s: _compile(s, work, src_hash, stamps), srcs))
+        tmp = os.path.join(work, os.path.basename(out))
         cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
         r = subprocess.run(cmd, capture_output=True, text=True)
         if r.returncode != 0:
             raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
-        os.replace(tmp, LIB)
+        os.replace(tmp, out)
     finally:
         shutil.rmtree(work, ignore_errors=True)
     if verbose:
-        print(f"built {LIB}")
-    return LIB
+        print(f"built {out}")
+    return out
 
 
-def build(jobs: int = 8, verbose: bool = True) -> str:
-    """Compile and link the library (always, even when one is present)."""
+def build(jobs: int = 8, verbose: bool = True, stamps: bool = False) -> str:
+    """Compile and link the library (always, even when one is present); with stamps,
+    the timeline-stamped build, libmoe_mi355_stamps.so."""
     with _build_lock():
-        return _build_locked(jobs, verbose)
+        return _build_locked(jobs, verbose, stamps)
 
 
-def ensure_built(jobs: int = 8, verbose: bool = False) -> str:
+def ensure_built(jobs: int = 8, verbose: bool = False, stamps: bool = False) -> str:
     """Build the library if it is missing or was built from other sources (the first
     use of a packed solution, or a kernel edited since the last build)."""
-    if is_current():
-        return LIB
+    out = STAMPS_LIB if stamps else LIB
+    if is_current(out):
+        return out
     with _build_lock():
-        if is_current():              # another process built it while this one waited
-            return LIB
-        return _build_locked(jobs, verbose)
+        if is_current(out):           # another process built it while this one waited
+            return out
+        return _build_locked(jobs, verbose, stamps)
 
 
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=8)
-    build(ap.parse_args().jobs)
+    ap.add_argument("--stamps", action="store_true",
+                    help="build libmoe_mi355_stamps.so (in-kernel timeline stamps) instead")
+    a = ap.parse_args()
+    build(a.jobs, stamps=a.stamps)

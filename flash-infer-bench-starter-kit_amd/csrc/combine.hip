@@ -16,6 +16,8 @@
 
 #include "combine_rows.h"
 
+MOE_STAMP_TABLE(combine)
+
 namespace moe {
 
 __global__ __launch_bounds__(128) void combine_kernel(ExpertRows rows, const int* __restrict__ rows_wide,
@@ -25,9 +27,11 @@ __global__ __launch_bounds__(128) void combine_kernel(ExpertRows rows, const int
     constexpr int kParts = kH / (128 * 8);  // 7 blocks of 128 threads per token
     const int t = blockIdx.x / kParts;
     const int h0 = ((blockIdx.x % kParts) * 128 + threadIdx.x) * 8;
+    MOE_STAMP(2 * (int)blockIdx.x);
     if (t >= T) return;
     combine_token8(rows, __builtin_amdgcn_readfirstlane(*rows_wide) != 0, inv + (size_t)t * kTopK,
                    sorted_w, h0, out + (size_t)t * kH + h0);
+    MOE_STAMP(2 * (int)blockIdx.x + 1);
 }
 
 void launch_combine(const ExpertRows& rows, const int* rows_wide, const float* sorted_w, const int* inv,

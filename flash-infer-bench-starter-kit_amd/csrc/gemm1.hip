@@ -27,6 +27,8 @@
 
 #include <mutex>
 
+MOE_STAMP_TABLE(gemm1)
+
 namespace moe {
 
 // The streaming GEMM1 over the row tiles of a dispatch (see gemm1_rstream_item).
@@ -285,6 +287,7 @@ __global__ __launch_bounds__(256) void gemm1_rstream_dispatch_kernel(
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const bool writer = blockIdx.x == gridDim.x - 1;
+    MOE_STAMP(3 * (int)blockIdx.x);
     if (wave == 0) {
         const TokenRoutes r = load_routes(topk_ids, topk_w, lane, T, offset);
         wave_ballots(r, 0, lane, s_dw.wcnt, s_dw.bal);
@@ -324,6 +327,7 @@ __global__ __launch_bounds__(256) void gemm1_rstream_dispatch_kernel(
         for (int i = tid; i < ntiles; i += 256) tiles[i] = s_tiles[i];
     }
     __syncthreads();
+    MOE_STAMP(3 * (int)blockIdx.x + 1);
     const TokenScales sa{hs_scale, T, 0};
     const int nwork = ntiles * S::kItems;
     for (int work = blockIdx.x; work < nwork; work += gridDim.x) {
@@ -332,6 +336,7 @@ __global__ __launch_bounds__(256) void gemm1_rstream_dispatch_kernel(
                                            work % S::kItems, [&](int row) { return s_stok[row]; },
                                            C, meta + kCWideFlag, slot_lds, red, wave);
     }
+    MOE_STAMP(3 * (int)blockIdx.x + 2);
 }
 
 // Epilogue of the prefill GEMM1 kernels: SwiGLU, then the fp8 hi/lo form of C.

@@ -22,6 +22,8 @@
 
 #include "gemm2_stream.h"
 
+MOE_STAMP_TABLE(gemm2)
+
 namespace moe {
 
 template <int D, int KSPLIT, int HF, int CB>
@@ -34,6 +36,7 @@ __global__ __launch_bounds__(256) void gemm2_rstream_kernel(
     constexpr int kItems = (kH / 16) / (NGW * HF);
     __shared__ __attribute__((aligned(1024))) uint8_t slot_lds[4][16 * HF * kBlk];
     __shared__ v4f red[4][HF][CB][64];
+    MOE_STAMP(2 * (int)blockIdx.x);
     const int nwork = (*num_tiles) * kItems;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     // the two paths keep separate loops, so each is register-allocated on its own
@@ -52,6 +55,7 @@ __global__ __launch_bounds__(256) void gemm2_rstream_kernel(
                                                     flags + 1, red, wave);
         }
     }
+    MOE_STAMP(2 * (int)blockIdx.x + 1);
 }
 
 // Prefill GEMM2 (many tokens per expert): MFMA-bound tiling on FP8 MFMA with C in

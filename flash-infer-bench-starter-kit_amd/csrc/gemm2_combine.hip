@@ -27,6 +27,8 @@
 #include "combine_rows.h"
 #include "gemm2_stream.h"
 
+MOE_STAMP_TABLE(gemm2_combine)
+
 namespace moe {
 
 constexpr int kFusedRows = kFusedCombineMaxT * kTopK;        // expert rows in LDS
@@ -62,6 +64,7 @@ __global__ __launch_bounds__(256 * NG, 1) void gemm2_combine_kernel(
     const int hg = blockIdx.x * HF;                  // first 16-column group
     const v4f zero = {0.f, 0.f, 0.f, 0.f};
     const int R = T * kTopK;
+    MOE_STAMP(2 * (int)blockIdx.x);
 
     // Straight into LDS: the routing weights of the rows and the inverse map (read by
     // the combine at the end; the waits of the K loop or the barrier before the combine
@@ -258,6 +261,7 @@ __global__ __launch_bounds__(256 * NG, 1) void gemm2_combine_kernel(
         *reinterpret_cast<uint32_t*>(out + (size_t)t * kH + blockIdx.x * kFusedCols + 2 * p) =
             f32_to_bf16_bits(a0) | (f32_to_bf16_bits(a1) << 16);
     }
+    MOE_STAMP(2 * (int)blockIdx.x + 1);
 }
 
 // GEMM2 variant 6: the streaming GEMM2 of variant 1 (16-row tiles, fp16 C) with the

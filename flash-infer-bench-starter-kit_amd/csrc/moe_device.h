@@ -8,6 +8,7 @@
 #include <utility>
 
 #include "moe_shape.h"
+#include "stamps.h"
 
 namespace moe {
 

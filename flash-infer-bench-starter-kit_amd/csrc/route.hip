@@ -17,6 +17,8 @@
 
 #include "moe_device.h"
 
+MOE_STAMP_TABLE(route)
+
 namespace moe {
 
 #pragma clang fp contract(off)
@@ -119,6 +121,7 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     // the forward's two per-call flag words (C and expert rows beyond the fp16 range, set
     // by GEMM1 and GEMM2, read by GEMM2 and the combine) start at 0
+    MOE_STAMP(2 * (int)blockIdx.x);
     if (clear_word != nullptr && blockIdx.x == 0 && threadIdx.x < 2) clear_word[threadIdx.x] = 0;
     if (t >= T) return;  // uniform per wave
 
@@ -220,6 +223,7 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
         topk_ids[(size_t)t * kTopK + lane] = my_id;
         topk_w[(size_t)t * kTopK + lane] = q * factor;
     }
+    MOE_STAMP(2 * (int)blockIdx.x + 1);
 }
 
 // clear_word (may be null): two ints the kernel sets to 0 for the kernels after it.
