@@ -2,10 +2,10 @@
 // the launch sequence and a small stage profiler.
 //
 // Replaces the host orchestration of the reference (solution/python/main.cpp:66-266):
-// there ~16 launches and ~20 torch allocations per call; here three to eight launches on
+// there ~16 launches and ~20 torch allocations per call; here two to eight launches on
 // the caller's stream over one caller-provided workspace, no host synchronisation and no
 // allocation:
-//   route    (T/4 workgroups)      -> topk ids / weights
+//   route    (T/4 workgroups; inside GEMM1 for T <= 4) -> topk ids / weights
 //   dispatch (1 workgroup, or count + place kernels; inside GEMM1 for T <= 64)
 //                                  -> expert offsets, row tiles, permutation, inverse map
 //   (gather  -> token scales in row order, for the plans that read them so)
@@ -21,6 +21,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "host_plan.h"
@@ -34,13 +35,13 @@ bool launch_dispatch(const int*, const float*, int, int, int, int, int*, int*, i
 bool launch_gemm1(int, const uint8_t*, const TokenScales&, int, const uint8_t*, const float*,
                   const int4*, const int*, const int*, int, const int*, const Intermediate&,
                   bool, hipStream_t);
-bool launch_gemm1_dispatch(const int*, const float*, int, int, const uint8_t*, const float*,
+bool launch_gemm1_dispatch(const RouteIn&, int*, float*, int, int, const uint8_t*, const float*,
                            const uint8_t*, const float*, int*, int4*, int*, float*, int*,
-                           const Intermediate&, hipStream_t);
+                           const Intermediate&, int, hipStream_t);
 bool launch_gemm2(int, const Intermediate&, const uint8_t*, const float*, const int4*, const int*,
                   const int*, int, const ExpertRows&, hipStream_t);
 bool launch_gemm2_combine(const Intermediate&, const uint8_t*, const float*, const int4*, const int*,
-                          int*, const int*, const float*, int, uint16_t*, hipStream_t);
+                          int*, const int*, const float*, int, uint16_t*, int, hipStream_t);
 void launch_combine(const ExpertRows&, const int*, const float*, const int*, int, uint16_t*, hipStream_t);
 void launch_e4m3_to_bf16(const uint8_t*, uint16_t*, int, hipStream_t);
 void launch_c_f16_to_hilo(const Intermediate&, const int*, hipStream_t);
@@ -93,7 +94,8 @@ Profiler g_prof;
 // on the current GPU comes from hipGetSymbolAddress, once per device (kept in
 // g_scratch_dev), and only that address reaches the kernels.  Every call on one GPU
 // shares the array: nothing in it needs to start at zero (the route kernel clears the
-// flag words, dispatch writes every offset, count and row the later kernels read),
+// flag words, or GEMM1 variant 9 marks them with the call's own tag; dispatch writes
+// every offset, count and row the later kernels read),
 // and calls that overlap on one GPU (two streams) race on it.
 constexpr size_t kScratchBytes = workspace_regions(MOE_MI355_NOALLOC_MAX_TOKENS).total;
 static_assert(kScratchBytes <= (size_t)64 << 20, "keep the per-GPU scratch array modest");
@@ -123,6 +125,13 @@ int scratch_on_current_device(void** out) {
     }
     *out = g_scratch_dev[dev];
     return MOE_OK;
+}
+
+// The C-range tag of a call whose GEMM1 routes its tokens itself (GEMM1 variant 9): a
+// value >= 2 that differs from the tags of the 2^31 - 3 calls before it in the process.
+std::atomic<uint32_t> g_wide_tag{0};
+int next_wide_tag() {
+    return 2 + (int)(g_wide_tag.fetch_add(1, std::memory_order_relaxed) % 0x7ffffffdu);
 }
 
 // The forward's launch sequence over a workspace of ws_bytes at ws (the caller's, or
@@ -163,9 +172,14 @@ int forward_impl(const moe_mi355_args& a, void* workspace, size_t ws_bytes, hipS
     };
     moe::g_kernel_timer = timer;   // the launches below time themselves (cleared before return)
 
+    // GEMM1 variant 9 routes the tokens itself (timed as the GEMM1 stage) and marks C
+    // beyond the fp16 range with the call's tag instead of 1 (no route kernel clears the
+    // flag word before it)
+    const int wide_tag = plan.route_in_gemm1 ? next_wide_tag() : 1;
     stage(0);
-    moe::launch_route(a.routing_logits, a.routing_bias, T, (float)a.routed_scaling_factor, ids,
-                      wts, meta + moe::kCWideFlag, s);
+    if (!plan.route_in_gemm1)
+        moe::launch_route(a.routing_logits, a.routing_bias, T, (float)a.routed_scaling_factor, ids,
+                          wts, meta + moe::kCWideFlag, s);
     stage(1);
     const int max_tiles = moe::dispatch_max_tiles(T, plan.tm);
     const bool half = plan.tm2 > 0;   // GEMM2 walks the second (128-row) tile list
@@ -184,11 +198,14 @@ int forward_impl(const moe_mi355_args& a, void* workspace, size_t ws_bytes, hipS
     const moe::TokenScales sa = plan.by_row ? moe::TokenScales{row_scales, T * moe::kTopK, 1}
                                             : moe::TokenScales{a.hidden_states_scale, T, 0};
     stage(2);
-    if (plan.dispatch_in_gemm1)
-        ok = ok && moe::launch_gemm1_dispatch(ids, wts, T, clamp_offset(a.local_expert_offset),
+    if (plan.dispatch_in_gemm1) {
+        const moe::RouteIn rin{plan.route_in_gemm1 ? a.routing_logits : nullptr, a.routing_bias,
+                               (float)a.routed_scaling_factor};
+        ok = ok && moe::launch_gemm1_dispatch(rin, ids, wts, T, clamp_offset(a.local_expert_offset),
                                               a.hidden_states, a.hidden_states_scale,
                                               a.gemm1_weights, a.gemm1_weights_scale, meta, tiles,
-                                              stok, sw, inv, inter, s);
+                                              stok, sw, inv, inter, wide_tag, s);
+    }
     else
         ok = ok && moe::launch_gemm1(plan.g1, a.hidden_states, sa, T, a.gemm1_weights,
                                      a.gemm1_weights_scale, tiles, num_tiles, meta, max_tiles,
@@ -197,7 +214,7 @@ int forward_impl(const moe_mi355_args& a, void* workspace, size_t ws_bytes, hipS
     if (ok && plan.convert) moe::launch_c_f16_to_hilo(inter, meta, s);   // in the GEMM2 stage
     if (ok && plan.combine_in_gemm2)      // GEMM2 writes the output (timed as the GEMM2 stage)
         ok = moe::launch_gemm2_combine(inter, a.gemm2_weights, a.gemm2_weights_scale, tiles,
-                                       num_tiles, meta, inv, sw, T, a.output, s);
+                                       num_tiles, meta, inv, sw, T, a.output, wide_tag, s);
     else if (ok && half)
         ok = moe::launch_gemm2(plan.g2, inter, a.gemm2_weights, a.gemm2_weights_scale, tiles2,
                                num_tiles2, meta, moe::dispatch_max_tiles(T, plan.tm2), rows, s);

@@ -24,6 +24,7 @@
 
 #include "dispatch_rows.h"
 #include "gemm1_stream.h"
+#include "route_token.h"
 
 #include <mutex>
 
@@ -264,14 +265,23 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(WPE)))
 // rows (128 items apart) run on one XCD.  The dispatch launch goes away; the part of the
 // dispatch before the first weight load costs a workgroup about what the separate
 // kernel's two dependent loads (tile list, then permutation) cost.
+//
+// ROUTE (T <= kRouteInGemm1MaxT = 4): the routing too.  Every workgroup routes the call's
+// tokens itself from the logits (route_token, the route kernel's computation: wave w
+// takes token w) into LDS, where the dispatch reads them; the last
+// workgroup also writes them to the workspace.  The route launch, its kernel boundary
+// and the dispatch's dependent load of the routing ids go away.  Nothing clears the
+// C-range flag word before this kernel, so it writes the call's wide_tag there instead
+// of 1, and the GEMM2 after it compares the word with the same tag.
 constexpr int kDG1MaxTiles = dispatch_max_tiles(kDispatchInGemm1MaxT, 16);   // 64
 
+template <bool ROUTE>
 __global__ __launch_bounds__(256) void gemm1_rstream_dispatch_kernel(
-    const int* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int offset,
+    RouteIn rin, int* __restrict__ topk_ids, float* __restrict__ topk_w, int T, int offset,
     const uint8_t* __restrict__ hidden, const float* __restrict__ hs_scale,
     const uint8_t* __restrict__ w1, const float* __restrict__ s1, int* __restrict__ meta,
     int4* __restrict__ tiles, int* __restrict__ sorted_tok, float* __restrict__ sorted_w,
-    int* __restrict__ inv, Intermediate C) {
+    int* __restrict__ inv, Intermediate C, int wide_tag) {
     using S = Gemm1Stream<1, 1, false>;
     constexpr int R = kDispatchInGemm1MaxT * kTopK;
     __shared__ __attribute__((aligned(1024))) uint8_t slot_lds[4][S::kSlot];
@@ -288,8 +298,36 @@ __global__ __launch_bounds__(256) void gemm1_rstream_dispatch_kernel(
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const bool writer = blockIdx.x == gridDim.x - 1;
     MOE_STAMP(3 * (int)blockIdx.x);
+    const int* ids_src = topk_ids;
+    const float* w_src = topk_w;
+    if constexpr (ROUTE) {
+        static_assert(kRouteInGemm1MaxT == 4, "one token per wave");
+        __shared__ __attribute__((aligned(16))) int s_rid[kRouteInGemm1MaxT][kTopK];
+        __shared__ __attribute__((aligned(16))) float s_rw[kRouteInGemm1MaxT][kTopK];
+        __shared__ float s_sel[4][kTopK];
+        __shared__ int s_sel_id[4][kTopK];
+        const int t = wave;
+        if (t < T) {   // uniform per wave
+            const float4 lg = reinterpret_cast<const float4*>(rin.logits + (size_t)t * kEG)[lane];
+            const uint2 bb = reinterpret_cast<const uint2*>(rin.bias)[lane];
+            int id;
+            float w;
+            route_token(lg, bb, lane, rin.factor, s_sel[wave], s_sel_id[wave], id, w);
+            if (lane < kTopK) {
+                s_rid[t][lane] = id;
+                s_rw[t][lane] = w;
+                if (writer) {
+                    topk_ids[t * kTopK + lane] = id;
+                    topk_w[t * kTopK + lane] = w;
+                }
+            }
+        }
+        __syncthreads();
+        ids_src = &s_rid[0][0];
+        w_src = &s_rw[0][0];
+    }
     if (wave == 0) {
-        const TokenRoutes r = load_routes(topk_ids, topk_w, lane, T, offset);
+        const TokenRoutes r = load_routes(ids_src, w_src, lane, T, offset);
         wave_ballots(r, 0, lane, s_dw.wcnt, s_dw.bal);
 #pragma unroll
         for (int k = 0; k < kTopK; ++k) {
@@ -334,7 +372,7 @@ __global__ __launch_bounds__(256) void gemm1_rstream_dispatch_kernel(
         const int4 tile = s_tiles[work / S::kItems];
         gemm1_rstream_item<4, 1, 1, false>(hidden, sa, w1, s1, tile.x, tile.y, tile.z,
                                            work % S::kItems, [&](int row) { return s_stok[row]; },
-                                           C, meta + kCWideFlag, slot_lds, red, wave);
+                                           C, meta + kCWideFlag, slot_lds, red, wave, wide_tag);
     }
     MOE_STAMP(3 * (int)blockIdx.x + 2);
 }
@@ -640,37 +678,51 @@ static int grid_for(long long work) { return (int)(work < 4096 ? work : 4096); }
 namespace {
 constexpr int kMaxDevices = 64;
 std::mutex g_dg1_mu;
-int g_dg1_grid[kMaxDevices] = {};
+int g_dg1_grid[2][kMaxDevices] = {};
 }  // namespace
 
-// GEMM1 with the dispatch folded in: a persistent grid of as many workgroups as the
-// device holds at once (occupancy x CUs, looked up once per device), capped by the most
-// work items T tokens can have.
-bool launch_gemm1_dispatch(const int* topk_ids, const float* topk_w, int T, int offset,
+// GEMM1 with the dispatch folded in (and with rin.logits set, T <= kRouteInGemm1MaxT, the
+// routing too): a persistent grid of as many workgroups as the device holds at once
+// (occupancy x CUs, looked up once per device and kernel), capped by the most work items
+// T tokens can have.  Without the routing, topk_ids / topk_w hold the routing; with it,
+// the kernel writes them.  wide_tag is the value the kernel writes into the C-range flag
+// word (1 after a route kernel cleared it).
+bool launch_gemm1_dispatch(const RouteIn& rin, int* topk_ids, float* topk_w, int T, int offset,
                            const uint8_t* hidden, const float* hs_scale, const uint8_t* w1,
                            const float* s1, int* meta, int4* tiles, int* sorted_tok,
-                           float* sorted_w, int* inv, const Intermediate& C, hipStream_t stream) {
-    if (T <= 0 || T > kDispatchInGemm1MaxT) return false;
+                           float* sorted_w, int* inv, const Intermediate& C, int wide_tag,
+                           hipStream_t stream) {
+    const bool route = rin.logits != nullptr;
+    if (T <= 0 || T > (route ? kRouteInGemm1MaxT : kDispatchInGemm1MaxT)) return false;
+    if (route && (rin.bias == nullptr || wide_tag < 2)) return false;
+    const void* fn = route ? reinterpret_cast<const void*>(gemm1_rstream_dispatch_kernel<true>)
+                           : reinterpret_cast<const void*>(gemm1_rstream_dispatch_kernel<false>);
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
     int resident = 0;
     {
         std::lock_guard<std::mutex> lock(g_dg1_mu);
-        if (g_dg1_grid[dev] == 0) {
+        int& g = g_dg1_grid[route ? 1 : 0][dev];
+        if (g == 0) {
             int per_cu = 0, cus = 0;
-            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemm1_rstream_dispatch_kernel, 256, 0) != hipSuccess ||
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, 0) != hipSuccess ||
                 hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
                 per_cu * cus <= 0)
                 return false;
-            g_dg1_grid[dev] = per_cu * cus;
+            g = per_cu * cus;
         }
-        resident = g_dg1_grid[dev];
+        resident = g;
     }
     const long long items = (long long)(((long long)T * kTopK + 15) / 16 + kEL) * Gemm1Stream<1, 1, false>::kItems;
     const int grid = (int)(items < resident ? items : resident);
-    launch_kernel(gemm1_rstream_dispatch_kernel, dim3(grid), dim3(256), 0, stream, topk_ids,
-                       topk_w, T, offset, hidden, hs_scale, w1, s1, meta, tiles, sorted_tok, sorted_w,
-                       inv, C);
+    if (route)
+        launch_kernel(gemm1_rstream_dispatch_kernel<true>, dim3(grid), dim3(256), 0, stream, rin,
+                      topk_ids, topk_w, T, offset, hidden, hs_scale, w1, s1, meta, tiles,
+                      sorted_tok, sorted_w, inv, C, wide_tag);
+    else
+        launch_kernel(gemm1_rstream_dispatch_kernel<false>, dim3(grid), dim3(256), 0, stream, rin,
+                      topk_ids, topk_w, T, offset, hidden, hs_scale, w1, s1, meta, tiles,
+                      sorted_tok, sorted_w, inv, C, 1);
     return true;
 }
 

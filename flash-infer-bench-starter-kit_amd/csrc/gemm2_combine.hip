@@ -42,13 +42,14 @@ __global__ __launch_bounds__(256 * NG, 1) void gemm2_combine_kernel(
     Intermediate C, int* __restrict__ flags, const uint8_t* __restrict__ w2,
     const float* __restrict__ s2, const int4* __restrict__ tiles,
     const int* __restrict__ num_tiles, const int* __restrict__ inv,
-    const float* __restrict__ sorted_w, int T, uint16_t* __restrict__ out) {
+    const float* __restrict__ sorted_w, int T, uint16_t* __restrict__ out, int wide_tag) {
     constexpr int HF = 2, KSPLIT = 4, KB = kIB / KSPLIT, D = KB;
     constexpr int NW = KSPLIT * NG;           // waves
     constexpr int CH = 4 * NG;                // tiles per reduction round (4 per group)
     constexpr int kVmPerStep = 2 * HF + 5;    // W2 loads, C loads, block scale of one (tile, K block)
     static_assert(HF == 2, "the HF column groups of a workgroup share one W2 scale block");
-    // flags[0]: C beyond the fp16 range (set by GEMM1); flags[1]: an expert row beyond it
+    // flags[0]: C beyond the fp16 range (GEMM1 wrote wide_tag there); flags[1]: an expert
+    // row beyond it (set to wide_tag here; nothing after this kernel reads it)
     __shared__ __attribute__((aligned(1024))) uint8_t slot_lds[NW][16 * HF * kBlk];
     __shared__ v4f red[KSPLIT][CH][HF][64];          // K partials of one round of tiles
     __shared__ float o_lds[kFusedRows][kFusedCols];  // expert rows (as the combine reads them)
@@ -132,7 +133,7 @@ __global__ __launch_bounds__(256 * NG, 1) void gemm2_combine_kernel(
     // reduction barriers), a group without a tile at some i only waits there
     const int imax = (nt + NG - 1) / NG;
     const int nt_g = (nt - grp + NG - 1) / NG;
-    if (__builtin_amdgcn_readfirstlane(flags[0]) == 0) {
+    if (__builtin_amdgcn_readfirstlane(flags[0]) != wide_tag) {
         // ---- the stream of (tile, K block) steps of this wave: step 4 i + j is tile
         // grp + NG i, K block 4 ks + j, held in ring slot j
         uint8_t* slot = &slot_lds[wave][0];
@@ -227,7 +228,7 @@ __global__ __launch_bounds__(256 * NG, 1) void gemm2_combine_kernel(
             if ((i & 3) == 3 || i == imax - 1) reduce_round(CH * (i >> 2));
         }
     }
-    if (any_e) flags[1] = 1;     // an expert row went beyond the fp16 range
+    if (any_e) flags[1] = wide_tag;   // an expert row went beyond the fp16 range
     __syncthreads();             // every row in o_lds, the routing tables landed
 
     // ---- the combine of the workgroup's 32 columns: thread (token t, column pair p),
@@ -265,13 +266,16 @@ __global__ __launch_bounds__(256 * NG, 1) void gemm2_combine_kernel(
 }
 
 // GEMM2 variant 6: the streaming GEMM2 of variant 1 (16-row tiles, fp16 C) with the
-// combine folded in, for T <= kFusedCombineMaxT; writes the bf16 output itself.
+// combine folded in, for T <= kFusedCombineMaxT; writes the bf16 output itself.  C went
+// beyond the fp16 range when the C-range flag word holds wide_tag (the value the GEMM1
+// before it writes there: 1 after a route kernel cleared the word, or the call's tag).
 bool launch_gemm2_combine(const Intermediate& C, const uint8_t* w2, const float* s2,
                           const int4* tiles, const int* num_tiles, int* meta, const int* inv,
-                          const float* sorted_w, int T, uint16_t* out, hipStream_t stream) {
-    if (T <= 0 || T > kFusedCombineMaxT) return false;
+                          const float* sorted_w, int T, uint16_t* out, int wide_tag,
+                          hipStream_t stream) {
+    if (T <= 0 || T > kFusedCombineMaxT || wide_tag == 0) return false;
     launch_kernel((gemm2_combine_kernel<2>), dim3(kH / kFusedCols), dim3(512), 0, stream, C,
-                       meta + kCWideFlag, w2, s2, tiles, num_tiles, inv, sorted_w, T, out);
+                       meta + kCWideFlag, w2, s2, tiles, num_tiles, inv, sorted_w, T, out, wide_tag);
     return true;
 }
 

@@ -47,20 +47,28 @@ struct Plan {
     bool by_row;   // GEMM1 reads the token scales gathered into row order
     bool dispatch_in_gemm1;   // GEMM1 variant 5 computes the dispatch itself (no launch)
     bool combine_in_gemm2;    // GEMM2 variant 6 writes the output itself (no combine launch)
+    bool route_in_gemm1;      // GEMM1 variant 9 routes the tokens itself (no route launch)
 };
 
-inline int g1_tile_m(int v) { return v == 1 || v == 5 ? 16 : v == 2 ? 32 : v == 7 || v == 8 ? 64 : 256; }
+inline int g1_tile_m(int v) { return v == 1 || v == 5 || v == 9 ? 16 : v == 2 ? 32 : v == 7 || v == 8 ? 64 : 256; }
 inline bool g1_hilo(int v) { return v == 4; }        // GEMM1 writes the hi/lo form
 inline bool g2_hilo(int v) { return v == 5; }        // GEMM2 reads the hi/lo form
 
 // The plan of a GEMM1 / GEMM2 pair, false when they cannot run together.  GEMM1
 // variant 5 is variant 1 with the dispatch folded in (T <= 64): every workgroup of a
 // persistent grid computes the call's dispatch from the routing ids, and the separate
-// dispatch launch goes away.
+// dispatch launch goes away.  GEMM1 variant 9 is variant 5 with the routing folded in too
+// (T <= kRouteInGemm1MaxT, GEMM2 variant 6 only): every workgroup routes the call's
+// tokens from the logits, and the route launch goes away.
 inline bool make_plan(int g1, int g2, int32_t T, Plan* p) {
     // GEMM2 variant 6 is variant 1 (16-row tiles, fp16 C) with the combine folded in,
     // for T <= kFusedCombineMaxT
-    if (g2 == 6 && (T > kFusedCombineMaxT || (g1 != 1 && g1 != 5))) return false;
+    if (g2 == 6 && (T > kFusedCombineMaxT || (g1 != 1 && g1 != 5 && g1 != 9))) return false;
+    if (g1 == 9) {
+        if (g2 != 6 || T > kRouteInGemm1MaxT) return false;
+        *p = {16, 0, 9, 6, false, false, true, true, true};
+        return true;
+    }
     if (g1 == 5) {
         if ((g2 != 1 && g2 != 6) || T > kDispatchInGemm1MaxT) return false;
         *p = {16, 0, 5, g2, false, false, true, g2 == 6};
@@ -108,7 +116,8 @@ inline int plan_for(int32_t T, int32_t flags, Plan* p) {
     int g1, g2;
     // GEMM1 with the dispatch folded in reads the token scales by token: asking for the
     // gathered ones selects the separate dispatch there
-    if (T <= kFusedCombineMaxT && !on) g1 = 5, g2 = 6;
+    if (T <= kRouteInGemm1MaxT && !on) g1 = 9, g2 = 6;   // T <= 4
+    else if (T <= kFusedCombineMaxT && !on) g1 = 5, g2 = 6;
     else if (T <= kDispatchInGemm1MaxT && !on) g1 = 5, g2 = 1;
     else if (T <= 88) g1 = 1, g2 = 1;
     else if (T <= 299) g1 = 2, g2 = 3;

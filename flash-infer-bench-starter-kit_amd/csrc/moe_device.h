@@ -278,6 +278,13 @@ struct TokenScales {
     int by_row;
 };
 
+// The routing inputs of a GEMM1 that routes its tokens itself (logits null: it does not).
+struct RouteIn {
+    const float* logits;      // [T, 256] fp32
+    const uint16_t* bias;     // [256] bf16
+    float factor;             // routed scaling factor
+};
+
 // One global_load_lds_dwordx4: lane L copies the 16 bytes at its own address g to
 // LDS l + 16 L (l must be wave-uniform).
 __device__ __forceinline__ void dma16(const uint8_t* g, uint8_t* l) {

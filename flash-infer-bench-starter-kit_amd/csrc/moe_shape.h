@@ -22,6 +22,11 @@ constexpr int kN1B = kN1 / kBlk;   // 32 GEMM1 output blocks
 // Words of the workspace's meta region after the 33 expert offsets [0 .. kEL]: the tile
 // count of the first list, of the second list, then two per-call flag words (cleared by
 // the route kernel): C of GEMM1 exceeds the fp16 range, an expert row of GEMM2 does.
+// Where no route kernel runs (GEMM1 variant 9 routes its tokens itself), the first word
+// is not cleared: that GEMM1 writes the call's tag (a value >= 2, different on every
+// call) there instead of 1, and its GEMM2 (variant 6) compares the word with the tag.
+// A word that holds the tag for another reason only sends GEMM2 down its rare path,
+// which reads C's group exponents, and GEMM1 writes every exponent on every call.
 constexpr int kCWideFlag = kEL + 3;
 constexpr int kRowsWideFlag = kEL + 4;
 constexpr int kGroup16 = 16;       // columns per fp16-form exponent byte
@@ -29,6 +34,12 @@ constexpr int kGroup16 = 16;       // columns per fp16-form exponent byte
 // Largest T whose dispatch runs inside the GEMM1 launch (GEMM1 variant 5): the kernel
 // keeps that call's permutation and tile list in LDS, sized by this bound.
 constexpr int kDispatchInGemm1MaxT = 64;
+
+// Largest T whose routing also runs inside the GEMM1 launch (GEMM1 variant 9): every
+// workgroup routes the call's tokens, one per wave, before its items.  A wave's routing is
+// a dependent chain of ~600 instructions; two tokens on one wave (T = 8) delayed the first
+// weight load by more than the route launch costs.
+constexpr int kRouteInGemm1MaxT = 4;
 
 // Largest T whose GEMM2 runs with the combine folded in (GEMM2 variant 6): the kernel
 // keeps every expert row of the call (8 T rows) for its 32 output columns in LDS.

@@ -8,7 +8,8 @@ the GEMM2 (streaming, or with the combine folded in) and the combine.  The scrip
 one BASELINE config on cuda:0 with its inputs rotating over ``--copies`` copies, in
 bursts of calls issued back to back; after each burst it reads the stamps, which then
 hold the burst's last call (a call in the steady state of a stream of calls).  It prints
-the median over ``--samples`` bursts, relative to the first route workgroup's start, of
+the median over ``--samples`` bursts, relative to the call's first workgroup start (the
+route kernel's, or at T <= 8 the GEMM1's, which routes the tokens itself), of
 each kernel's first and last workgroup start, the median and last workgroup end, and
 the gap from the previous kernel's last end to the next kernel's first start.
 
@@ -97,8 +98,8 @@ def main() -> int:
             k.forward(*wl.as_args(copies[(smp * a.burst + i) % len(copies)]), workspace=ws)
         torch.cuda.synchronize()
         t = {name: read(name).copy() for name in readers}
-        route = t["route"].reshape(-1, 2)
-        t0 = route[route[:, 0] > 0, 0].min()
+        starts = [t[name][:(SLOTS // per) * per].reshape(-1, per)[:, 0] for name, per, _ in TABLES]
+        t0 = min(x[x > 0].min() for x in starts if (x > 0).any())
         prev_end = None
         for name, per, _ in TABLES:
             m = t[name][:(SLOTS // per) * per].reshape(-1, per)
@@ -121,7 +122,7 @@ def main() -> int:
             "last end", "gap before"]
     title = f"config {a.config} (T = {cfg.T}, offset {cfg.local_expert_offset}), {a.samples} samples"
     if a.markdown:
-        print(f"Timeline of one call, {title} (µs from the first route workgroup's start, medians):\n")
+        print(f"Timeline of one call, {title} (µs from the call's first workgroup start, medians):\n")
         print("| kernel | " + " | ".join(cols) + " |")
         print("|---" * (len(cols) + 1) + "|")
     else:

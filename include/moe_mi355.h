@@ -122,15 +122,20 @@ typedef struct moe_mi355_args {
  *                                  with GEMM2 variants 1 and 6): bit-identical output,
  *                                  one launch fewer.  GEMM2 variant 6 is variant 1 with
  *                                  the combine computed inside it (T <= 32, the default
- *                                  there, after GEMM1 variant 5 or 1): bit-identical
- *                                  output, one launch fewer.
+ *                                  there, after GEMM1 variant 5, 1 or 9): bit-identical
+ *                                  output, one launch fewer.  GEMM1 variant 9 is variant 5
+ *                                  with the routing computed inside it too (T <= 4, the
+ *                                  default there; pairs with GEMM2 variant 6 only):
+ *                                  bit-identical output and workspace routing, one launch
+ *                                  fewer; it marks C beyond the fp16 range with a per-call
+ *                                  tag instead of clearing the flag word.
  *   MOE_MI355_FLAG_ROW_SCALES_ON / _OFF  GEMM1 reads the token scales gathered into row
  *                                  order / straight by token (default: gathered from
  *                                  T = 512, except under GEMM1 variants 7 and 8, which gather
  *                                  them itself).  Bit-identical results either way.  GEMM1
- *                                  variant 5 reads them by token: _ON selects the separate
- *                                  dispatch at T <= 64 (and is an error with variant 5
- *                                  forced).
+ *                                  variants 5 and 9 read them by token: _ON selects the
+ *                                  separate dispatch at T <= 64 (and is an error with
+ *                                  variant 5 or 9 forced).
  *   MOE_MI355_FLAG_LIST_ORDER      the prefill GEMM1 (variant 4) takes its work items in
  *                                  tile-list order also at T <= 3500 (by default it
  *                                  ranks them by expert rows there, which balances the

@@ -22,7 +22,7 @@ static int g_fail = 0;
         }                                                                      \
     } while (0)
 
-static const int32_t kTs[] = {INT32_MIN, -1, 0, 1, 2, 8, 16, 32, 33, 63, 64, 65, 88, 89, 299, 300, 511,
+static const int32_t kTs[] = {INT32_MIN, -1, 0, 1, 2, 4, 5, 8, 16, 32, 33, 63, 64, 65, 88, 89, 299, 300, 511,
                               512, 960, 961, 1024, 1344, 1345, 3500, 3501, 8192,
                               (1 << 19) - 1, 1 << 19, (1 << 19) + 1, INT32_MAX};
 
@@ -77,6 +77,8 @@ static unsigned long long sweep_plans() {
                 CHECK(p.tm == L.tile_m);
                 CHECK(p.tm2 == 0 || p.tm2 == 128);
                 CHECK(!p.dispatch_in_gemm1 || T <= moe::kDispatchInGemm1MaxT);
+                CHECK(!p.route_in_gemm1 || (T <= moe::kRouteInGemm1MaxT && p.dispatch_in_gemm1 &&
+                                             p.combine_in_gemm2 && p.g1 == 9));
                 CHECK(!p.combine_in_gemm2 || (T <= moe::kFusedCombineMaxT && p.tm == 16));
                 CHECK(L.combine_in_gemm2 == (p.combine_in_gemm2 ? 1 : 0));
                 check_layout(T, L);

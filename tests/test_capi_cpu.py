@@ -184,8 +184,9 @@ def _fake_args(k, T=4):
                                    (1, 2), (5, 2), (2, 6), (7, 3), (7, 1), (9, 5), (8, 1), (8, 3)])
 def test_forced_plan_that_cannot_run_is_an_error(lib, g1, g2):
     """A GEMM pair that cannot run together (GEMM1 writes hi/lo C but GEMM2 reads fp16,
-    mismatched tile heights, unknown variants: GEMM1 3, GEMM2 2 and 4, kernels of
-    earlier builds that no plan used, are gone) is rejected before any launch with
+    mismatched tile heights, GEMM1 9 with any GEMM2 but 6, unknown variants: GEMM1 3,
+    GEMM2 2 and 4, kernels of earlier builds that no plan used, are gone) is rejected
+    before any launch with
     MOE_ERR_BAD_FLAGS, and the Python entry turns the status into a RuntimeError."""
     k = pkg("kernel")
     a = _fake_args(k)
@@ -242,6 +243,15 @@ def test_layout_reports_the_forced_plan():
     assert k.workspace_layout(8, k.plan_flags(1, 6)).dispatch_in_gemm1 == 0
     for t, g1 in ((33, 5), (8, 2), (8, 4), (8, 7)):
         assert lib.moe_mi355_get_workspace_layout(t, k.plan_flags(g1, 6), ctypes.byref(lay)) == -7
+    # GEMM1 variant 9 (routing, dispatch and GEMM1 in one launch) up to T = 4, with
+    # GEMM2 variant 6 only
+    assert k.workspace_layout(4, k.plan_flags(9, 6)).dispatch_in_gemm1 == 1
+    assert k.workspace_layout(4, k.plan_flags(9, 6)).combine_in_gemm2 == 1
+    assert k.workspace_layout(4, k.plan_flags(9, 6)).tile_m == 16
+    for t, g2 in ((5, 6), (8, 6), (4, 1), (4, 3), (4, 5), (1, 1)):
+        assert lib.moe_mi355_get_workspace_layout(t, k.plan_flags(9, g2), ctypes.byref(lay)) == -7
+    assert lib.moe_mi355_get_workspace_layout(4, k.plan_flags(9, 6) | k.FLAG_ROW_SCALES_ON,
+                                              ctypes.byref(lay)) == -7
     # gathered token scales need the separate dispatch
     assert k.workspace_layout(8, k.FLAG_ROW_SCALES_ON).dispatch_in_gemm1 == 0
     assert k.workspace_layout(8, k.FLAG_ROW_SCALES_OFF).dispatch_in_gemm1 == 1
