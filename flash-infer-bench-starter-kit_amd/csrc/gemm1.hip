@@ -42,14 +42,26 @@ __global__ __launch_bounds__(256) void gemm1_rstream_kernel(
     using S = Gemm1Stream<CB, NGRP, TL>;
     __shared__ __attribute__((aligned(1024))) uint8_t slot_lds[4][S::kSlot];
     __shared__ v4f red[4][2][NGRP * CB][64];
+    // the first item's tile read before the tile count, both loads in flight together
+    // (blockIdx.x / kItems is inside the list's capacity: the grid has at most capacity x
+    // kItems workgroups; a workgroup past the count does not use what it read); each later
+    // tile is read after the item before it
+    const int4 tl0 = tiles[blockIdx.x / S::kItems];
+    int te = __builtin_amdgcn_readfirstlane(tl0.x), tr = __builtin_amdgcn_readfirstlane(tl0.y),
+        tn = __builtin_amdgcn_readfirstlane(tl0.z);
     const int nwork = (*num_tiles) * S::kItems;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     for (int work = blockIdx.x; work < nwork; work += gridDim.x) {
-        const int4 tile = tiles[work / S::kItems];
-        gemm1_rstream_item<D, CB, NGRP, TL>(hidden, sa, w1, s1, tile.x, tile.y, tile.z,
+        gemm1_rstream_item<D, CB, NGRP, TL>(hidden, sa, w1, s1, te, tr, tn,
                                             (work % S::kItems) * NGRP,
                                             [&](int row) { return sorted_tok[row]; }, C, c_wide,
                                             slot_lds, red, wave);
+        if (work + (int)gridDim.x < nwork) {
+            const int4 t = tiles[(work + gridDim.x) / S::kItems];
+            te = t.x;
+            tr = t.y;
+            tn = t.z;
+        }
     }
 }
 

@@ -37,15 +37,28 @@ __global__ __launch_bounds__(256) void gemm2_rstream_kernel(
     __shared__ __attribute__((aligned(1024))) uint8_t slot_lds[4][16 * HF * kBlk];
     __shared__ v4f red[4][HF][CB][64];
     MOE_STAMP(2 * (int)blockIdx.x);
+    // The first item's tile is read before the tile count, so that the two loads are in
+    // flight together instead of one after the other: blockIdx.x / kItems is inside the
+    // list's capacity (the grid has at most capacity x kItems workgroups), and a workgroup
+    // past the count does not use what it read.  Each later tile is read after the item
+    // before it.
+    const int4 tl0 = tiles[blockIdx.x / kItems];
+    int te = __builtin_amdgcn_readfirstlane(tl0.x), tr = __builtin_amdgcn_readfirstlane(tl0.y),
+        tn = __builtin_amdgcn_readfirstlane(tl0.z);
     const int nwork = (*num_tiles) * kItems;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     // the two paths keep separate loops, so each is register-allocated on its own
     if (__builtin_amdgcn_readfirstlane(flags[0]) == 0) {
         for (int work = blockIdx.x; work < nwork; work += gridDim.x) {
-            const int4 tile = tiles[work / kItems];
-            gemm2_rstream_item<D, KSPLIT, HF, CB>(C.f16(), w2, s2, tile.x, tile.y, tile.z,
+            gemm2_rstream_item<D, KSPLIT, HF, CB>(C.f16(), w2, s2, te, tr, tn,
                                                   (work % kItems) * NGW * HF, rows, flags + 1,
                                                   slot_lds, red, wave);
+            if (work + (int)gridDim.x < nwork) {
+                const int4 t = tiles[(work + gridDim.x) / kItems];
+                te = t.x;
+                tr = t.y;
+                tn = t.z;
+            }
         }
     } else {
         for (int work = blockIdx.x; work < nwork; work += gridDim.x) {
