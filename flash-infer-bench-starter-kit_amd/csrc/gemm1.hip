@@ -247,19 +247,31 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(WPE)))
     // token rows: T * 7168 < 2^32 (kMaxT); token scales: 56 x stride floats
     const __amdgpu_buffer_rsrc_t rs_h = buffer_rsrc(hidden, (uint32_t)T * kH);
     const __amdgpu_buffer_rsrc_t rs_s = buffer_rsrc(sa.p, (uint32_t)kHB * (uint32_t)sa.stride * 4);
+    // the first item's tile read before the tile count, both loads in flight together
+    // (blockIdx.x / kItems is inside the list's capacity: the grid has at most capacity x
+    // kItems workgroups; a workgroup past the count does not use what it read); each later
+    // tile is read after the item before it
+    const int4 tl0 = tiles[blockIdx.x / S::kItems];
+    int te = __builtin_amdgcn_readfirstlane(tl0.x), tr = __builtin_amdgcn_readfirstlane(tl0.y),
+        tn = __builtin_amdgcn_readfirstlane(tl0.z);
     const int nwork = (*num_tiles) * S::kItems;
     int G = gridDim.x;
     if (WPE == 3 && G == 768 && nwork > 768 && nwork <= 1024) G = 512;
     if ((int)blockIdx.x >= G) return;   // uniform: the whole workgroup
     for (int work = blockIdx.x; work < nwork; work += G) {
-        const int4 tile = tiles[work / S::kItems];
         const int ng = (work % S::kItems) * NWV + wave;
-        with_live_blocks(live_blocks(0, tile.z), [&](auto live) {
+        with_live_blocks(live_blocks(0, tn), [&](auto live) {
             constexpr int CB = decltype(live)::value;
             if constexpr (CB > 0)
-                gemm1_shared_item<D, NWV, CB>(hidden, sa, rs_h, rs_s, w1, s1, tile.x, tile.y, tile.z, ng,
+                gemm1_shared_item<D, NWV, CB>(hidden, sa, rs_h, rs_s, w1, s1, te, tr, tn, ng,
                                          sorted_tok, C, c_wide, lds, wave);
         });
+        if (work + G < nwork) {
+            const int4 t = tiles[(work + G) / S::kItems];
+            te = t.x;
+            tr = t.y;
+            tn = t.z;
+        }
         __syncthreads();   // the next item's first loads reuse the token stages
     }
 }
