@@ -16,15 +16,21 @@ namespace moe {
 // One row per workgroup pass; wave w converts columns 512 w .. 512 w + 511, lane l eight
 // of them, and the 16 lanes of each 128-column block share its absmax by xor shuffles.
 __global__ __launch_bounds__(256) void c_f16_to_hilo_kernel(Intermediate C, const int* __restrict__ meta) {
-    const int na = meta[kEL];                 // rows of this call
-    const bool wide = meta[kCWideFlag] != 0;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int col = wave * 512 + lane * 8;
     const int block = col >> 7;
+    // the first row's values are read before the row count, so that the two loads are in
+    // flight together (blockIdx.x < the grid <= the row capacity of C; a workgroup past
+    // the count does not use them); each later row's values are read ahead of the
+    // conversion of the row before
+    uint4 hv = *reinterpret_cast<const uint4*>(C.f16() + (size_t)blockIdx.x * kI + col);
+    const int na = meta[kEL];                 // rows of this call
+    const bool wide = meta[kCWideFlag] != 0;
     for (int row = blockIdx.x; row < na; row += gridDim.x) {
         const size_t off = (size_t)row * kI + col;
-        const uint4 hv = *reinterpret_cast<const uint4*>(C.f16() + off);
         const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
+        if (row + (int)gridDim.x < na)
+            hv = *reinterpret_cast<const uint4*>(C.f16() + off + (size_t)gridDim.x * kI);
         // the group exponent applies only on a call whose flag is raised
         const int e = wide ? C.f16_exp()[(size_t)row * (kI / kGroup16) + col / kGroup16] : 0;
         float x[8];

@@ -157,10 +157,17 @@ __global__ __launch_bounds__(kChunk) void dispatch_place_kernel(
 __global__ __launch_bounds__(256) void gather_row_scales_kernel(
     const float* __restrict__ hs_scale, int T, const int* __restrict__ sorted_tok,
     const int* __restrict__ exp_off, float* __restrict__ row_scales, int rows_cap) {
+    // the first row's token is read before the row count, so that the two loads are in
+    // flight together (its index clamped to the permutation's capacity; a thread past the
+    // count does not use it, and no scale is read before the count says the token is real)
+    const int row0 = blockIdx.x * 256 + threadIdx.x;
+    int tok = sorted_tok[min(row0, rows_cap - 1)];
     const int na = exp_off[kEL];
     const int kb = blockIdx.y;
-    for (int row = blockIdx.x * 256 + threadIdx.x; row < na; row += gridDim.x * 256)
-        row_scales[(size_t)kb * rows_cap + row] = hs_scale[(size_t)kb * T + sorted_tok[row]];
+    for (int row = row0; row < na; row += gridDim.x * 256) {
+        if (row != row0) tok = sorted_tok[row];
+        row_scales[(size_t)kb * rows_cap + row] = hs_scale[(size_t)kb * T + tok];
+    }
 }
 
 void launch_gather_row_scales(const float* hs_scale, int T, const int* sorted_tok,
