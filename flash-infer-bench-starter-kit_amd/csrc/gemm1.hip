@@ -89,20 +89,6 @@ struct Gemm1Shared {
     static constexpr int kRowsPerWave = 64 / NWV;           // token rows each wave moves
 };
 
-// vmcnt immediate for v = 0 .. 24 (uniform v; the switch keeps every wait an immediate)
-__device__ __forceinline__ void wait_vm_upto24(int v) {
-    switch (v) {
-#define MOE_WAIT_CASE(n) case n: __builtin_amdgcn_s_waitcnt(vmcnt_imm(n)); break;
-        MOE_WAIT_CASE(1) MOE_WAIT_CASE(2) MOE_WAIT_CASE(3) MOE_WAIT_CASE(4) MOE_WAIT_CASE(5)
-        MOE_WAIT_CASE(6) MOE_WAIT_CASE(7) MOE_WAIT_CASE(8) MOE_WAIT_CASE(9) MOE_WAIT_CASE(10)
-        MOE_WAIT_CASE(11) MOE_WAIT_CASE(12) MOE_WAIT_CASE(13) MOE_WAIT_CASE(14) MOE_WAIT_CASE(15)
-        MOE_WAIT_CASE(16) MOE_WAIT_CASE(17) MOE_WAIT_CASE(18) MOE_WAIT_CASE(19) MOE_WAIT_CASE(20)
-        MOE_WAIT_CASE(21) MOE_WAIT_CASE(22) MOE_WAIT_CASE(23) MOE_WAIT_CASE(24)
-#undef MOE_WAIT_CASE
-        default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
-    }
-}
-
 // One item of gemm1_shared_kernel with CB live 16-row blocks (the tile has 16 CB - 15 ..
 // 16 CB rows): wave `wave` computes SwiGLU columns 16 ng .. 16 ng + 15 of rows row0 ..
 // row0 + nrows - 1.

@@ -367,11 +367,16 @@ __global__ void e4m3_to_f16_kernel(const uint32_t* __restrict__ in, uint2* __res
 
 static int grid_for2(long long work) { return (int)(work < 4096 ? work : 4096); }
 
+bool launch_gemm2_shared(const Intermediate&, int*, const uint8_t*, const float*, const int4*, const int*,
+                         int, const ExpertRows&, hipStream_t);
+
 // Variants (the tile height of the dispatch they expect, and the form of C they read):
 //   1  register-staged streaming, 32 columns x 1 row block per wave      16-row   fp16
 //   3  register-staged streaming, 64 columns x 2 row blocks per wave     32-row   fp16
 //   5  prefill, 8 waves, 128 x 256 workgroup tile, over the 128-row second tile list
 //      of the dispatch (whatever the first list's height)                         hi/lo
+//   7  token-sharing: 64-row tile x 128 columns, C rows shared in LDS (gemm2_shared.hip)
+//                                                                      64-row   fp16
 bool launch_gemm2(int variant, const Intermediate& C, const uint8_t* w2, const float* s2,
                   const int4* tiles, const int* num_tiles, const int* exp_off, int max_tiles,
                   const ExpertRows& rows, hipStream_t stream) {
@@ -391,6 +396,8 @@ bool launch_gemm2(int variant, const Intermediate& C, const uint8_t* w2, const f
             launch_kernel(gemm2_prefill8_kernel, dim3(256), dim3(512), 0, stream, C, w2, s2, tiles,
                                num_tiles, exp_off, rows, flags + 1);
             return true;
+        case 7:
+            return launch_gemm2_shared(C, flags, w2, s2, tiles, num_tiles, max_tiles, rows, stream);
         default: return false;
     }
 }

@@ -30,13 +30,15 @@ constexpr int kMinTileM = 16;           // smallest row tile; sizes the tile lis
 // fp16 C of a streaming GEMM1 is converted to the hi/lo form for a prefill GEMM2.
 // Small T streams weights with the register-staged kernels, C in fp16: 16-row tiles up
 // to T = 88, 32-row tiles (GEMM1 with two column groups per wave, GEMM2 with two row
-// blocks per wave) beyond.  From T = 300 GEMM1 is the token-sharing kernel on 64-row
+// blocks per wave) beyond.  From T = 200 GEMM1 is the token-sharing kernel on 64-row
 // tiles (fewer requests per output once an expert has dozens of rows; variant 8, which
-// runs three or two workgroups per CU as the call's tile count makes best), feeding the
-// prefill GEMM2 (128-row tiles, FP8 MFMA on the hi/lo form); from T = 1345 both GEMMs are
-// the MFMA-bound prefill kernels on 256-row tiles (GEMM2 on the 128-row second list).  The
-// boundaries come from wall-clock sweeps of the pairs at T = 72 .. 2560 on MI355X over
-// routing seeds from light to heavy routing to the local experts.  Between T = 961 and
+// runs three or two workgroups per CU as the call's tile count makes best), feeding up to
+// T = 559 the token-sharing GEMM2 on the same tiles (variant 7: fp16 C, no conversion;
+// 1-13 us faster than the neighbouring pairs at T = 200 .. 560 over three routings) and
+// beyond the prefill GEMM2 (128-row tiles, FP8 MFMA on the hi/lo form); from T = 1345 both
+// GEMMs are the MFMA-bound prefill kernels on 256-row tiles (GEMM2 on the 128-row second
+// list).  The boundaries come from wall-clock sweeps of the pairs at T = 72 .. 2560 on
+// MI355X over routing seeds from light to heavy routing to the local experts.  Between T = 961 and
 // 1344 variant 8 was 6-25 us faster than variant 7 (always two per CU) on three routings
 // and 4-10 us slower on three; heavier routing there can prefer the prefill pair.
 struct Plan {
@@ -52,7 +54,7 @@ struct Plan {
 
 inline int g1_tile_m(int v) { return v == 1 || v == 5 || v == 9 ? 16 : v == 2 ? 32 : v == 7 || v == 8 ? 64 : 256; }
 inline bool g1_hilo(int v) { return v == 4; }        // GEMM1 writes the hi/lo form
-inline bool g2_hilo(int v) { return v == 5; }        // GEMM2 reads the hi/lo form
+inline bool g2_hilo(int v) { return v == 5; }        // GEMM2 reads the hi/lo form (7: fp16)
 
 // The plan of a GEMM1 / GEMM2 pair, false when they cannot run together.  GEMM1
 // variant 5 is variant 1 with the dispatch folded in (T <= 64): every workgroup of a
@@ -76,6 +78,11 @@ inline bool make_plan(int g1, int g2, int32_t T, Plan* p) {
     }
     if (g1 == 1 && g2 == 6) {
         *p = {16, 0, 1, 6, false, false, false, true};
+        return true;
+    }
+    if (g2 == 7) {   // the token-sharing GEMM2 over the token-sharing GEMM1's 64-row tiles
+        if (g1 != 7 && g1 != 8) return false;
+        *p = {64, 0, g1, 7, false, false, false, false};
         return true;
     }
     if ((g1 != 1 && g1 != 2 && g1 != 4 && g1 != 7 && g1 != 8) || (g2 != 1 && g2 != 3 && g2 != 5)) return false;
@@ -120,7 +127,8 @@ inline int plan_for(int32_t T, int32_t flags, Plan* p) {
     else if (T <= kFusedCombineMaxT && !on) g1 = 5, g2 = 6;
     else if (T <= kDispatchInGemm1MaxT && !on) g1 = 5, g2 = 1;
     else if (T <= 88) g1 = 1, g2 = 1;
-    else if (T <= 299) g1 = 2, g2 = 3;
+    else if (T <= 199) g1 = 2, g2 = 3;
+    else if (T <= 559) g1 = 8, g2 = 7;
     else if (T <= 1344) g1 = 8, g2 = 5;
     else g1 = 4, g2 = 5;
     if (flags & MOE_MI355_FLAG_FORCE_PLAN) {

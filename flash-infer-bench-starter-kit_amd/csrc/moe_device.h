@@ -303,6 +303,20 @@ __device__ __forceinline__ constexpr int vmcnt_imm(int v) {
     return (v & 15) | ((v >> 4) << 14) | (7 << 4) | (15 << 8);
 }
 
+// vmcnt immediate for v = 0 .. 24 (uniform v; the switch keeps every wait an immediate)
+__device__ __forceinline__ void wait_vm_upto24(int v) {
+    switch (v) {
+#define MOE_WAIT_CASE(n) case n: __builtin_amdgcn_s_waitcnt(vmcnt_imm(n)); break;
+        MOE_WAIT_CASE(1) MOE_WAIT_CASE(2) MOE_WAIT_CASE(3) MOE_WAIT_CASE(4) MOE_WAIT_CASE(5)
+        MOE_WAIT_CASE(6) MOE_WAIT_CASE(7) MOE_WAIT_CASE(8) MOE_WAIT_CASE(9) MOE_WAIT_CASE(10)
+        MOE_WAIT_CASE(11) MOE_WAIT_CASE(12) MOE_WAIT_CASE(13) MOE_WAIT_CASE(14) MOE_WAIT_CASE(15)
+        MOE_WAIT_CASE(16) MOE_WAIT_CASE(17) MOE_WAIT_CASE(18) MOE_WAIT_CASE(19) MOE_WAIT_CASE(20)
+        MOE_WAIT_CASE(21) MOE_WAIT_CASE(22) MOE_WAIT_CASE(23) MOE_WAIT_CASE(24)
+#undef MOE_WAIT_CASE
+        default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
+    }
+}
+
 // Workgroup barrier that orders LDS only.  __syncthreads() is a release/acquire of all
 // memory at workgroup scope, which waits for every outstanding vector-memory load
 // (vmcnt(0)) and would drain the weight ring at every K block; here the caller has

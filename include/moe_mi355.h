@@ -109,14 +109,17 @@ typedef struct moe_mi355_args {
  *                                  sweeps and tests.  GEMM1: 1 streaming 16-row tiles,
  *                                  2 streaming 32-row tiles, 4 prefill 256-row tiles,
  *                                  7 streaming with shared token rows, 64-row tiles
- *                                  (pairs with GEMM2 5 only), two workgroups per CU,
- *                                  8 the same held to three per CU, of which it runs
+ *                                  (pairs with GEMM2 5 and 7 only), two workgroups per
+ *                                  CU, 8 the same held to three per CU, of which it runs
  *                                  three or two by the call's tile count (the default
- *                                  for 300 <= T <= 1344);
+ *                                  for 200 <= T <= 1344);
  *                                  GEMM2: 1 streaming 16-row, 3 streaming 32-row,
- *                                  5 prefill on a second list of 128-row tiles.  A pair
- *                                  that cannot run together, or an unknown variant,
- *                                  gives MOE_ERR_BAD_FLAGS.
+ *                                  5 prefill on a second list of 128-row tiles (the
+ *                                  default for 560 <= T), 7 streaming with shared C
+ *                                  rows on the 64-row tiles of GEMM1 7 or 8 (the default
+ *                                  for 200 <= T <= 559).  A pair that cannot run
+ *                                  together, or an unknown variant, gives
+ *                                  MOE_ERR_BAD_FLAGS.
  *                                  GEMM1 variant 5 is variant 1 with the dispatch
  *                                  computed inside it (T <= 64, the default there; pairs
  *                                  with GEMM2 variants 1 and 6): bit-identical output,

@@ -223,11 +223,13 @@ def test_list_order_flag_is_known_and_keeps_the_plan():
 def test_layout_reports_the_forced_plan():
     k = pkg("kernel")
     assert k.workspace_layout(64).tile_m == 16 and k.workspace_layout(64).intermediate_format == 0
-    # 32-row streaming tiles up to T = 299, then the token-sharing GEMM1 on 64-row tiles
-    # (C converted to the hi/lo form for the prefill GEMM2), then 256-row prefill tiles
-    assert [k.workspace_layout(t).tile_m for t in (89, 299, 300, 960, 961, 1344, 1345)] == \
+    # 32-row streaming tiles up to T = 199, then the token-sharing GEMM1 on 64-row tiles
+    # (fp16 C for the token-sharing GEMM2 up to T = 559, C converted to the hi/lo form for
+    # the prefill GEMM2 beyond), then 256-row prefill tiles
+    assert [k.workspace_layout(t).tile_m for t in (89, 199, 200, 559, 560, 1344, 1345)] == \
         [32, 32, 64, 64, 64, 64, 256]
-    assert [k.workspace_layout(t).intermediate_format for t in (299, 300, 1344, 1345)] == [0, 2, 2, 1]
+    assert [k.workspace_layout(t).intermediate_format for t in (199, 200, 559, 560, 1344, 1345)] == \
+        [0, 0, 0, 2, 2, 1]
     # GEMM1 computes the dispatch itself up to T = 64, a dispatch launch from T = 65
     assert [k.workspace_layout(t).dispatch_in_gemm1 for t in (1, 8, 64, 65, 200, 9000)] == [1, 1, 1, 0, 0, 0]
     assert k.workspace_layout(64, k.plan_flags(1, 1)).dispatch_in_gemm1 == 0
@@ -252,6 +254,12 @@ def test_layout_reports_the_forced_plan():
         assert lib.moe_mi355_get_workspace_layout(t, k.plan_flags(9, g2), ctypes.byref(lay)) == -7
     assert lib.moe_mi355_get_workspace_layout(4, k.plan_flags(9, 6) | k.FLAG_ROW_SCALES_ON,
                                               ctypes.byref(lay)) == -7
+    # the token-sharing GEMM2 (variant 7) reads the fp16 C of the token-sharing GEMM1s on
+    # their 64-row tiles: no conversion, no second tile list
+    lay7 = k.workspace_layout(600, k.plan_flags(8, 7))
+    assert (lay7.tile_m, lay7.intermediate_format) == (64, 0)
+    for g1 in (1, 2, 4, 5, 9):
+        assert lib.moe_mi355_get_workspace_layout(600, k.plan_flags(g1, 7), ctypes.byref(lay)) == -7
     # gathered token scales need the separate dispatch
     assert k.workspace_layout(8, k.FLAG_ROW_SCALES_ON).dispatch_in_gemm1 == 0
     assert k.workspace_layout(8, k.FLAG_ROW_SCALES_OFF).dispatch_in_gemm1 == 1

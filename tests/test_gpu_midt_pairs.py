@@ -6,8 +6,9 @@ workgroups per CU work: two when the items (64-row tiles x 32) fall in (768, 102
 both take two rounds, three otherwise.  The light routing of config 2 (707 rows) lands
 in that window, the heavy one (eight hot local experts, every token routed to them) far
 above it, so both paths run.  Every pair that can run at this T -- the default, the
-two-per-CU token-sharing GEMM1 (7/5), the prefill pair (4/5) and the 32-row streaming
-GEMM1 with the conversion (2/5) -- must match the fp32 oracle on sampled tokens."""
+two-per-CU token-sharing GEMM1 (7/5), both token-sharing GEMM1s with the token-sharing
+GEMM2 (8/7, 7/7), the prefill pair (4/5) and the 32-row streaming GEMM1 with the
+conversion (2/5) -- must match the fp32 oracle on sampled tokens."""
 import numpy as np
 import pytest
 import torch
@@ -17,7 +18,7 @@ from gpu_common import compare_to_oracle, config_inputs, note
 
 pytestmark = pytest.mark.gpu
 
-PAIRS = [(8, 5), (7, 5), (4, 5), (2, 5)]
+PAIRS = [(8, 5), (7, 5), (8, 7), (7, 7), (4, 5), (2, 5)]
 
 
 def _inputs(routing):
@@ -67,3 +68,4 @@ def test_every_pair_matches_oracle_at_t1024(routing):
     assert torch.equal(default_out.view(torch.int16), forced[(8, 5)].view(torch.int16))
     # variants 7 and 8 compute every item the same way: only the workgroup differs
     assert torch.equal(forced[(7, 5)].view(torch.int16), forced[(8, 5)].view(torch.int16))
+    assert torch.equal(forced[(7, 7)].view(torch.int16), forced[(8, 7)].view(torch.int16))

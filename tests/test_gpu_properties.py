@@ -107,13 +107,13 @@ def test_small_odd_batches(T):
     assert st["frac_within"] == 1.0, st
 
 
-@pytest.mark.parametrize("T", [88, 89, 299, 300, 640, 641, 960, 961, 1344, 1345])
+@pytest.mark.parametrize("T", [88, 89, 199, 200, 559, 560, 640, 641, 960, 961, 1344, 1345])
 def test_plan_boundaries_match_oracle(T):
     """Token counts on both sides of every change of kernel plan (16-row streaming,
     32-row streaming, the token-sharing GEMM1 on 64-row tiles with three and then two
-    workgroups per CU feeding the prefill GEMM2, 256-row prefill tiles) and of the
-    dispatch (one workgroup up to T = 640, count and place kernels over 256-token
-    chunks beyond)."""
+    workgroups per CU feeding the token-sharing GEMM2 and then the prefill GEMM2, 256-row
+    prefill tiles) and of the dispatch (one workgroup up to T = 640, count and place
+    kernels over 256-token chunks beyond)."""
     d = first_tokens(config_inputs(3), T)
     note(f"[gpu] plan boundary T={T}")
     out = run_forward(d)
@@ -127,7 +127,9 @@ def test_plan_boundaries_match_oracle(T):
 @pytest.mark.parametrize("T,g1,g2", [(64, 1, 1), (150, 1, 1), (64, 2, 3), (500, 2, 3),
                                      (1000, 4, 5), (3000, 4, 5), (1500, 2, 5), (150, 1, 5),
                                      (1000, 7, 5), (300, 7, 5), (37, 7, 5), (2000, 7, 5),
-                                     (600, 8, 5), (150, 8, 5), (1500, 8, 5), (500, 2, 5)])
+                                     (600, 8, 5), (150, 8, 5), (1500, 8, 5), (500, 2, 5),
+                                     (600, 8, 7), (1000, 7, 7), (300, 8, 7), (150, 8, 7),
+                                     (37, 7, 7), (1500, 8, 7)])
 def test_every_gemm_variant_matches_oracle(T, g1, g2):
     """Each GEMM1 / GEMM2 kernel variant (forced with the call's plan flags) stays
     within the tolerance."""
@@ -371,11 +373,11 @@ def test_values_beyond_fp16_range_converted_plan():
 
 
 def test_values_beyond_fp16_range_32_row_streaming_plan():
-    """T = 200 (the default plan there: 32-row streaming GEMM1, variant 2, and the
+    """T = 150 (the default plan there: 32-row streaming GEMM1, variant 2, and the
     32-row streaming GEMM2, variant 3, whose rare path reads C's group exponents)."""
-    d = first_tokens(config_inputs(3), 200)
-    note("[gpu] values beyond the fp16 range, T=200, plan 2/3")
-    lay = pkg("kernel").workspace_layout(200)
+    d = first_tokens(config_inputs(3), 150)
+    note("[gpu] values beyond the fp16 range, T=150, plan 2/3")
+    lay = pkg("kernel").workspace_layout(150)
     assert lay.tile_m == 32 and lay.intermediate_format == 0
     _huge_inputs_check(d, c_flag=1)
 
@@ -392,6 +394,14 @@ def test_values_beyond_fp16_range_token_sharing_gemm1():
     d = first_tokens(config_inputs(3), 1024)
     note("[gpu] values beyond the fp16 range, T=1024, GEMM1 variant 7")
     _huge_inputs_check(d, c_flag=1, flags=pkg("kernel").plan_flags(7, 5))
+
+
+def test_values_beyond_fp16_range_token_sharing_gemm2():
+    """T = 600 with the token-sharing GEMM2 (variant 7) forced after the token-sharing
+    GEMM1: its rare path rebuilds C from the group exponents, one row block at a time."""
+    d = first_tokens(config_inputs(3), 600)
+    note("[gpu] values beyond the fp16 range, T=600, plan 8/7")
+    _huge_inputs_check(d, c_flag=1, flags=pkg("kernel").plan_flags(8, 7))
 
 
 def test_values_beyond_fp16_range_prefill_plan():

@@ -65,8 +65,9 @@ def test_host_logic_default_plans(drivers):
     assert g(5) == (5, 6) and g(32) == (5, 6)
     assert g(33) == (5, 1) and g(64) == (5, 1)
     assert g(65) == (1, 1) and g(88) == (1, 1)
-    assert g(89) == (2, 3) and g(299) == (2, 3)
-    assert g(300) == (8, 5) and g(960) == (8, 5)
+    assert g(89) == (2, 3) and g(199) == (2, 3)
+    assert g(200) == (8, 7) and g(559) == (8, 7)
+    assert g(560) == (8, 5) and g(960) == (8, 5)
     assert g(961) == (8, 5) and g(1344) == (8, 5)
     assert g(1345) == (4, 5) and g(1 << 19) == (4, 5)
     assert "T -1 status -2" in out and f"T {(1 << 19) + 1} status -2" in out
