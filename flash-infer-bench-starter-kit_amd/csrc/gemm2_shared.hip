@@ -19,11 +19,14 @@
 // a 16-row block past the tile moves nothing and its MFMAs are skipped); one barrier per
 // K block hands a stage over.  In a stage, row r keeps its 16-byte chunk c at position
 // c ^ (r mod 16), so the 16 rows an MFMA operand read touches land on 16 different bank
-// groups.  Against the prefill GEMM2 on 128-row tiles (one workgroup per CU, W2 by
-// LDS DMA) this keeps more W2 bytes in flight per CU and reads C in the fp16 form the
-// token-sharing GEMM1 writes, so the fp16 -> hi/lo conversion launch goes away.
+// groups.  It reads C in the fp16 form the token-sharing GEMM1 writes, so the fp16 ->
+// hi/lo conversion launch of the prefill GEMM2 goes away, and it has two workgroups per CU
+// (212 registers, 64 KB of LDS) where the prefill GEMM2 has one.  Measured against that
+// pair it is faster while the tiles hold few rows (T = 200 .. 559, the plan there) and
+// slower beyond, where it moves about as much C per item as W2 at a similar per-CU rate.
 // When GEMM1 flagged C beyond the fp16 range, each wave computes its columns on the rare
-// path of the streaming GEMM2 (bf16 MFMAs on C rebuilt from its group exponents).
+// path of the streaming GEMM2 (bf16 MFMAs on C rebuilt from its group exponents), one
+// 16-row block at a time.
 
 #include "gemm2_stream.h"
 
