@@ -106,12 +106,28 @@ __global__ __launch_bounds__(kChunk) void dispatch_place_kernel(
     const int chunk = blockIdx.x;
 
     const TokenRoutes r = load_routes(topk_ids, topk_w, chunk * kChunk + tid, T, offset);
+    // thread (g, e) sums expert e's counts over chunks g, g + kGroups, ...: the first kPre of
+    // them are read here, together with the routes, and summed after the ranks (up to
+    // T = kChunk * kGroups * kPre every count; beyond, the rest one stride at a time)
+    constexpr int kPre = 8;
+    const int e = tid % kEL, g = tid / kEL;
+    int pre[kPre];
+#pragma unroll
+    for (int i = 0; i < kPre; ++i) {
+        const int c = g + i * kGroups;
+        pre[i] = c < nchunks ? chunk_cnt[c * kEL + e] : 0;
+    }
     int rank[kTopK];
     wave_ranks(r, wave, lane, wcnt, bal[wave], rank);
     {
-        const int e = tid % kEL, g = tid / kEL;
         int total = 0, before = 0;
-        for (int c = g; c < nchunks; c += kGroups) {
+#pragma unroll
+        for (int i = 0; i < kPre; ++i) {
+            const int c = g + i * kGroups;
+            before += (c < chunk) ? pre[i] : 0;
+            total += pre[i];
+        }
+        for (int c = g + kPre * kGroups; c < nchunks; c += kGroups) {
             const int v = chunk_cnt[c * kEL + e];
             before += (c < chunk) ? v : 0;
             total += v;
