@@ -64,12 +64,15 @@ __device__ __forceinline__ float canon_sigmoid(float x) {
 
 // ---- cross-lane helpers (DPP; identity 0 for unsigned max) ------------------
 
-// value of lane i^1, i^2 (quad permutes) and i^4 (swap of the two quads of an octet)
+// value of lane i^1, i^2 (quad permutes) and i^4 (swap of the two quads of an octet).
+// Where every lane has a source lane (quad permutes, row rotations) the DPP moves are
+// written with old = 0 and bound_ctrl set, which lets the compiler fold each into the
+// max or min that consumes it (v_max_u32_dpp): the same values, one instruction fewer.
 __device__ __forceinline__ uint32_t xor1(uint32_t v) {
-    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xb1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xb1, 0xf, 0xf, true);  // quad_perm [1,0,3,2]
 }
 __device__ __forceinline__ uint32_t xor2(uint32_t v) {
-    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4e, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4e, 0xf, 0xf, true);  // quad_perm [2,3,0,1]
 }
 __device__ __forceinline__ uint32_t xor4(uint32_t v) {
     // banks 0,2 (lanes 0-3, 8-11 of a row) read lane+4; banks 1,3 read lane-4
@@ -79,7 +82,7 @@ __device__ __forceinline__ uint32_t xor4(uint32_t v) {
 
 // value of lane i^8 (rotation by 8 inside each row of 16 lanes)
 __device__ __forceinline__ uint32_t xor8(uint32_t v) {
-    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xf, 0xf, false);  // row_ror:8
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xf, 0xf, true);  // row_ror:8
 }
 // value of lane i^16 and i^32: v_permlane16_swap / v_permlane32_swap of v with itself
 // leave the value of the partner row (half) in the second result for even rows (the
@@ -97,10 +100,10 @@ __device__ __forceinline__ uint32_t xor32(uint32_t v, int lane) {
 // inside each row, then the row and half swaps (each lane meets every other lane's
 // value; no lane reads past its row)
 __device__ __forceinline__ uint32_t wave_max_all(uint32_t v) {
-    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xb1, 0xf, 0xf, false));   // quad_perm [1,0,3,2]
-    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4e, 0xf, 0xf, false));   // quad_perm [2,3,0,1]
-    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x124, 0xf, 0xf, false));  // row_ror:4
-    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xf, 0xf, false));  // row_ror:8
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xb1, 0xf, 0xf, true));   // quad_perm [1,0,3,2]
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4e, 0xf, 0xf, true));   // quad_perm [2,3,0,1]
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x124, 0xf, 0xf, true));  // row_ror:4
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xf, 0xf, true));  // row_ror:8
     auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
     v = max((uint32_t)p[0], (uint32_t)p[1]);
     p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
