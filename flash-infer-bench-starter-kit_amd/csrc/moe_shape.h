@@ -25,8 +25,9 @@ constexpr int kN1B = kN1 / kBlk;   // 32 GEMM1 output blocks
 // Where no route kernel runs (GEMM1 variant 9 routes its tokens itself), the first word
 // is not cleared: that GEMM1 writes the call's tag (a value >= 2, different on every
 // call) there instead of 1, and its GEMM2 (variant 6) compares the word with the tag.
-// A word that holds the tag for another reason only sends GEMM2 down its rare path,
-// which reads C's group exponents, and GEMM1 writes every exponent on every call.
+// A word that holds the tag for another reason (garbage, or a HIP graph replaying one
+// call's tag after a replay whose C was wide) only sends GEMM2 down its rare path, which
+// reads C's group exponents, and GEMM1 writes every exponent on every call.
 constexpr int kCWideFlag = kEL + 3;
 constexpr int kRowsWideFlag = kEL + 4;
 constexpr int kGroup16 = 16;       // columns per fp16-form exponent byte
