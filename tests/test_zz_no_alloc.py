@@ -54,7 +54,8 @@ def test_noalloc_rejects_sizes_beyond_its_maximum():
 @pytest.mark.gpu
 def test_noalloc_matches_forward_on_consecutive_calls():
     """T = 256 (the maximum), then smaller calls on the same array (37 tokens with
-    another expert offset, then 5): each output is bit-identical to
+    another expert offset, then 5, then 3, where GEMM1 routes the tokens itself and marks
+    the array's flag word with its call tag): each output is bit-identical to
     moe_mi355_forward's with a fresh workspace, and the call allocates no memory
     through torch."""
     from gpu_common import config_inputs, first_tokens, note
@@ -63,7 +64,7 @@ def test_noalloc_matches_forward_on_consecutive_calls():
     L = k._build_extension()
     dev = torch.device("cuda:0")
     full = config_inputs(3)
-    for T, offset in ((MAX_T, 0), (37, 64), (5, 0)):
+    for T, offset in ((MAX_T, 0), (37, 64), (5, 0), (3, 32)):
         d = first_tokens(full, T)
         d["local_expert_offset"] = offset
         note(f"[gpu] noalloc T={T} offset={offset}")
@@ -85,7 +86,7 @@ def test_noalloc_matches_forward_on_consecutive_calls():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("T", [8, MAX_T])
+@pytest.mark.parametrize("T", [3, 8, MAX_T])
 def test_noalloc_under_graph_capture(T):
     """After one eager call on the device (which looks up the array's address and the
     launch grid), noalloc calls can be captured into a HIP graph: each replay, run
