@@ -1,6 +1,6 @@
 """The GEMM pairs of mid-size T on a light and a heavy routing (T = 1024).
 
-Between T = 300 and 1344 the default GEMM1 (variant 8, token-sharing, three workgroups
+Between T = 200 and 1344 the default GEMM1 (variant 8, token-sharing, three workgroups
 per CU) decides on the device, from the call's tile count, whether three or two
 workgroups per CU work: two when the items (64-row tiles x 32) fall in (768, 1024], where
 both take two rounds, three otherwise.  The light routing of config 2 (707 rows) lands
