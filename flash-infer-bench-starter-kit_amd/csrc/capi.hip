@@ -29,9 +29,13 @@
 #include "moe_mi355.h"
 
 namespace moe {
-void launch_route(const float*, const uint16_t*, int, float, int*, float*, int*, hipStream_t);
+void launch_route(const float*, const uint16_t*, int, float, int*, float*, int*, uint32_t*, int,
+                  hipStream_t);
 bool launch_dispatch(const int*, const float*, int, int, int, int, int*, int*, int4*, int*, float*,
                      int*, int*, hipStream_t, int*, int4*);
+bool launch_dispatch_masks(const int*, const float*, const uint32_t*, int, int, int, int, int*, int*,
+                           int4*, int*, int4*, int*, float*, int*, const float*, float*, int,
+                           hipStream_t);
 bool launch_gemm1(int, const uint8_t*, const TokenScales&, int, const uint8_t*, const float*,
                   const int4*, const int*, const int*, int, const int*, const Intermediate&,
                   bool, hipStream_t);
@@ -176,23 +180,35 @@ int forward_impl(const moe_mi355_args& a, void* workspace, size_t ws_bytes, hipS
     // beyond the fp16 range with the call's tag instead of 1 (no route kernel clears the
     // flag word before it)
     const int wide_tag = plan.route_in_gemm1 ? next_wide_tag() : 1;
+    const int offset = clamp_offset(a.local_expert_offset);
+    // the dispatch in one launch from the route kernel's local-expert masks (with the
+    // token-scale gather when GEMM1 reads the scales in row order)
+    const bool by_masks =
+        !plan.dispatch_in_gemm1 && T >= moe::kMaskDispatchMinT && T <= moe::kMaskDispatchMaxT;
+    uint32_t* masks = by_masks ? reinterpret_cast<uint32_t*>(ws + L.token_masks) : nullptr;
     stage(0);
     if (!plan.route_in_gemm1)
         moe::launch_route(a.routing_logits, a.routing_bias, T, (float)a.routed_scaling_factor, ids,
-                          wts, meta + moe::kCWideFlag, s);
+                          wts, meta + moe::kCWideFlag, masks, offset, s);
     stage(1);
     const int max_tiles = moe::dispatch_max_tiles(T, plan.tm);
     const bool half = plan.tm2 > 0;   // GEMM2 walks the second (128-row) tile list
     int4* tiles2 = tiles + max_tiles;
     int* num_tiles2 = meta + moe::kEL + 2;
     // GEMM1 variant 5 computes the dispatch itself (timed as the GEMM1 stage)
-    bool ok = plan.dispatch_in_gemm1 ||
-              moe::launch_dispatch(ids, wts, T, clamp_offset(a.local_expert_offset), plan.tm,
-                                   plan.tm2, meta, num_tiles, tiles, stok, sw, inv, chunk_cnt, s,
-                                   half ? num_tiles2 : nullptr, half ? tiles2 : nullptr);
+    bool ok = true;
+    if (by_masks)
+        ok = moe::launch_dispatch_masks(ids, wts, masks, T, offset, plan.tm, plan.tm2, meta, num_tiles,
+                                        tiles, half ? num_tiles2 : nullptr, half ? tiles2 : nullptr,
+                                        stok, sw, inv, plan.by_row ? a.hidden_states_scale : nullptr,
+                                        plan.by_row ? row_scales : nullptr, T * moe::kTopK, s);
+    else if (!plan.dispatch_in_gemm1)
+        ok = moe::launch_dispatch(ids, wts, T, offset, plan.tm, plan.tm2, meta, num_tiles, tiles, stok,
+                                  sw, inv, chunk_cnt, s, half ? num_tiles2 : nullptr,
+                                  half ? tiles2 : nullptr);
     // GEMM1 reads the token scales gathered into row order (counted in the dispatch stage)
     // or, where the gather would cost more than it saves, straight by token
-    if (ok && plan.by_row)
+    if (ok && plan.by_row && !by_masks)
         moe::launch_gather_row_scales(a.hidden_states_scale, T, stok, meta, row_scales,
                                       T * moe::kTopK, s);
     const moe::TokenScales sa = plan.by_row ? moe::TokenScales{row_scales, T * moe::kTopK, 1}
@@ -201,7 +217,7 @@ int forward_impl(const moe_mi355_args& a, void* workspace, size_t ws_bytes, hipS
     if (plan.dispatch_in_gemm1) {
         const moe::RouteIn rin{plan.route_in_gemm1 ? a.routing_logits : nullptr, a.routing_bias,
                                (float)a.routed_scaling_factor};
-        ok = ok && moe::launch_gemm1_dispatch(rin, ids, wts, T, clamp_offset(a.local_expert_offset),
+        ok = ok && moe::launch_gemm1_dispatch(rin, ids, wts, T, offset,
                                               a.hidden_states, a.hidden_states_scale,
                                               a.gemm1_weights, a.gemm1_weights_scale, meta, tiles,
                                               stok, sw, inv, inter, wide_tag, s);
@@ -286,7 +302,7 @@ int moe_mi355_route(const float* routing_logits, const uint16_t* routing_bias, i
     if (!aligned16(routing_logits) || ((uintptr_t)routing_bias & 7u)) return MOE_ERR_MISALIGNED;
     hipStream_t s = (hipStream_t)stream;
     moe::launch_route(routing_logits, routing_bias, T, (float)routed_scaling_factor, topk_ids,
-                      topk_weights, nullptr, s);
+                      topk_weights, nullptr, nullptr, 0, s);
     return hip_status(hipGetLastError());
 }
 

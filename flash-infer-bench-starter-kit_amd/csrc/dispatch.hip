@@ -165,6 +165,264 @@ __global__ __launch_bounds__(kChunk) void dispatch_place_kernel(
     place(r, rank, chunk * kChunk + tid, T, wbase[wave], sorted_tok, sorted_w, inv);
 }
 
+// ---------------------------------------------------------------------------
+// The forward's dispatch in one launch (kMaskDispatchMinT <= T <= kMaskDispatchMaxT),
+// from the route kernel's per-token local-expert masks (bit e: local expert e).  One
+// workgroup per 256-token chunk, as in the place kernel, but each workgroup counts every
+// expert over all T tokens itself, so no count launch runs before it: in each row of 16
+// lanes, 16 masks are transposed as two 16 x 16 bit matrices (lane i of the row then
+// holds bit i and bit 16 + i of the row's 16 masks), and two popcounts give the counts
+// of experts i and 16 + i over them.  The totals give the expert offsets (and, in chunk
+// 0, the tile lists), the counts of the chunks before this one its base in each expert;
+// the ranks inside the chunk and the placement are the place kernel's.  With row_scales
+// set, the workgroups also write the token scales of the rows in row order (the gather
+// launch's work), spread over gridDim.y workgroups per chunk: each computes the chunk's
+// dispatch (only the first, y = 0, stores it) and writes the scales of its share of the
+// 56 K blocks; its chunk's token scales of those K blocks come into LDS by DMA at kernel
+// start, and its rows are written one contiguous run per expert.
+
+// Stage s of the transpose (s = 1, 2, 4, 8): lanes l and l ^ s swap the off-diagonal
+// s x s blocks of their 2s x 2s block.  The lower lane keeps its bits at positions with
+// bit s clear (keep = M_s) and takes the partner's there, moved up by s (rot = 32 - s, a
+// rotation right); the upper lane keeps the positions with bit s set (keep = ~M_s) and
+// takes the partner's moved down by s (rot = s).  The bits a rotation wraps around land
+// where keep selects the lane's own bits, and no bit crosses between the two 16-bit halves.
+__device__ __forceinline__ uint32_t transpose_stage(uint32_t x, uint32_t partner, uint32_t rot,
+                                                    uint32_t keep) {
+    const uint32_t q = __builtin_amdgcn_alignbit(partner, partner, rot);
+    return (x & keep) | (q & ~keep);
+}
+
+static_assert(kMaskDispatchMaxT <= 64 * kChunk, "the count reads at most 64 chunks");
+static_assert(kChunk <= 256, "a token's index in its chunk is kept in one byte");
+
+// NB: chunks the count reads (a power of two >= ceil(T / 256)); masks past T read 0.
+// GATHER: row_scales is written (a template parameter, so that the wait for the first
+// mask counts the token-scale DMA issued after it exactly and does not wait for it).
+template <int NB, bool GATHER>
+__global__ __launch_bounds__(kChunk) void dispatch_masks_kernel(
+    const int* __restrict__ topk_ids, const float* __restrict__ topk_w,
+    const uint32_t* __restrict__ masks, int T, int offset, int tm, int tm2,
+    int* __restrict__ exp_off, int* __restrict__ num_tiles, int4* __restrict__ tiles,
+    int* __restrict__ num_tiles2, int4* __restrict__ tiles2, int* __restrict__ sorted_tok,
+    float* __restrict__ sorted_w, int* __restrict__ inv, const float* __restrict__ hs_scale,
+    float* __restrict__ row_scales, int rows_cap) {
+    __shared__ int wcnt[kChunkWaves][kEL];
+    __shared__ int wbase[kChunkWaves][kEL];
+    __shared__ int off[kEL];
+    __shared__ int cbase[kEL];
+    __shared__ int cpre[kEL + 1];                  // the chunk's rows before expert e
+    __shared__ int part[2][kChunkWaves][kEL];
+    __shared__ uint64_t bal[kChunkWaves][kEL];
+    __shared__ float s_hs[kHB][kChunk];            // the chunk's token scales [kb][token]
+    __shared__ int s_row[kChunk * kTopK];          // the chunk's rows, expert-major
+    __shared__ uint8_t s_tok[kChunk * kTopK];      // their tokens (index in the chunk)
+    load_args_into_sgprs(topk_ids, topk_w, masks, T, offset, tm, tm2, exp_off, num_tiles, tiles,
+                         num_tiles2, tiles2, sorted_tok, sorted_w, inv, hs_scale, row_scales, rows_cap);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int chunk = blockIdx.x;
+    const int t = chunk * kChunk + tid;
+    const bool lead = blockIdx.y == 0;                       // stores the dispatch
+    const int kpb = (kHB + (int)gridDim.y - 1) / (int)gridDim.y;
+    const int kb0 = (int)blockIdx.y * kpb, kb1 = min(kHB, kb0 + kpb);   // its token-scale K blocks
+
+    // every load first, in the order they are needed: this chunk's routes, the masks of
+    // every chunk (token b * 256 + tid), then the chunk's token scales straight into LDS
+    // (reads past T return 0 and are not used)
+    v4u rid[2], rw[2];
+    {
+        const __amdgpu_buffer_rsrc_t rs_i = buffer_rsrc(topk_ids, (uint32_t)T * kTopK * 4);
+        const __amdgpu_buffer_rsrc_t rs_w = buffer_rsrc(topk_w, (uint32_t)T * kTopK * 4);
+        const uint32_t o = (uint32_t)t * kTopK * 4;
+        rid[0] = __builtin_amdgcn_raw_buffer_load_b128(rs_i, o, 0, 0);
+        rid[1] = __builtin_amdgcn_raw_buffer_load_b128(rs_i, o + 16, 0, 0);
+        rw[0] = __builtin_amdgcn_raw_buffer_load_b128(rs_w, o, 0, 0);
+        rw[1] = __builtin_amdgcn_raw_buffer_load_b128(rs_w, o + 16, 0, 0);
+    }
+    // wave w counts chunks w, w + 4, ...: one 16-byte load gives each lane 4 consecutive
+    // tokens' masks of a chunk, 4 blocks of 64 tokens per load (the route kernel writes 0
+    // for the tokens from T up to 4 ceil(T / 4); loads past them read 0)
+    constexpr int NL = NB / kChunkWaves;
+    v4u mk[NL];
+    {
+        const __amdgpu_buffer_rsrc_t rs_m = buffer_rsrc(masks, (uint32_t)((T + 3) & ~3) * 4);
+#pragma unroll
+        for (int i = 0; i < NL; ++i)
+            mk[i] = __builtin_amdgcn_raw_buffer_load_b128(
+                rs_m, (uint32_t)((kChunkWaves * i + wave) * kChunk + 4 * lane) * 4, 0, 0);
+    }
+    if constexpr (GATHER) {
+        const __amdgpu_buffer_rsrc_t rs_s = buffer_rsrc(hs_scale, (uint32_t)T * kHB * 4);
+        for (int kb = kb0; kb < kb1; ++kb) bdma4(rs_s, (uint32_t)t * 4, (uint32_t)kb * T * 4, &s_hs[kb][64 * wave]);
+    }
+    TokenRoutes r;
+    {
+        const int ids[kTopK] = {(int)rid[0][0], (int)rid[0][1], (int)rid[0][2], (int)rid[0][3],
+                                (int)rid[1][0], (int)rid[1][1], (int)rid[1][2], (int)rid[1][3]};
+        // each element into a scalar first: hipcc's __builtin_bit_cast of a vector element
+        // taken with a subscript read element 0 whatever the index
+        float ws[kTopK];
+#pragma unroll
+        for (int k = 0; k < kTopK; ++k) {
+            const uint32_t u = rw[k >> 2][k & 3];
+            ws[k] = __builtin_bit_cast(float, u);
+        }
+        r = decode_routes(ids, ws, t, T, offset);
+    }
+
+    // expert counts over this wave's chunks (tot) and over those of them before this
+    // workgroup's chunk (bef): lane l holds experts l % 16 (lo) and 16 + l % 16 (hi) over
+    // the tokens of its row of 16 lanes; the rows, then the four waves, are added after
+    uint32_t rot[4], keep[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        constexpr uint32_t kM[4] = {0x55555555u, 0x33333333u, 0x0f0f0f0fu, 0x00ff00ffu};
+        const uint32_t sft = 1u << i;
+        const bool lower = (lane & sft) == 0;
+        rot[i] = lower ? 32u - sft : sft;
+        keep[i] = lower ? kM[i] : ~kM[i];
+    }
+    uint32_t tot_lo = 0, tot_hi = 0, bef_lo = 0, bef_hi = 0;
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+        // the load's 4 blocks stage by stage, so that their chains interleave
+        uint32_t x[4] = {mk[i][0], mk[i][1], mk[i][2], mk[i][3]};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x[j] = transpose_stage(x[j], xor1(x[j]), rot[0], keep[0]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x[j] = transpose_stage(x[j], xor2(x[j]), rot[1], keep[1]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x[j] = transpose_stage(x[j], xor4(x[j]), rot[2], keep[2]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x[j] = transpose_stage(x[j], xor8(x[j]), rot[3], keep[3]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            // opaque to the optimiser: it would otherwise push the half-word masks below
+            // back through every stage, computing each stage's select three times over
+            __asm__("" : "+v"(x[j]));
+            tot_lo += (uint32_t)__builtin_popcount(x[j] & 0xffffu);
+            tot_hi += (uint32_t)__builtin_popcount(x[j] >> 16);
+        }
+        if (kChunkWaves * i + wave < chunk) {   // uniform: this load's chunk is before ours
+            bef_lo = tot_lo;
+            bef_hi = tot_hi;
+        }
+    }
+    // add the four rows (lanes l, l ^ 16, l ^ 32, l ^ 48): lane i < 16 then holds experts
+    // i and 16 + i over all of the wave's tokens
+    tot_lo += xor16(tot_lo, lane);
+    tot_hi += xor16(tot_hi, lane);
+    bef_lo += xor16(bef_lo, lane);
+    bef_hi += xor16(bef_hi, lane);
+    tot_lo += xor32(tot_lo, lane);
+    tot_hi += xor32(tot_hi, lane);
+    bef_lo += xor32(bef_lo, lane);
+    bef_hi += xor32(bef_hi, lane);
+    if (lane < 16) {
+        part[0][wave][lane] = (int)tot_lo;
+        part[0][wave][16 + lane] = (int)tot_hi;
+        part[1][wave][lane] = (int)bef_lo;
+        part[1][wave][16 + lane] = (int)bef_hi;
+    }
+
+    // LDS-only barriers below: __syncthreads would also wait for the token-scale DMA
+    // and for chunk 0's tile-list stores
+    int rank[kTopK];
+    wave_ranks(r, wave, lane, wcnt, bal[wave], rank);
+    lds_barrier();
+    // this wave's token-scale DMA (issued before the count, landed by now): waited for
+    // here, before any store, so that the wait covers nothing else
+    if constexpr (GATHER) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    if (wave == 0) {
+        int total = 0, before = 0, cc = 0;
+        if (lane < kEL) {
+            for (int w = 0; w < kChunkWaves; ++w) {
+                total += part[0][w][lane];
+                before += part[1][w][lane];
+                cc += wcnt[w][lane];
+            }
+        }
+        if (chunk == 0 && lead) {
+            write_offsets_and_tiles_rt(lane < kEL ? total : 0, lane, off, exp_off, num_tiles, tiles, tm,
+                                       num_tiles2, tiles2, tm2);
+        } else {
+            const int ci = scan32(lane < kEL ? total : 0, lane);
+            if (lane < kEL) off[lane] = ci - total;
+        }
+        const int cp = scan32(lane < kEL ? cc : 0, lane);
+        if (lane < kEL) {
+            cbase[lane] = before;
+            cpre[lane] = cp - cc;
+        }
+        if (lane == kEL - 1) cpre[kEL] = cp;
+    }
+    lds_barrier();
+    if (tid < kEL) {
+        int run = off[tid] + cbase[tid];
+        for (int w = 0; w < kChunkWaves; ++w) {
+            wbase[w][tid] = run;
+            run += wcnt[w][tid];
+        }
+    }
+    lds_barrier();
+    if (lead) place(r, rank, t, T, wbase[wave], sorted_tok, sorted_w, inv);
+    if constexpr (!GATHER) return;
+
+    // the chunk's rows of expert e are wbase[0][e] .. + count - 1, entries cpre[e] .. of
+    // the expert-major list; then every row's scale of each K block
+    if (t < T) {
+#pragma unroll
+        for (int k = 0; k < kTopK; ++k) {
+            const int e = r.lek[k];
+            if (e >= 0) {
+                const int row = wbase[wave][e] + rank[k];
+                const int q = cpre[e] + (row - wbase[0][e]);
+                s_row[q] = row;
+                s_tok[q] = (uint8_t)tid;
+            }
+        }
+    }
+    lds_barrier();   // s_row / s_tok, and every wave's token scales (waited for above)
+    const int nq = cpre[kEL];
+    for (int q = tid; q < nq; q += kChunk) {
+        const int row = s_row[q], tk = s_tok[q];
+#pragma unroll 8
+        for (int kb = kb0; kb < kb1; ++kb) row_scales[(size_t)kb * rows_cap + row] = s_hs[kb][tk];
+    }
+}
+
+// The forward's dispatch from the token masks; hs_scale / row_scales (both or neither)
+// add the gather of the token scales into row order (rows_cap: row_scales' row stride).
+bool launch_dispatch_masks(const int* topk_ids, const float* topk_w, const uint32_t* masks, int T,
+                           int offset, int tm, int tm2, int* exp_off, int* num_tiles, int4* tiles,
+                           int* num_tiles2, int4* tiles2, int* sorted_tok, float* sorted_w,
+                           int* inv, const float* hs_scale, float* row_scales, int rows_cap,
+                           hipStream_t stream) {
+    if (T < 1 || T > kMaskDispatchMaxT || masks == nullptr) return false;
+    if (tm != 16 && tm != 32 && tm != 64 && tm != 128 && tm != 256) return false;
+    if (tm2 != 0 && (tm2 != 128 || !tiles2 || !num_tiles2)) return false;
+    if ((hs_scale == nullptr) != (row_scales == nullptr)) return false;
+    const int nchunks = (T + kChunk - 1) / kChunk;
+    // with the gather, about 256 workgroups: up to 8 per chunk, each writing the token
+    // scales of 56 / 8 .. 56 K blocks (the stores are what takes the time there)
+    const int slices = row_scales ? min(8, max(1, 256 / nchunks)) : 1;
+    auto run = [&](auto nb, auto gather) {
+        launch_kernel((dispatch_masks_kernel<decltype(nb)::value, decltype(gather)::value>),
+                      dim3(nchunks, slices), dim3(kChunk), 0, stream, topk_ids, topk_w, masks, T, offset, tm,
+                      tm2, exp_off, num_tiles, tiles, num_tiles2, tiles2, sorted_tok, sorted_w, inv,
+                      hs_scale, row_scales, rows_cap);
+    };
+    auto by_nb = [&](auto gather) {
+        if (nchunks <= 8) run(IntC<8>{}, gather);
+        else if (nchunks <= 16) run(IntC<16>{}, gather);
+        else if (nchunks <= 32) run(IntC<32>{}, gather);
+        else run(IntC<64>{}, gather);
+    };
+    if (row_scales) by_nb(BoolC<true>{});
+    else by_nb(BoolC<false>{});
+    return true;
+}
+
 // Token scales in row order for GEMM1 (reference kernel.cu:204-230, prepare_sfa_kernel,
 // builds the same table over its padded rows): row_scales[kb][row] =
 // hs_scale[kb][sorted_tok[row]] for the exp_off[32] rows of the permutation.  A GEMM1

@@ -29,6 +29,22 @@ struct TokenRoutes {
     uint32_t mask;
 };
 
+// A token's routes from its 8 ids and weights (t >= T: no route).
+__device__ __forceinline__ TokenRoutes decode_routes(const int* ids, const float* ws, int t, int T,
+                                                     int offset) {
+    TokenRoutes r;
+    r.mask = 0;
+#pragma unroll
+    for (int k = 0; k < kTopK; ++k) {
+        const int le = ids[k] - offset;
+        const bool loc = t < T && (unsigned)le < (unsigned)kEL;
+        r.lek[k] = loc ? le : -1;
+        r.wk[k] = t < T ? ws[k] : 0.f;
+        if (loc) r.mask |= 1u << le;
+    }
+    return r;
+}
+
 __device__ __forceinline__ TokenRoutes load_routes(const int* __restrict__ topk_ids,
                                                    const float* __restrict__ topk_w, int t, int T,
                                                    int offset) {
@@ -41,14 +57,7 @@ __device__ __forceinline__ TokenRoutes load_routes(const int* __restrict__ topk_
         const float4 w0 = wp[0], w1 = wp[1];
         const int ids[kTopK] = {i0.x, i0.y, i0.z, i0.w, i1.x, i1.y, i1.z, i1.w};
         const float ws[kTopK] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-#pragma unroll
-        for (int k = 0; k < kTopK; ++k) {
-            const int le = ids[k] - offset;
-            const bool loc = (unsigned)le < (unsigned)kEL;
-            r.lek[k] = loc ? le : -1;
-            r.wk[k] = ws[k];
-            if (loc) r.mask |= 1u << le;
-        }
+        r = decode_routes(ids, ws, t, T, offset);
     } else {
 #pragma unroll
         for (int k = 0; k < kTopK; ++k) { r.lek[k] = -1; r.wk[k] = 0.f; }
@@ -121,18 +130,17 @@ __device__ __forceinline__ void place(const TokenRoutes& r, const int* rank, int
 }
 
 // expert offsets, tile list and tile count from the per-expert totals (wave 0).
-// With TM2 > 0 (and tiles2 set), also a second list of tiles of TM2 rows over the same
+// With tm2 > 0 (and tiles2 set), also a second list of tiles of tm2 rows over the same
 // rows (num_tiles2 = its count), for a GEMM2 that walks other tiles than the GEMM1.
-template <int TM, int TM2>
-__device__ __forceinline__ void write_offsets_and_tiles(int c, int lane, int* off_lds,
-                                                        int* __restrict__ exp_off,
-                                                        int* __restrict__ num_tiles,
-                                                        int4* __restrict__ tiles,
-                                                        int* __restrict__ num_tiles2,
-                                                        int4* __restrict__ tiles2) {
-    constexpr int TM2r = TM2 > 0 ? TM2 : TM;
-    const int nt = (c + TM - 1) / TM;
-    const int nt2 = (c + TM2r - 1) / TM2r;
+__device__ __forceinline__ void write_offsets_and_tiles_rt(int c, int lane, int* off_lds,
+                                                           int* __restrict__ exp_off,
+                                                           int* __restrict__ num_tiles,
+                                                           int4* __restrict__ tiles, int tm,
+                                                           int* __restrict__ num_tiles2,
+                                                           int4* __restrict__ tiles2, int tm2) {
+    const int tm2r = tm2 > 0 ? tm2 : tm;
+    const int nt = (c + tm - 1) / tm;
+    const int nt2 = (c + tm2r - 1) / tm2r;
     const int ci = scan32(c, lane);
     const int ti = scan32(nt, lane);
     const int ti2 = scan32(nt2, lane);
@@ -140,18 +148,30 @@ __device__ __forceinline__ void write_offsets_and_tiles(int c, int lane, int* of
         const int o = ci - c, to = ti - nt;
         off_lds[lane] = o;
         exp_off[lane] = o;
-        for (int j = 0; j < nt; ++j) tiles[to + j] = make_int4(lane, o + j * TM, min(TM, c - j * TM), 0);
-        if (TM2 > 0 && tiles2) {
+        for (int j = 0; j < nt; ++j) tiles[to + j] = make_int4(lane, o + j * tm, min(tm, c - j * tm), 0);
+        if (tm2 > 0 && tiles2) {
             const int to2 = ti2 - nt2;
             for (int j = 0; j < nt2; ++j)
-                tiles2[to2 + j] = make_int4(lane, o + j * TM2r, min(TM2r, c - j * TM2r), 0);
+                tiles2[to2 + j] = make_int4(lane, o + j * tm2r, min(tm2r, c - j * tm2r), 0);
         }
     }
     if (lane == kEL - 1) {
         exp_off[kEL] = ci;
         *num_tiles = ti;
-        if (TM2 > 0 && tiles2) *num_tiles2 = ti2;
+        if (tm2 > 0 && tiles2) *num_tiles2 = ti2;
     }
+}
+
+// The same with the tile heights known at compile time.
+template <int TM, int TM2>
+__device__ __forceinline__ void write_offsets_and_tiles(int c, int lane, int* off_lds,
+                                                        int* __restrict__ exp_off,
+                                                        int* __restrict__ num_tiles,
+                                                        int4* __restrict__ tiles,
+                                                        int* __restrict__ num_tiles2,
+                                                        int4* __restrict__ tiles2) {
+    write_offsets_and_tiles_rt(c, lane, off_lds, exp_off, num_tiles, tiles, TM, num_tiles2, tiles2,
+                               TM2);
 }
 
 // Per-wave LDS of dispatch_wave.

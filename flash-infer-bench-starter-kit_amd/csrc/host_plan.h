@@ -166,6 +166,7 @@ constexpr moe_mi355_workspace_layout workspace_regions(int32_t T) {
     L.sorted_tokens = take(R * 4);
     L.sorted_weights = take(R * 4);
     L.chunk_counts = take((size_t)((T + 255) / 256) * kEL * 4);
+    L.token_masks = take((size_t)T * 4);
     L.row_scales = take(R * kHB * 4);        // token scales in row order, [56, 8T]
     // hi/lo, fp16 and the fp16 form's group exponents
     L.intermediate = take(R * (kI * 4 + kI / kGroup16));

@@ -331,11 +331,29 @@ __device__ __forceinline__ void lds_barrier() {
     __asm__ volatile("" ::: "memory");
 }
 
+// Loads kernel arguments into SGPRs at the point of the call: an empty asm statement that
+// takes each one as an SGPR operand, so the compiler loads them from the kernel-argument
+// segment there instead of deferring each load to its first use, where a wave would wait
+// a memory round trip for it mid-kernel.  The values are not modified, so a pointer keeps
+// its inferred address space (global stores, not flat ones).
+template <class A>
+__device__ __forceinline__ void load_arg_into_sgprs(const A& a) {
+    __asm__ volatile("" ::"s"(a));
+}
+template <class... A>
+__device__ __forceinline__ void load_args_into_sgprs(const A&... a) {
+    (load_arg_into_sgprs(a), ...);
+}
+
 // Compile-time int for generic lambdas (kernels specialise their K loop on the number
 // of 16-row blocks of a tile a wave actually has to compute).
 template <int N>
 struct IntC {
     static constexpr int value = N;
+};
+template <bool B>
+struct BoolC {
+    static constexpr bool value = B;
 };
 
 // Calls f(IntC<n>{}) for n in 0..4.
@@ -482,6 +500,40 @@ struct Intermediate {
 __device__ __forceinline__ float f16_scaled_to_f32(uint32_t h, int e) {
     const float v = (float)__builtin_bit_cast(_Float16, (uint16_t)h);
     return e ? ldexpf(v, e) : v;
+}
+
+// ---- lane exchanges (DPP and the lane-swap instructions) ----------------------
+
+// value of lane i^1, i^2 (quad permutes) and i^4 (swap of the two quads of an octet).
+// Where every lane has a source lane (quad permutes, row rotations) the DPP moves are
+// written with old = 0 and bound_ctrl set, which lets the compiler fold each into the
+// max or min that consumes it (v_max_u32_dpp): the same values, one instruction fewer.
+__device__ __forceinline__ uint32_t xor1(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xb1, 0xf, 0xf, true);  // quad_perm [1,0,3,2]
+}
+__device__ __forceinline__ uint32_t xor2(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4e, 0xf, 0xf, true);  // quad_perm [2,3,0,1]
+}
+__device__ __forceinline__ uint32_t xor4(uint32_t v) {
+    // banks 0,2 (lanes 0-3, 8-11 of a row) read lane+4; banks 1,3 read lane-4
+    const int a = __builtin_amdgcn_update_dpp((int)v, (int)v, 0x104, 0xf, 0x5, false);  // row_shl:4
+    return (uint32_t)__builtin_amdgcn_update_dpp(a, (int)v, 0x114, 0xf, 0xa, false);     // row_shr:4
+}
+
+// value of lane i^8 (rotation by 8 inside each row of 16 lanes)
+__device__ __forceinline__ uint32_t xor8(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xf, 0xf, true);  // row_ror:8
+}
+// value of lane i^16 and i^32: v_permlane16_swap / v_permlane32_swap of v with itself
+// leave the value of the partner row (half) in the second result for even rows (the
+// lower half) and in the first for odd rows (the upper half)
+__device__ __forceinline__ uint32_t xor16(uint32_t v, int lane) {
+    const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return ((lane >> 4) & 1) ? p[0] : p[1];
+}
+__device__ __forceinline__ uint32_t xor32(uint32_t v, int lane) {
+    const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (lane >> 5) ? p[0] : p[1];
 }
 
 }  // namespace moe

@@ -42,6 +42,14 @@ constexpr int kDispatchInGemm1MaxT = 64;
 // weight load by more than the route launch costs.
 constexpr int kRouteInGemm1MaxT = 4;
 
+// Token counts whose forward dispatch is one launch over the local-expert masks the route
+// kernel writes (dispatch_masks_kernel): every workgroup counts the experts of all T tokens
+// from the masks, which replaces the count launch (and, where GEMM1 reads the token scales
+// in row order, the gather launch).  Up to kMaskDispatchMaxT a workgroup's count reads at
+// most 64 masks per thread; beyond, the count and place launches run.
+constexpr int kMaskDispatchMinT = 641;
+constexpr int kMaskDispatchMaxT = 16384;
+
 // Largest T whose GEMM2 runs with the combine folded in (GEMM2 variant 6): the kernel
 // keeps every expert row of the call (8 T rows) for its 32 output columns in LDS.
 constexpr int kFusedCombineMaxT = 32;

@@ -61,7 +61,7 @@ class WorkspaceLayout(ctypes.Structure):
     """``moe_mi355_workspace_layout`` of include/moe_mi355.h."""
     _fields_ = [(n, ctypes.c_size_t) for n in (
         "topk_ids", "topk_weights", "inverse_rows", "meta", "tiles", "sorted_tokens",
-        "sorted_weights", "chunk_counts", "row_scales", "intermediate", "intermediate_scales", "expert_out", "expert_out_exp",
+        "sorted_weights", "chunk_counts", "token_masks", "row_scales", "intermediate", "intermediate_scales", "expert_out", "expert_out_exp",
         "total")] + [
         ("tile_m", ctypes.c_int32), ("max_tiles", ctypes.c_int32),
         ("intermediate_format", ctypes.c_int32), ("dispatch_in_gemm1", ctypes.c_int32),

@@ -31,11 +31,12 @@ static const int32_t kTs[] = {INT32_MIN, -1, 0, 1, 2, 4, 5, 8, 16, 32, 33, 63, 6
 static void check_layout(int32_t T, const moe_mi355_workspace_layout& L) {
     const size_t R = (size_t)T * 8;
     const size_t off[] = {L.topk_ids, L.topk_weights, L.inverse_rows, L.meta, L.tiles,
-                          L.sorted_tokens, L.sorted_weights, L.chunk_counts, L.row_scales,
-                          L.intermediate, L.intermediate_scales, L.expert_out, L.expert_out_exp,
-                          L.total};
+                          L.sorted_tokens, L.sorted_weights, L.chunk_counts, L.token_masks,
+                          L.row_scales, L.intermediate, L.intermediate_scales, L.expert_out,
+                          L.expert_out_exp, L.total};
     const size_t need[] = {R * 4, R * 4, R * 4, 256, (size_t)L.max_tiles * 32, R * 4, R * 4,
-                           (size_t)((T + 255) / 256) * 128, R * 56 * 4, R * (2048 * 4 + 128),
+                           (size_t)((T + 255) / 256) * 128, (size_t)T * 4, R * 56 * 4,
+                           R * (2048 * 4 + 128),
                            R * 16 * 4, R * 7168 * 2, R * 448};
     for (size_t i = 0; i + 1 < sizeof off / sizeof off[0]; ++i) {
         CHECK(off[i] % 256 == 0);

@@ -51,9 +51,10 @@ def test_workspace_bytes(lib):
     lay = k.workspace_layout(64)
     assert lay.total == sizes[3]
     offs = [lay.topk_ids, lay.topk_weights, lay.inverse_rows, lay.meta, lay.tiles,
-            lay.sorted_tokens, lay.sorted_weights, lay.chunk_counts, lay.row_scales, lay.intermediate,
-            lay.expert_out, lay.expert_out_exp]
+            lay.sorted_tokens, lay.sorted_weights, lay.chunk_counts, lay.token_masks, lay.row_scales,
+            lay.intermediate, lay.expert_out, lay.expert_out_exp]
     assert offs == sorted(offs) and all(o % 256 == 0 for o in offs)
+    assert lay.token_masks + 64 * 4 <= lay.row_scales                        # [T] uint32
     assert lay.row_scales + 56 * 64 * 8 * 4 <= lay.intermediate               # [56, 8T] fp32
     assert lay.intermediate + 64 * 8 * (2048 * 4 + 128) <= lay.intermediate_scales  # hi/lo, fp16, exps
     assert lay.expert_out + 64 * 8 * 7168 * 2 <= lay.expert_out_exp          # fp16 expert rows
