@@ -46,8 +46,10 @@ constexpr int kRouteInGemm1MaxT = 4;
 // kernel writes (dispatch_masks_kernel): every workgroup counts the experts of all T tokens
 // from the masks, which replaces the count launch (and, where GEMM1 reads the token scales
 // in row order, the gather launch).  Up to kMaskDispatchMaxT a workgroup's count reads at
-// most 64 masks per thread; beyond, the count and place launches run.
-constexpr int kMaskDispatchMinT = 641;
+// most 64 masks per thread; beyond, the count and place launches run.  Below
+// kMaskDispatchMinT the one-workgroup dispatch is as fast or faster (measured: T = 300
+// +0.4 us, 350 even, 400 -0.5, 600 -1.3 us for the masks).
+constexpr int kMaskDispatchMinT = 400;
 constexpr int kMaskDispatchMaxT = 16384;
 
 // Largest T whose GEMM2 runs with the combine folded in (GEMM2 variant 6): the kernel

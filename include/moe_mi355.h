@@ -249,7 +249,7 @@ typedef struct moe_mi355_workspace_layout {
     size_t chunk_counts;    /* int32 [ceil(T/256), 32] dispatch scratch */
     size_t token_masks;     /* uint32 [T]: each token's local experts (bit e: local expert
                                e), written by the route kernel where the dispatch counts
-                               from them (641 <= T <= 16384) */
+                               from them (400 <= T <= 16384) */
     size_t row_scales;      /* fp32  [56, 8T]: hidden_states_scale gathered into row order,
                                [kb][row] = scale[kb][sorted_tokens[row]] (the rows
                                in use, for the token counts where GEMM1 reads them) */

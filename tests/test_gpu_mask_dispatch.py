@@ -1,4 +1,4 @@
-"""The forward's one-launch dispatch for 641 <= T <= 16384: the route kernel also writes
+"""The forward's one-launch dispatch for 400 <= T <= 16384: the route kernel also writes
 each token's local-expert mask, and every workgroup of the dispatch counts all T tokens'
 experts from the masks (a bit transpose per wave and a popcount), then places its own
 256-token chunk; where GEMM1 reads the token scales in row order it also writes them.
@@ -43,7 +43,7 @@ def _inputs(src, T, offset):
 
 
 @pytest.mark.parametrize("src,T,offset,flags", [
-    (3, 641, 0, 0), (3, 1000, 96, 0), (2, 1024, 64, "rows_on"), (3, 1344, 224, 0),
+    (3, 399, 0, 0), (3, 400, 0, 0), (3, 641, 0, 0), (3, 1000, 96, 0), (2, 1024, 64, "rows_on"), (3, 1344, 224, 0),
     (3, 1345, 0, 0), (3, 2049, 32, 0), (4, 4096, 0, 0), (3, 4097, 160, 0), (3, 8192, 0, 0),
     ("big", 16384, 0, 0), ("big", 16384, 224, 0), ("big", 16385, 0, 0)])
 def test_workspace_dispatch_is_bit_exact(src, T, offset, flags):
@@ -67,7 +67,7 @@ def test_workspace_dispatch_is_bit_exact(src, T, offset, flags):
     le = rids.astype(np.int64) - offset
     loc = (le >= 0) & (le < 32)
     masks = np.bitwise_or.reduce(np.where(loc, np.left_shift(1, np.where(loc, le, 0)), 0), axis=1)
-    if T <= 16384:
+    if 400 <= T <= 16384:
         assert np.array_equal(arr(lay.token_masks, T, torch.int32).view(np.uint32),
                               masks.astype(np.uint32))
     r = o.dispatch(rids, rw, offset, lay.tile_m)
@@ -100,7 +100,7 @@ def test_one_workspace_across_sizes():
     wl = pkg("workloads")
     o = oracle()
     ws = torch.empty(k.workspace_layout(8192).total, dtype=torch.uint8, device="cuda")
-    for T in (8192, 700, 3000, 641):
+    for T in (8192, 700, 3000, 400):
         d = _inputs(3, T, 0)
         lay = k.workspace_layout(T)
         note(f"[gpu] mask dispatch on a shared workspace T={T}")
