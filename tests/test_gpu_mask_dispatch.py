@@ -114,3 +114,60 @@ def test_one_workspace_across_sizes():
         assert np.array_equal(got, r["sorted_tok"])
         inv = ws[lay.inverse_rows:lay.inverse_rows + T * 32].view(torch.int32).cpu().numpy()
         assert np.array_equal(inv.reshape(T, 8), r["inv"])
+
+
+@pytest.mark.parametrize("T", [500, 3000])
+def test_no_local_expert(T):
+    """An offset that selects no expert: every mask is 0, the counts and tile lists are
+    empty, and the output is exactly zero."""
+    k = pkg("kernel")
+    wl = pkg("workloads")
+    d = _inputs(3, T, 1000)
+    lay = k.workspace_layout(T)
+    ws = torch.empty(lay.total, dtype=torch.uint8, device="cuda")
+    out = torch.full_like(d["output"], float("nan"))
+    note(f"[gpu] mask dispatch, no local expert, T={T}")
+    k.forward(*wl.as_args({**d, "output": out}), workspace=ws)
+    torch.cuda.synchronize()
+    assert (out.view(torch.int16) == 0).all()
+    masks = ws[lay.token_masks:lay.token_masks + T * 4].view(torch.int32)
+    assert (masks == 0).all()
+    meta = ws[lay.meta:lay.meta + 35 * 4].view(torch.int32).cpu().numpy()
+    assert (meta[:34] == 0).all()          # offsets, tile count
+    if lay.intermediate_format != 0:       # the plans with a second tile list
+        assert meta[34] == 0
+
+
+def test_all_local_workspace_is_bit_exact():
+    """Every token routed to 8 local experts (T = 1500: 1500 rows per expert, six full
+    256-row tiles each, twelve 128-row ones): the counts reach their maximum and the
+    dispatch and row-order scales still equal the oracle's bit for bit."""
+    k = pkg("kernel")
+    wl = pkg("workloads")
+    T = 1500
+    cfg = wl.Config("all_local", T, 0, hot_local_experts=tuple(range(32)), seed=20261202)
+    d = dict(config_inputs(4))                   # offset 0: reuse its weights
+    d.update(wl.make_activations(cfg, device="cuda"))
+    d["output"] = torch.empty(T, 7168, dtype=torch.bfloat16, device="cuda")
+    d["local_expert_offset"] = 0
+    lay = k.workspace_layout(T)
+    ws = torch.empty(lay.total, dtype=torch.uint8, device="cuda")
+    note(f"[gpu] mask dispatch, all local, T={T}")
+    k.forward(*wl.as_args({**d, "output": torch.empty_like(d["output"])}), workspace=ws)
+    torch.cuda.synchronize()
+    o = oracle()
+    rids, rw = o.route(d["routing_logits"], d["routing_bias"], d["routed_scaling_factor"])
+    r = o.dispatch(rids, rw, 0, lay.tile_m)
+    assert int(r["exp_off"][-1]) == 8 * T
+    na = 8 * T
+    meta = ws[lay.meta:lay.meta + 35 * 4].view(torch.int32).cpu().numpy()
+    assert np.array_equal(meta[:33], r["exp_off"])
+    assert np.array_equal(ws[lay.sorted_tokens:lay.sorted_tokens + na * 4].view(torch.int32).cpu().numpy(),
+                          r["sorted_tok"])
+    assert np.array_equal(ws[lay.inverse_rows:lay.inverse_rows + na * 4].view(torch.int32).cpu().numpy()
+                          .reshape(T, 8), r["inv"])
+    m = ws[lay.token_masks:lay.token_masks + T * 4].view(torch.int32).cpu().numpy().view(np.uint32)
+    assert (sum((m >> i) & 1 for i in range(32)) == 8).all()     # eight local experts each
+    stok = torch.from_numpy(np.asarray(r["sorted_tok"], np.int64)).cuda()
+    tab = ws[lay.row_scales:lay.row_scales + 56 * na * 4].view(torch.float32).view(56, na)
+    assert torch.equal(tab, d["hidden_states_scale"][:, stok])
