@@ -179,7 +179,10 @@ __global__ __launch_bounds__(kChunk) void dispatch_place_kernel(
 // launch's work), spread over gridDim.y workgroups per chunk: each computes the chunk's
 // dispatch (only the first, y = 0, stores it) and writes the scales of its share of the
 // 56 K blocks; its chunk's token scales of those K blocks come into LDS by DMA at kernel
-// start, and its rows are written one contiguous run per expert.
+// start, and its rows are written one contiguous run per expert.  One more workgroup
+// (x = the chunk count, y = 0) counts the totals as the others do and writes only the
+// expert offsets and the tile lists: written by a chunk's workgroup, they delayed its end,
+// and with it the kernel's, by ~2 us at T = 8192.
 
 // Stage s of the transpose (s = 1, 2, 4, 8): lanes l and l ^ s swap the off-diagonal
 // s x s blocks of their 2s x 2s block.  The lower lane keeps its bits at positions with
@@ -222,6 +225,8 @@ __global__ __launch_bounds__(kChunk) void dispatch_masks_kernel(
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int chunk = blockIdx.x;
     const int t = chunk * kChunk + tid;
+    const bool tiler = chunk == (int)gridDim.x - 1;          // writes the offsets and tile lists
+    if (tiler && blockIdx.y != 0) return;                     // uniform: one tiler
     const bool lead = blockIdx.y == 0;                       // stores the dispatch
     const int kpb = (kHB + (int)gridDim.y - 1) / (int)gridDim.y;
     const int kb0 = (int)blockIdx.y * kpb, kb1 = min(kHB, kb0 + kpb);   // its token-scale K blocks
@@ -342,7 +347,7 @@ __global__ __launch_bounds__(kChunk) void dispatch_masks_kernel(
                 cc += wcnt[w][lane];
             }
         }
-        if (chunk == 0 && lead) {
+        if (tiler) {
             write_offsets_and_tiles_rt(lane < kEL ? total : 0, lane, off, exp_off, num_tiles, tiles, tm,
                                        num_tiles2, tiles2, tm2);
         } else {
@@ -356,6 +361,7 @@ __global__ __launch_bounds__(kChunk) void dispatch_masks_kernel(
         }
         if (lane == kEL - 1) cpre[kEL] = cp;
     }
+    if (tiler) return;   // uniform
     lds_barrier();
     if (tid < kEL) {
         int run = off[tid] + cbase[tid];
@@ -408,7 +414,7 @@ bool launch_dispatch_masks(const int* topk_ids, const float* topk_w, const uint3
     const int slices = row_scales ? min(8, max(1, 256 / nchunks)) : 1;
     auto run = [&](auto nb, auto gather) {
         launch_kernel((dispatch_masks_kernel<decltype(nb)::value, decltype(gather)::value>),
-                      dim3(nchunks, slices), dim3(kChunk), 0, stream, topk_ids, topk_w, masks, T, offset, tm,
+                      dim3(nchunks + 1, slices), dim3(kChunk), 0, stream, topk_ids, topk_w, masks, T, offset, tm,
                       tm2, exp_off, num_tiles, tiles, num_tiles2, tiles2, sorted_tok, sorted_w, inv,
                       hs_scale, row_scales, rows_cap);
     };
