@@ -5,7 +5,7 @@
 // there ~16 launches and ~20 torch allocations per call; here two to eight launches on
 // the caller's stream over one caller-provided workspace, no host synchronisation and no
 // allocation:
-//   route    (T/4 workgroups; inside GEMM1 for T <= 4) -> topk ids / weights
+//   route    (T/4 workgroups; inside GEMM1 for T <= 8) -> topk ids / weights
 //   dispatch (1 workgroup, or count + place kernels; inside GEMM1 for T <= 64)
 //                                  -> expert offsets, row tiles, permutation, inverse map
 //   (gather  -> token scales in row order, for the plans that read them so)

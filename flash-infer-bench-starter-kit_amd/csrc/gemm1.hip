@@ -276,17 +276,20 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(WPE)))
 // dispatch before the first weight load costs a workgroup about what the separate
 // kernel's two dependent loads (tile list, then permutation) cost.
 //
-// ROUTE (T <= kRouteInGemm1MaxT = 4): the routing too.  Every workgroup routes the call's
-// tokens itself from the logits (route_token, the route kernel's computation: wave w
-// takes token w) into LDS, where the dispatch reads them; the last
-// workgroup also writes them to the workspace.  The route launch, its kernel boundary
+// NRW > 0 (T <= NRW): the routing too.  Every workgroup routes the call's tokens itself
+// from the logits (route_token, the route kernel's computation: wave w takes token w) into
+// LDS, where the dispatch reads them; the last workgroup also writes them to the
+// workspace.  NRW = 8 (5 <= T <= 8) runs workgroups of 8 waves, one per CU, so that a SIMD
+// routes two tokens, not six; its waves then work as two groups of four, each taking every
+// other of the workgroup's items, in step (a group without an item passes the item's two
+// barriers), so a CU still streams two items at a time.  The route launch, its kernel boundary
 // and the dispatch's dependent load of the routing ids go away.  Nothing clears the
 // C-range flag word before this kernel, so it writes the call's wide_tag there instead
 // of 1, and the GEMM2 after it compares the word with the same tag.
 constexpr int kDG1MaxTiles = dispatch_max_tiles(kDispatchInGemm1MaxT, 16);   // 64
 
-template <bool ROUTE>
-__global__ __launch_bounds__(256) void gemm1_rstream_dispatch_kernel(
+template <int NRW>
+__global__ __launch_bounds__(NRW == 8 ? 512 : 256) void gemm1_rstream_dispatch_kernel(
     RouteIn rin, int* __restrict__ topk_ids, float* __restrict__ topk_w, int T, int offset,
     const uint8_t* __restrict__ hidden, const float* __restrict__ hs_scale,
     const uint8_t* __restrict__ w1, const float* __restrict__ s1, int* __restrict__ meta,
@@ -294,8 +297,9 @@ __global__ __launch_bounds__(256) void gemm1_rstream_dispatch_kernel(
     int* __restrict__ inv, Intermediate C, int wide_tag) {
     using S = Gemm1Stream<1, 1, false>;
     constexpr int R = kDispatchInGemm1MaxT * kTopK;
-    __shared__ __attribute__((aligned(1024))) uint8_t slot_lds[4][S::kSlot];
-    __shared__ v4f red[4][2][1][64];
+    constexpr int NG = NRW == 8 ? 2 : 1;   // groups of 4 waves taking items
+    __shared__ __attribute__((aligned(1024))) uint8_t slot_lds[4 * NG][S::kSlot];
+    __shared__ v4f red[4 * NG][2][1][64];
     __shared__ int s_exp_off[kEL + 1];
     __shared__ int s_num_tiles;
     __shared__ int4 s_tiles[kDG1MaxTiles];
@@ -310,12 +314,13 @@ __global__ __launch_bounds__(256) void gemm1_rstream_dispatch_kernel(
     MOE_STAMP(3 * (int)blockIdx.x);
     const int* ids_src = topk_ids;
     const float* w_src = topk_w;
-    if constexpr (ROUTE) {
-        static_assert(kRouteInGemm1MaxT == 4, "one token per wave");
-        __shared__ __attribute__((aligned(16))) int s_rid[kRouteInGemm1MaxT][kTopK];
-        __shared__ __attribute__((aligned(16))) float s_rw[kRouteInGemm1MaxT][kTopK];
-        __shared__ float s_sel[4][kTopK];
-        __shared__ int s_sel_id[4][kTopK];
+    if constexpr (NRW > 0) {
+        static_assert(NRW == 4 || NRW == 8, "one token per wave");
+        static_assert(kRouteInGemm1MaxT <= 8, "at most 8 waves route");
+        __shared__ __attribute__((aligned(16))) int s_rid[NRW][kTopK];
+        __shared__ __attribute__((aligned(16))) float s_rw[NRW][kTopK];
+        __shared__ float s_sel[NRW][kTopK];
+        __shared__ int s_sel_id[NRW][kTopK];
         const int t = wave;
         if (t < T) {   // uniform per wave
             const float4 lg = reinterpret_cast<const float4*>(rin.logits + (size_t)t * kEG)[lane];
@@ -350,7 +355,7 @@ __global__ __launch_bounds__(256) void gemm1_rstream_dispatch_kernel(
     }
     __syncthreads();
     const int ntiles = s_num_tiles;
-    if (lane < T) {   // token lane: its routes 2 wave and 2 wave + 1
+    if (wave < 4 && lane < T) {   // token lane: its routes 2 wave and 2 wave + 1
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
             const int k = 2 * wave + kk;
@@ -378,11 +383,32 @@ __global__ __launch_bounds__(256) void gemm1_rstream_dispatch_kernel(
     MOE_STAMP(3 * (int)blockIdx.x + 1);
     const TokenScales sa{hs_scale, T, 0};
     const int nwork = ntiles * S::kItems;
-    for (int work = blockIdx.x; work < nwork; work += gridDim.x) {
-        const int4 tile = s_tiles[work / S::kItems];
-        gemm1_rstream_item<4, 1, 1, false>(hidden, sa, w1, s1, tile.x, tile.y, tile.z,
-                                           work % S::kItems, [&](int row) { return s_stok[row]; },
-                                           C, meta + kCWideFlag, slot_lds, red, wave, wide_tag);
+    if constexpr (NG == 2) {
+        // group g takes the workgroup's items 2 i + g (items b, b + G, b + 2 G, ...)
+        const int grp = wave >> 2, w4 = wave & 3;
+        const int G = gridDim.x, b = blockIdx.x;
+        const int mine = b < nwork ? (nwork - b + G - 1) / G : 0;
+        for (int i = 0; i < (mine + 1) / 2; ++i) {
+            const int k = 2 * i + grp;
+            if (k < mine) {   // uniform per wave
+                const int work = b + k * G;
+                const int4 tile = s_tiles[work / S::kItems];
+                gemm1_rstream_item<4, 1, 1, false>(hidden, sa, w1, s1, tile.x, tile.y, tile.z,
+                                                   work % S::kItems, [&](int row) { return s_stok[row]; },
+                                                   C, meta + kCWideFlag, &slot_lds[4 * grp], &red[4 * grp],
+                                                   w4, wide_tag);
+            } else {
+                __syncthreads();   // the two barriers of the item the other group runs
+                __syncthreads();
+            }
+        }
+    } else {
+        for (int work = blockIdx.x; work < nwork; work += gridDim.x) {
+            const int4 tile = s_tiles[work / S::kItems];
+            gemm1_rstream_item<4, 1, 1, false>(hidden, sa, w1, s1, tile.x, tile.y, tile.z,
+                                               work % S::kItems, [&](int row) { return s_stok[row]; },
+                                               C, meta + kCWideFlag, slot_lds, red, wave, wide_tag);
+        }
     }
     MOE_STAMP(3 * (int)blockIdx.x + 2);
 }
@@ -688,15 +714,16 @@ static int grid_for(long long work) { return (int)(work < 4096 ? work : 4096); }
 namespace {
 constexpr int kMaxDevices = 64;
 std::mutex g_dg1_mu;
-int g_dg1_grid[2][kMaxDevices] = {};
+int g_dg1_grid[3][kMaxDevices] = {};
 }  // namespace
 
 // GEMM1 with the dispatch folded in (and with rin.logits set, T <= kRouteInGemm1MaxT, the
 // routing too): a persistent grid of as many workgroups as the device holds at once
-// (occupancy x CUs, looked up once per device and kernel), capped by the most work items
-// T tokens can have.  Without the routing, topk_ids / topk_w hold the routing; with it,
-// the kernel writes them.  wide_tag is the value the kernel writes into the C-range flag
-// word (1 after a route kernel cleared it).
+// (occupancy x CUs, looked up once per device and kernel; with the 8-wave routing of
+// 5 <= T <= 8, one per CU, so that a SIMD routes two tokens, not six), capped by the most
+// work items T tokens can have.  Without the routing, topk_ids / topk_w hold the routing;
+// with it, the kernel writes them.  wide_tag is the value the kernel writes into the
+// C-range flag word (1 after a route kernel cleared it).
 bool launch_gemm1_dispatch(const RouteIn& rin, int* topk_ids, float* topk_w, int T, int offset,
                            const uint8_t* hidden, const float* hs_scale, const uint8_t* w1,
                            const float* s1, int* meta, int4* tiles, int* sorted_tok,
@@ -705,32 +732,40 @@ bool launch_gemm1_dispatch(const RouteIn& rin, int* topk_ids, float* topk_w, int
     const bool route = rin.logits != nullptr;
     if (T <= 0 || T > (route ? kRouteInGemm1MaxT : kDispatchInGemm1MaxT)) return false;
     if (route && (rin.bias == nullptr || wide_tag < 2)) return false;
-    const void* fn = route ? reinterpret_cast<const void*>(gemm1_rstream_dispatch_kernel<true>)
-                           : reinterpret_cast<const void*>(gemm1_rstream_dispatch_kernel<false>);
+    const int nrw = route ? (T <= 4 ? 4 : 8) : 0;   // routing waves
+    const int kind = nrw / 4;                        // 0, 1, 2
+    const void* fn = nrw == 8 ? reinterpret_cast<const void*>(gemm1_rstream_dispatch_kernel<8>)
+                   : nrw == 4 ? reinterpret_cast<const void*>(gemm1_rstream_dispatch_kernel<4>)
+                              : reinterpret_cast<const void*>(gemm1_rstream_dispatch_kernel<0>);
+    const int threads = nrw == 8 ? 512 : 256;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
     int resident = 0;
     {
         std::lock_guard<std::mutex> lock(g_dg1_mu);
-        int& g = g_dg1_grid[route ? 1 : 0][dev];
+        int& g = g_dg1_grid[kind][dev];
         if (g == 0) {
             int per_cu = 0, cus = 0;
-            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, 0) != hipSuccess ||
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, 0) != hipSuccess ||
                 hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
                 per_cu * cus <= 0)
                 return false;
-            g = per_cu * cus;
+            g = nrw == 8 ? cus : per_cu * cus;
         }
         resident = g;
     }
     const long long items = (long long)(((long long)T * kTopK + 15) / 16 + kEL) * Gemm1Stream<1, 1, false>::kItems;
     const int grid = (int)(items < resident ? items : resident);
-    if (route)
-        launch_kernel(gemm1_rstream_dispatch_kernel<true>, dim3(grid), dim3(256), 0, stream, rin,
+    if (nrw == 8)
+        launch_kernel(gemm1_rstream_dispatch_kernel<8>, dim3(grid), dim3(512), 0, stream, rin,
+                      topk_ids, topk_w, T, offset, hidden, hs_scale, w1, s1, meta, tiles,
+                      sorted_tok, sorted_w, inv, C, wide_tag);
+    else if (nrw == 4)
+        launch_kernel(gemm1_rstream_dispatch_kernel<4>, dim3(grid), dim3(256), 0, stream, rin,
                       topk_ids, topk_w, T, offset, hidden, hs_scale, w1, s1, meta, tiles,
                       sorted_tok, sorted_w, inv, C, wide_tag);
     else
-        launch_kernel(gemm1_rstream_dispatch_kernel<false>, dim3(grid), dim3(256), 0, stream, rin,
+        launch_kernel(gemm1_rstream_dispatch_kernel<0>, dim3(grid), dim3(256), 0, stream, rin,
                       topk_ids, topk_w, T, offset, hidden, hs_scale, w1, s1, meta, tiles,
                       sorted_tok, sorted_w, inv, C, 1);
     return true;

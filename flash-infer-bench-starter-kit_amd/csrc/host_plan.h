@@ -123,7 +123,7 @@ inline int plan_for(int32_t T, int32_t flags, Plan* p) {
     int g1, g2;
     // GEMM1 with the dispatch folded in reads the token scales by token: asking for the
     // gathered ones selects the separate dispatch there
-    if (T <= kRouteInGemm1MaxT && !on) g1 = 9, g2 = 6;   // T <= 4
+    if (T <= kRouteInGemm1MaxT && !on) g1 = 9, g2 = 6;   // T <= 8
     else if (T <= kFusedCombineMaxT && !on) g1 = 5, g2 = 6;
     else if (T <= kDispatchInGemm1MaxT && !on) g1 = 5, g2 = 1;
     else if (T <= 88) g1 = 1, g2 = 1;

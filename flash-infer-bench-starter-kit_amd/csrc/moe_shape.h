@@ -37,10 +37,12 @@ constexpr int kGroup16 = 16;       // columns per fp16-form exponent byte
 constexpr int kDispatchInGemm1MaxT = 64;
 
 // Largest T whose routing also runs inside the GEMM1 launch (GEMM1 variant 9): every
-// workgroup routes the call's tokens, one per wave, before its items.  A wave's routing is
-// a dependent chain of ~600 instructions; two tokens on one wave (T = 8) delayed the first
-// weight load by more than the route launch costs.
-constexpr int kRouteInGemm1MaxT = 4;
+// workgroup routes the call's tokens, one per wave, before its items (T <= 4: the 4 waves
+// of the usual workgroup; 5 <= T <= 8: workgroups of 8 waves, one per CU, working as two
+// groups of four after routing).  A wave's routing is a dependent chain of ~600
+// instructions; two tokens on one wave delayed the first weight load by more than the
+// route launch costs, and so did six routing waves on one SIMD.
+constexpr int kRouteInGemm1MaxT = 8;
 
 // Token counts whose forward dispatch is one launch over the local-expert masks the route
 // kernel writes (dispatch_masks_kernel): every workgroup counts the experts of all T tokens

@@ -127,7 +127,7 @@ typedef struct moe_mi355_args {
  *                                  the combine computed inside it (T <= 32, the default
  *                                  there, after GEMM1 variant 5, 1 or 9): bit-identical
  *                                  output, one launch fewer.  GEMM1 variant 9 is variant 5
- *                                  with the routing computed inside it too (T <= 4, the
+ *                                  with the routing computed inside it too (T <= 8, the
  *                                  default there; pairs with GEMM2 variant 6 only):
  *                                  bit-identical output and workspace routing, one launch
  *                                  fewer; it marks C beyond the fp16 range with a per-call

@@ -246,12 +246,13 @@ def test_layout_reports_the_forced_plan():
     assert k.workspace_layout(8, k.plan_flags(1, 6)).dispatch_in_gemm1 == 0
     for t, g1 in ((33, 5), (8, 2), (8, 4), (8, 7)):
         assert lib.moe_mi355_get_workspace_layout(t, k.plan_flags(g1, 6), ctypes.byref(lay)) == -7
-    # GEMM1 variant 9 (routing, dispatch and GEMM1 in one launch) up to T = 4, with
-    # GEMM2 variant 6 only
-    assert k.workspace_layout(4, k.plan_flags(9, 6)).dispatch_in_gemm1 == 1
-    assert k.workspace_layout(4, k.plan_flags(9, 6)).combine_in_gemm2 == 1
-    assert k.workspace_layout(4, k.plan_flags(9, 6)).tile_m == 16
-    for t, g2 in ((5, 6), (8, 6), (4, 1), (4, 3), (4, 5), (1, 1)):
+    # GEMM1 variant 9 (routing, dispatch and GEMM1 in one launch) up to T = 8, with GEMM2
+    # variant 6 only
+    for t in (4, 5, 8):
+        assert k.workspace_layout(t, k.plan_flags(9, 6)).dispatch_in_gemm1 == 1
+        assert k.workspace_layout(t, k.plan_flags(9, 6)).combine_in_gemm2 == 1
+        assert k.workspace_layout(t, k.plan_flags(9, 6)).tile_m == 16
+    for t, g2 in ((9, 6), (16, 6), (4, 1), (4, 3), (4, 5), (1, 1)):
         assert lib.moe_mi355_get_workspace_layout(t, k.plan_flags(9, g2), ctypes.byref(lay)) == -7
     assert lib.moe_mi355_get_workspace_layout(4, k.plan_flags(9, 6) | k.FLAG_ROW_SCALES_ON,
                                               ctypes.byref(lay)) == -7

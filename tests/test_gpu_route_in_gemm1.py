@@ -1,5 +1,7 @@
 """GEMM1 with the routing and the dispatch folded in (GEMM1 variant 9, the plan for
-T <= 4): every workgroup routes the call's tokens from the logits itself, then runs the
+T <= 8; from T = 5 in workgroups of 8 waves, one token per wave, then two groups of four
+taking items): every
+workgroup routes the call's tokens from the logits itself, then runs the
 folded dispatch and its streaming items; the route launch goes away.  Its output must
 be bit-identical to the pair it replaces (GEMM1 variant 5 after the route kernel, with
 GEMM2 variant 6), its workspace must hold the same routing and dispatch, and the
@@ -37,7 +39,8 @@ def _c_flag(ws, lay):
 
 
 @pytest.mark.parametrize("T,cfg,offset", [(1, 0, 0), (1, 3, 32), (2, 1, 0), (3, 3, 0), (3, 0, 96),
-                                          (4, 0, 0), (4, 1, 224), (4, 3, 64)])
+                                          (4, 0, 0), (4, 1, 224), (4, 3, 64), (5, 0, 0), (6, 3, 32),
+                                          (7, 1, 0), (8, 0, 0), (8, 3, 224)])
 def test_matches_the_route_kernel_pair_bit_for_bit(T, cfg, offset):
     k = pkg("kernel")
     d = first_tokens(config_inputs(cfg), T)
