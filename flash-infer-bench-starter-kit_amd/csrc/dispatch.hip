@@ -172,8 +172,9 @@ __global__ __launch_bounds__(kChunk) void dispatch_place_kernel(
 // expert over all T tokens itself, so no count launch runs before it: in each row of 16
 // lanes, 16 masks are transposed as two 16 x 16 bit matrices (lane i of the row then
 // holds bit i and bit 16 + i of the row's 16 masks), and two popcounts give the counts
-// of experts i and 16 + i over them.  The totals give the expert offsets (and, in chunk
-// 0, the tile lists), the counts of the chunks before this one its base in each expert;
+// of experts i and 16 + i over them.  The totals give the expert offsets (and, in the extra
+// workgroup below, the tile lists), the counts of the chunks before this one its base in
+// each expert;
 // the ranks inside the chunk and the placement are the place kernel's.  With row_scales
 // set, the workgroups also write the token scales of the rows in row order (the gather
 // launch's work), spread over gridDim.y workgroups per chunk: each computes the chunk's
@@ -197,6 +198,12 @@ __device__ __forceinline__ uint32_t transpose_stage(uint32_t x, uint32_t partner
 }
 
 static_assert(kMaskDispatchMaxT <= 64 * kChunk, "the count reads at most 64 chunks");
+
+// Token-scale K blocks per gathering workgroup: 8 workgroups per chunk up to 32 chunks,
+// 4 beyond (about 256 workgroups in all).
+template <int NB>
+constexpr int kMasksKbPerSlice = NB <= 32 ? kHB / 8 : kHB / 4;
+static_assert(kHB % 8 == 0, "the K blocks split evenly over 8 or 4 workgroups");
 static_assert(kChunk <= 256, "a token's index in its chunk is kept in one byte");
 
 // NB: chunks the count reads (a power of two >= ceil(T / 256)); masks past T read 0.
@@ -228,12 +235,15 @@ __global__ __launch_bounds__(kChunk) void dispatch_masks_kernel(
     const bool tiler = chunk == (int)gridDim.x - 1;          // writes the offsets and tile lists
     if (tiler && blockIdx.y != 0) return;                     // uniform: one tiler
     const bool lead = blockIdx.y == 0;                       // stores the dispatch
-    const int kpb = (kHB + (int)gridDim.y - 1) / (int)gridDim.y;
-    const int kb0 = (int)blockIdx.y * kpb, kb1 = min(kHB, kb0 + kpb);   // its token-scale K blocks
+    // its token-scale K blocks: KPB of them from kb0 (gridDim.y = kHB / KPB workgroups per
+    // chunk); a compile-time count, so that the waits for the loads issued before the DMA
+    // count it exactly
+    constexpr int KPB = kMasksKbPerSlice<NB>;
+    const int kb0 = (int)blockIdx.y * KPB;
 
     // every load first, in the order they are needed: this chunk's routes, the masks of
-    // every chunk (token b * 256 + tid), then the chunk's token scales straight into LDS
-    // (reads past T return 0 and are not used)
+    // every chunk, then the chunk's token scales straight into LDS (reads past T return 0
+    // and are not used)
     v4u rid[2], rw[2];
     {
         const __amdgpu_buffer_rsrc_t rs_i = buffer_rsrc(topk_ids, (uint32_t)T * kTopK * 4);
@@ -256,9 +266,12 @@ __global__ __launch_bounds__(kChunk) void dispatch_masks_kernel(
             mk[i] = __builtin_amdgcn_raw_buffer_load_b128(
                 rs_m, (uint32_t)((kChunkWaves * i + wave) * kChunk + 4 * lane) * 4, 0, 0);
     }
-    if constexpr (GATHER) {
+    if constexpr (GATHER) {   // (the tiler's DMA is not used; skipping it under a branch
+                              // made the waits below count it conservatively)
         const __amdgpu_buffer_rsrc_t rs_s = buffer_rsrc(hs_scale, (uint32_t)T * kHB * 4);
-        for (int kb = kb0; kb < kb1; ++kb) bdma4(rs_s, (uint32_t)t * 4, (uint32_t)kb * T * 4, &s_hs[kb][64 * wave]);
+#pragma unroll
+        for (int k = 0; k < KPB; ++k)
+            bdma4(rs_s, (uint32_t)t * 4, (uint32_t)(kb0 + k) * T * 4, &s_hs[kb0 + k][64 * wave]);
     }
     TokenRoutes r;
     {
@@ -331,7 +344,7 @@ __global__ __launch_bounds__(kChunk) void dispatch_masks_kernel(
     }
 
     // LDS-only barriers below: __syncthreads would also wait for the token-scale DMA
-    // and for chunk 0's tile-list stores
+    // and for the place stores
     int rank[kTopK];
     wave_ranks(r, wave, lane, wcnt, bal[wave], rank);
     lds_barrier();
@@ -393,7 +406,7 @@ __global__ __launch_bounds__(kChunk) void dispatch_masks_kernel(
     for (int q = tid; q < nq; q += kChunk) {
         const int row = s_row[q], tk = s_tok[q];
 #pragma unroll 8
-        for (int kb = kb0; kb < kb1; ++kb) row_scales[(size_t)kb * rows_cap + row] = s_hs[kb][tk];
+        for (int k = 0; k < KPB; ++k) row_scales[(size_t)(kb0 + k) * rows_cap + row] = s_hs[kb0 + k][tk];
     }
 }
 
@@ -409,11 +422,12 @@ bool launch_dispatch_masks(const int* topk_ids, const float* topk_w, const uint3
     if (tm2 != 0 && (tm2 != 128 || !tiles2 || !num_tiles2)) return false;
     if ((hs_scale == nullptr) != (row_scales == nullptr)) return false;
     const int nchunks = (T + kChunk - 1) / kChunk;
-    // with the gather, about 256 workgroups: up to 8 per chunk, each writing the token
-    // scales of 56 / 8 .. 56 K blocks (the stores are what takes the time there)
-    const int slices = row_scales ? min(8, max(1, 256 / nchunks)) : 1;
+    // with the gather, about 256 workgroups: 8 or 4 per chunk, each writing the token
+    // scales of 7 or 14 of the 56 K blocks (the stores are what takes the time there)
     auto run = [&](auto nb, auto gather) {
-        launch_kernel((dispatch_masks_kernel<decltype(nb)::value, decltype(gather)::value>),
+        constexpr int NBv = decltype(nb)::value;
+        const int slices = decltype(gather)::value ? kHB / kMasksKbPerSlice<NBv> : 1;
+        launch_kernel((dispatch_masks_kernel<NBv, decltype(gather)::value>),
                       dim3(nchunks + 1, slices), dim3(kChunk), 0, stream, topk_ids, topk_w, masks, T, offset, tm,
                       tm2, exp_off, num_tiles, tiles, num_tiles2, tiles2, sorted_tok, sorted_w, inv,
                       hs_scale, row_scales, rows_cap);
