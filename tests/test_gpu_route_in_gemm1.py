@@ -55,7 +55,7 @@ def test_matches_the_route_kernel_pair_bit_for_bit(T, cfg, offset):
     assert st["frac_within"] == 1.0, st
 
 
-@pytest.mark.parametrize("T,offset", [(3, 0), (4, 64)])
+@pytest.mark.parametrize("T,offset", [(3, 0), (4, 64), (7, 32), (8, 0)])
 def test_workspace_routing_and_dispatch_are_bit_exact(T, offset):
     """The routing ids and weights the last workgroup writes, and the dispatch, equal
     the oracle's bit for bit (the separate route kernel's are pinned the same way)."""
@@ -88,41 +88,44 @@ def test_workspace_routing_and_dispatch_are_bit_exact(T, offset):
     assert np.array_equal(arr(lay.inverse_rows, T * 8, torch.int32).reshape(T, 8), r["inv"])
 
 
-def test_c_beyond_fp16_sets_the_call_tag():
+@pytest.mark.parametrize("T", [4, 8])
+def test_c_beyond_fp16_sets_the_call_tag(T):
     """Hidden-state scales 2^10 times larger: C leaves the fp16 range, GEMM1 writes the
     call's tag (>= 2) into the flag word, GEMM2 takes its rare path, and the output is the
     route-kernel pair's bit for bit.  A normal call on the same workspace afterwards (a
-    new tag; the stale one stays in the word) takes the normal path and matches too."""
+    new tag; the stale one stays in the word) takes the normal path and matches too.
+    T = 4 runs the 4-wave form, T = 8 the 8-wave one."""
     k = pkg("kernel")
-    d = dict(first_tokens(config_inputs(1), 4))
+    d = dict(first_tokens(config_inputs(1), T))
     d["hidden_states_scale"] = d["hidden_states_scale"] * 1024.0
     flags = k.plan_flags(9, 6)
-    lay = k.workspace_layout(4, flags)
+    lay = k.workspace_layout(T, flags)
     ws = torch.empty(lay.total, dtype=torch.uint8, device="cuda")
-    note("[gpu] route in GEMM1, C beyond fp16, T=4")
+    note(f"[gpu] route in GEMM1, C beyond fp16, T={T}")
     wide = _call(d, flags, ws)
     tag = _c_flag(ws, lay)
     assert tag >= 2
     assert torch.equal(_bits(wide), _bits(run_forward(d, flags=k.plan_flags(5, 6))))
-    d2 = first_tokens(config_inputs(1), 4)
+    d2 = first_tokens(config_inputs(1), T)
     normal = _call(d2, flags, ws)
     assert _c_flag(ws, lay) == tag          # nothing wrote the word on the normal call
     assert torch.equal(_bits(normal), _bits(run_forward(d2, flags=k.plan_flags(5, 6))))
 
 
-def test_flag_word_holding_the_next_tag_still_gives_the_right_output():
+@pytest.mark.parametrize("T", [4, 8])
+def test_flag_word_holding_the_next_tag_still_gives_the_right_output(T):
     """A workspace whose flag word already holds the tag the next call will use (the tag
     goes up by one per call of this plan): GEMM2 takes its rare path on a C that never left
     the fp16 range, reading the group exponents GEMM1 wrote (all 0), and the output stays
     within the oracle's tolerance."""
     k = pkg("kernel")
-    d = dict(first_tokens(config_inputs(1), 4))
+    d = dict(first_tokens(config_inputs(1), T))
     dw = dict(d)
     dw["hidden_states_scale"] = d["hidden_states_scale"] * 1024.0
     flags = k.plan_flags(9, 6)
-    lay = k.workspace_layout(4, flags)
+    lay = k.workspace_layout(T, flags)
     ws = torch.empty(lay.total, dtype=torch.uint8, device="cuda")
-    note("[gpu] route in GEMM1, flag word holding the next tag, T=4")
+    note(f"[gpu] route in GEMM1, flag word holding the next tag, T={T}")
     _call(dw, flags, ws)
     tag = _c_flag(ws, lay)
     ws[lay.meta + C_FLAG * 4:lay.meta + (C_FLAG + 1) * 4].view(torch.int32).fill_(tag + 1)
@@ -130,15 +133,16 @@ def test_flag_word_holding_the_next_tag_still_gives_the_right_output():
     out = _call(d, flags, ws)
     assert _c_flag(ws, lay) == tag + 1
     assert not torch.isnan(out.float()).any()
-    st = compare_to_oracle(d, out, list(range(4)))
+    st = compare_to_oracle(d, out, list(range(T)))
     note(f"[gpu] rare path on a normal C: {st}")
     assert st["frac_within"] == 1.0, st
 
 
-def test_no_local_expert_gives_zeros():
+@pytest.mark.parametrize("T", [4, 8])
+def test_no_local_expert_gives_zeros(T):
     k = pkg("kernel")
-    d = first_tokens(config_inputs(0), 4)
+    d = first_tokens(config_inputs(0), T)
     d["local_expert_offset"] = 256
-    note("[gpu] route in GEMM1, no local expert")
+    note(f"[gpu] route in GEMM1, no local expert, T={T}")
     out = run_forward(d, flags=k.plan_flags(9, 6))
     assert torch.equal(_bits(out), torch.zeros_like(_bits(out)))
