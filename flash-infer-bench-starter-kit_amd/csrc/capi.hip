@@ -21,7 +21,6 @@
 #include <stdlib.h>
 #include <string.h>
 
-#include <atomic>
 #include <mutex>
 
 #include "host_plan.h"
@@ -41,11 +40,11 @@ bool launch_gemm1(int, const uint8_t*, const TokenScales&, int, const uint8_t*, 
                   bool, hipStream_t);
 bool launch_gemm1_dispatch(const RouteIn&, int*, float*, int, int, const uint8_t*, const float*,
                            const uint8_t*, const float*, int*, int4*, int*, float*, int*,
-                           const Intermediate&, int, hipStream_t);
+                           const Intermediate&, hipStream_t);
 bool launch_gemm2(int, const Intermediate&, const uint8_t*, const float*, const int4*, const int*,
                   const int*, int, const ExpertRows&, hipStream_t);
 bool launch_gemm2_combine(const Intermediate&, const uint8_t*, const float*, const int4*, const int*,
-                          int*, const int*, const float*, int, uint16_t*, int, hipStream_t);
+                          int*, const int*, const float*, int, uint16_t*, hipStream_t);
 void launch_combine(const ExpertRows&, const int*, const float*, const int*, int, uint16_t*, hipStream_t);
 void launch_e4m3_to_bf16(const uint8_t*, uint16_t*, int, hipStream_t);
 void launch_c_f16_to_hilo(const Intermediate&, const int*, hipStream_t);
@@ -131,13 +130,6 @@ int scratch_on_current_device(void** out) {
     return MOE_OK;
 }
 
-// The C-range tag of a call whose GEMM1 routes its tokens itself (GEMM1 variant 9): a
-// value >= 2 that differs from the tags of the 2^31 - 3 calls before it in the process.
-std::atomic<uint32_t> g_wide_tag{0};
-int next_wide_tag() {
-    return 2 + (int)(g_wide_tag.fetch_add(1, std::memory_order_relaxed) % 0x7ffffffdu);
-}
-
 // The forward's launch sequence over a workspace of ws_bytes at ws (the caller's, or
 // for moe_mi355_forward_noalloc the library's own).  Returns MOE_OK or a status; a
 // status from a failed launch means the earlier launches of the call may have run.
@@ -176,10 +168,7 @@ int forward_impl(const moe_mi355_args& a, void* workspace, size_t ws_bytes, hipS
     };
     moe::g_kernel_timer = timer;   // the launches below time themselves (cleared before return)
 
-    // GEMM1 variant 9 routes the tokens itself (timed as the GEMM1 stage) and marks C
-    // beyond the fp16 range with the call's tag instead of 1 (no route kernel clears the
-    // flag word before it)
-    const int wide_tag = plan.route_in_gemm1 ? next_wide_tag() : 1;
+    // GEMM1 variant 9 routes the tokens itself (timed as the GEMM1 stage)
     const int offset = clamp_offset(a.local_expert_offset);
     // the dispatch in one launch from the route kernel's local-expert masks (with the
     // token-scale gather when GEMM1 reads the scales in row order)
@@ -220,7 +209,7 @@ int forward_impl(const moe_mi355_args& a, void* workspace, size_t ws_bytes, hipS
         ok = ok && moe::launch_gemm1_dispatch(rin, ids, wts, T, offset,
                                               a.hidden_states, a.hidden_states_scale,
                                               a.gemm1_weights, a.gemm1_weights_scale, meta, tiles,
-                                              stok, sw, inv, inter, wide_tag, s);
+                                              stok, sw, inv, inter, s);
     }
     else
         ok = ok && moe::launch_gemm1(plan.g1, a.hidden_states, sa, T, a.gemm1_weights,
@@ -230,7 +219,7 @@ int forward_impl(const moe_mi355_args& a, void* workspace, size_t ws_bytes, hipS
     if (ok && plan.convert) moe::launch_c_f16_to_hilo(inter, meta, s);   // in the GEMM2 stage
     if (ok && plan.combine_in_gemm2)      // GEMM2 writes the output (timed as the GEMM2 stage)
         ok = moe::launch_gemm2_combine(inter, a.gemm2_weights, a.gemm2_weights_scale, tiles,
-                                       num_tiles, meta, inv, sw, T, a.output, wide_tag, s);
+                                       num_tiles, meta, inv, sw, T, a.output, s);
     else if (ok && half)
         ok = moe::launch_gemm2(plan.g2, inter, a.gemm2_weights, a.gemm2_weights_scale, tiles2,
                                num_tiles2, meta, moe::dispatch_max_tiles(T, plan.tm2), rows, s);

@@ -284,8 +284,9 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(WPE)))
 // other of the workgroup's items, in step (a group without an item passes the item's two
 // barriers), so a CU still streams two items at a time.  The route launch, its kernel boundary
 // and the dispatch's dependent load of the routing ids go away.  Nothing clears the
-// C-range flag word before this kernel, so it writes the call's wide_tag there instead
-// of 1, and the GEMM2 after it compares the word with the same tag.
+// C-range flag word before this kernel: it sets the word when C goes beyond the fp16
+// range, and the GEMM2 after it (variant 6) checks a nonzero word against C's group
+// exponents (a stale word from earlier calls or other data sends it nowhere else).
 constexpr int kDG1MaxTiles = dispatch_max_tiles(kDispatchInGemm1MaxT, 16);   // 64
 
 template <int NRW>
@@ -294,7 +295,7 @@ __global__ __launch_bounds__(NRW == 8 ? 512 : 256) void gemm1_rstream_dispatch_k
     const uint8_t* __restrict__ hidden, const float* __restrict__ hs_scale,
     const uint8_t* __restrict__ w1, const float* __restrict__ s1, int* __restrict__ meta,
     int4* __restrict__ tiles, int* __restrict__ sorted_tok, float* __restrict__ sorted_w,
-    int* __restrict__ inv, Intermediate C, int wide_tag) {
+    int* __restrict__ inv, Intermediate C) {
     using S = Gemm1Stream<1, 1, false>;
     constexpr int R = kDispatchInGemm1MaxT * kTopK;
     constexpr int NG = NRW == 8 ? 2 : 1;   // groups of 4 waves taking items
@@ -383,6 +384,7 @@ __global__ __launch_bounds__(NRW == 8 ? 512 : 256) void gemm1_rstream_dispatch_k
     MOE_STAMP(3 * (int)blockIdx.x + 1);
     const TokenScales sa{hs_scale, T, 0};
     const int nwork = ntiles * S::kItems;
+    int* const c_wide = meta + kCWideFlag;
     if constexpr (NG == 2) {
         // group g takes the workgroup's items 2 i + g (items b, b + G, b + 2 G, ...)
         const int grp = wave >> 2, w4 = wave & 3;
@@ -395,8 +397,7 @@ __global__ __launch_bounds__(NRW == 8 ? 512 : 256) void gemm1_rstream_dispatch_k
                 const int4 tile = s_tiles[work / S::kItems];
                 gemm1_rstream_item<4, 1, 1, false>(hidden, sa, w1, s1, tile.x, tile.y, tile.z,
                                                    work % S::kItems, [&](int row) { return s_stok[row]; },
-                                                   C, meta + kCWideFlag, &slot_lds[4 * grp], &red[4 * grp],
-                                                   w4, wide_tag);
+                                                   C, c_wide, &slot_lds[4 * grp], &red[4 * grp], w4);
             } else {
                 __syncthreads();   // the two barriers of the item the other group runs
                 __syncthreads();
@@ -407,7 +408,7 @@ __global__ __launch_bounds__(NRW == 8 ? 512 : 256) void gemm1_rstream_dispatch_k
             const int4 tile = s_tiles[work / S::kItems];
             gemm1_rstream_item<4, 1, 1, false>(hidden, sa, w1, s1, tile.x, tile.y, tile.z,
                                                work % S::kItems, [&](int row) { return s_stok[row]; },
-                                               C, meta + kCWideFlag, slot_lds, red, wave, wide_tag);
+                                               C, c_wide, slot_lds, red, wave);
         }
     }
     MOE_STAMP(3 * (int)blockIdx.x + 2);
@@ -722,16 +723,16 @@ int g_dg1_grid[3][kMaxDevices] = {};
 // (occupancy x CUs, looked up once per device and kernel; with the 8-wave routing of
 // 5 <= T <= 8, one per CU, so that a SIMD routes two tokens, not six), capped by the most
 // work items T tokens can have.  Without the routing, topk_ids / topk_w hold the routing;
-// with it, the kernel writes them.  wide_tag is the value the kernel writes into the
-// C-range flag word (1 after a route kernel cleared it).
+// with it, the kernel writes them.  It sets the C-range flag word when C goes beyond the
+// fp16 range (cleared by the route kernel, or with the routing not cleared at all).
 bool launch_gemm1_dispatch(const RouteIn& rin, int* topk_ids, float* topk_w, int T, int offset,
                            const uint8_t* hidden, const float* hs_scale, const uint8_t* w1,
                            const float* s1, int* meta, int4* tiles, int* sorted_tok,
-                           float* sorted_w, int* inv, const Intermediate& C, int wide_tag,
+                           float* sorted_w, int* inv, const Intermediate& C,
                            hipStream_t stream) {
     const bool route = rin.logits != nullptr;
     if (T <= 0 || T > (route ? kRouteInGemm1MaxT : kDispatchInGemm1MaxT)) return false;
-    if (route && (rin.bias == nullptr || wide_tag < 2)) return false;
+    if (route && rin.bias == nullptr) return false;
     const int nrw = route ? (T <= 4 ? 4 : 8) : 0;   // routing waves
     const int kind = nrw / 4;                        // 0, 1, 2
     const void* fn = nrw == 8 ? reinterpret_cast<const void*>(gemm1_rstream_dispatch_kernel<8>)
@@ -759,15 +760,15 @@ bool launch_gemm1_dispatch(const RouteIn& rin, int* topk_ids, float* topk_w, int
     if (nrw == 8)
         launch_kernel(gemm1_rstream_dispatch_kernel<8>, dim3(grid), dim3(512), 0, stream, rin,
                       topk_ids, topk_w, T, offset, hidden, hs_scale, w1, s1, meta, tiles,
-                      sorted_tok, sorted_w, inv, C, wide_tag);
+                      sorted_tok, sorted_w, inv, C);
     else if (nrw == 4)
         launch_kernel(gemm1_rstream_dispatch_kernel<4>, dim3(grid), dim3(256), 0, stream, rin,
                       topk_ids, topk_w, T, offset, hidden, hs_scale, w1, s1, meta, tiles,
-                      sorted_tok, sorted_w, inv, C, wide_tag);
+                      sorted_tok, sorted_w, inv, C);
     else
         launch_kernel(gemm1_rstream_dispatch_kernel<0>, dim3(grid), dim3(256), 0, stream, rin,
                       topk_ids, topk_w, T, offset, hidden, hs_scale, w1, s1, meta, tiles,
-                      sorted_tok, sorted_w, inv, C, 1);
+                      sorted_tok, sorted_w, inv, C);
     return true;
 }
 

@@ -22,11 +22,11 @@ __device__ __forceinline__ float silu_f32(float x) {
 
 // Four SwiGLU values of row `row`, columns n0..n0+3, in the fp16 form of C with its
 // 16-column group exponent (moe_device.h): the plain fp16 rounding unless the group
-// holds a value beyond the fp16 range, which sets the flag word to wide_tag.  Every lane of the
-// wave calls it; lanes with `valid` false (rows past the tile) store nothing.
+// holds a value beyond the fp16 range, which sets the flag word *c_wide to 1 (a word in
+// global memory or in LDS).  Every lane of the wave calls it; lanes with `valid` false
+// (rows past the tile) store nothing.
 __device__ __forceinline__ void store_swiglu4(const Intermediate& C, int* __restrict__ c_wide, int row,
-                                              int n0, const v4f& g, const v4f& u, bool valid,
-                                              int wide_tag = 1) {
+                                              int n0, const v4f& g, const v4f& u, bool valid) {
     float c[4];
     float m = 0.f;
 #pragma unroll
@@ -44,7 +44,7 @@ __device__ __forceinline__ void store_swiglu4(const Intermediate& C, int* __rest
     if (!valid) return;
     store_f16x4_scaled(C.f16() + (size_t)row * kI + n0, c, e);
     if ((n0 & (kGroup16 - 1)) == 0) C.f16_exp()[(size_t)row * (kI / kGroup16) + n0 / kGroup16] = (uint8_t)e;
-    if (e) *c_wide = wide_tag;
+    if (e) *c_wide = 1;
 }
 
 // ---------------------------------------------------------------------------
@@ -88,8 +88,7 @@ __device__ __forceinline__ void gemm1_rstream_item(
     const uint8_t* __restrict__ hidden, const TokenScales& sa, const uint8_t* __restrict__ w1,
     const float* __restrict__ s1, int le, int row0, int nrows, int ng,
     const TokOf& tok_of, const Intermediate& C, int* __restrict__ c_wide,
-    uint8_t (*slot_lds)[Gemm1Stream<CB, NGRP, TL>::kSlot], v4f (*red)[2][NGRP * CB][64], int wave,
-    int wide_tag = 1) {
+    uint8_t (*slot_lds)[Gemm1Stream<CB, NGRP, TL>::kSlot], v4f (*red)[2][NGRP * CB][64], int wave) {
     constexpr int KSPLIT = 4;
     constexpr int KB = kHB / KSPLIT;                  // 14 K blocks per wave
     constexpr int NW = 4 * NGRP;                      // weight loads per K block (8 rows each)
@@ -265,7 +264,7 @@ __device__ __forceinline__ void gemm1_rstream_item(
                     u += red[q][1][gi * CB + c][lane];
                 }
                 store_swiglu4(C, c_wide, row0 + 16 * c + r16, (ng + gi) * 16 + kq * 4, g, u,
-                              16 * c + r16 < nrows, wide_tag);
+                              16 * c + r16 < nrows);
             }
     }
     __syncthreads();

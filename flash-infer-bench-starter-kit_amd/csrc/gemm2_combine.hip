@@ -42,20 +42,23 @@ __global__ __launch_bounds__(256 * NG, 1) void gemm2_combine_kernel(
     Intermediate C, int* __restrict__ flags, const uint8_t* __restrict__ w2,
     const float* __restrict__ s2, const int4* __restrict__ tiles,
     const int* __restrict__ num_tiles, const int* __restrict__ inv,
-    const float* __restrict__ sorted_w, int T, uint16_t* __restrict__ out, int wide_tag) {
+    const float* __restrict__ sorted_w, int T, uint16_t* __restrict__ out) {
     constexpr int HF = 2, KSPLIT = 4, KB = kIB / KSPLIT, D = KB;
     constexpr int NW = KSPLIT * NG;           // waves
     constexpr int CH = 4 * NG;                // tiles per reduction round (4 per group)
     constexpr int kVmPerStep = 2 * HF + 5;    // W2 loads, C loads, block scale of one (tile, K block)
     static_assert(HF == 2, "the HF column groups of a workgroup share one W2 scale block");
-    // flags[0]: C beyond the fp16 range (GEMM1 wrote wide_tag there); flags[1]: an expert
-    // row beyond it (set to wide_tag here; nothing after this kernel reads it)
+    // flags[0]: C went beyond the fp16 range, when zero certainly not (GEMM1 sets it, and
+    // with a route kernel before it, that kernel clears it; without one a nonzero word may
+    // be stale and is checked against C's group exponents); flags[1]: an expert row went
+    // beyond the range (set here; nothing after this kernel reads it).
     __shared__ __attribute__((aligned(1024))) uint8_t slot_lds[NW][16 * HF * kBlk];
     __shared__ v4f red[KSPLIT][CH][HF][64];          // K partials of one round of tiles
     __shared__ float o_lds[kFusedRows][kFusedCols];  // expert rows (as the combine reads them)
     __shared__ int s_inv[kFusedRows];
     __shared__ float s_w[kFusedRows];
     __shared__ int4 s_tiles[64];
+    __shared__ int s_beyond[NW];                     // a wave read a nonzero group exponent
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -86,7 +89,36 @@ __global__ __launch_bounds__(256 * NG, 1) void gemm2_combine_kernel(
         }
     }
     const int nt = __builtin_amdgcn_readfirstlane(*num_tiles);
+    const int c_flag = __builtin_amdgcn_readfirstlane(flags[0]);
     __syncthreads();   // the tile list is in LDS
+
+    // A nonzero flag word is checked against C's group exponents of every row in the
+    // tiles (GEMM1 writes each one on every call): wave (grp, ks) reads bytes 32 ks ..
+    // 32 ks + 31 of rows 64 i + 32 grp + lane / 2, in 16-byte halves, so the 8 waves cover
+    // every exponent; rows past the last tile read 0.  A word the check finds stale is
+    // cleared (a workgroup that reads it cleared takes the usual path, as the check would
+    // have sent it there).
+    bool beyond = false;
+    if (c_flag != 0) {
+        static_assert(NG == 2 && kFusedRows % 64 == 0, "exponent rows: 32 per wave and load");
+        const int4 last = nt > 0 ? s_tiles[nt - 1] : int4{0, 0, 0, 0};
+        const uint32_t rows = (uint32_t)__builtin_amdgcn_readfirstlane(last.y + last.z);
+        const __amdgpu_buffer_rsrc_t rs_ex = buffer_rsrc(C.f16_exp(), rows * (kI / kGroup16));
+        uint32_t ex = 0;
+#pragma unroll
+        for (int i = 0; i < kFusedRows / 64; ++i) {
+            const uint32_t row = 64 * i + 32 * grp + (lane >> 1);
+            const v4u e = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(
+                rs_ex, row * (kI / kGroup16) + 32 * ks + 16 * (lane & 1), 0, 0));
+            ex |= e[0] | e[1] | e[2] | e[3];
+        }
+        const bool mine = __ballot(ex != 0) != 0;
+        if (lane == 0) s_beyond[wave] = mine;
+        __syncthreads();
+#pragma unroll
+        for (int w = 0; w < NW; ++w) beyond = beyond || s_beyond[w] != 0;
+        if (!beyond && tid == 0) flags[0] = 0;
+    }
 
     // tile t: local expert, first row, rows
     auto tile_of = [&](int t) {
@@ -133,7 +165,7 @@ __global__ __launch_bounds__(256 * NG, 1) void gemm2_combine_kernel(
     // reduction barriers), a group without a tile at some i only waits there
     const int imax = (nt + NG - 1) / NG;
     const int nt_g = (nt - grp + NG - 1) / NG;
-    if (__builtin_amdgcn_readfirstlane(flags[0]) != wide_tag) {
+    if (!beyond) {   // the usual path: C within the fp16 range (every group exponent 0)
         // ---- the stream of (tile, K block) steps of this wave: step 4 i + j is tile
         // grp + NG i, K block 4 ks + j, held in ring slot j
         uint8_t* slot = &slot_lds[wave][0];
@@ -228,7 +260,7 @@ __global__ __launch_bounds__(256 * NG, 1) void gemm2_combine_kernel(
             if ((i & 3) == 3 || i == imax - 1) reduce_round(CH * (i >> 2));
         }
     }
-    if (any_e) flags[1] = wide_tag;   // an expert row went beyond the fp16 range
+    if (any_e) flags[1] = 1;   // an expert row went beyond the fp16 range
     __syncthreads();             // every row in o_lds, the routing tables landed
 
     // ---- the combine of the workgroup's 32 columns: thread (token t, column pair p),
@@ -267,15 +299,14 @@ __global__ __launch_bounds__(256 * NG, 1) void gemm2_combine_kernel(
 
 // GEMM2 variant 6: the streaming GEMM2 of variant 1 (16-row tiles, fp16 C) with the
 // combine folded in, for T <= kFusedCombineMaxT; writes the bf16 output itself.  C went
-// beyond the fp16 range when the C-range flag word holds wide_tag (the value the GEMM1
-// before it writes there: 1 after a route kernel cleared the word, or the call's tag).
+// beyond the fp16 range when the C-range flag word is set and C's group exponents confirm
+// it (GEMM1 variant 9 sets the word, but no route kernel clears it before).
 bool launch_gemm2_combine(const Intermediate& C, const uint8_t* w2, const float* s2,
                           const int4* tiles, const int* num_tiles, int* meta, const int* inv,
-                          const float* sorted_w, int T, uint16_t* out, int wide_tag,
-                          hipStream_t stream) {
-    if (T <= 0 || T > kFusedCombineMaxT || wide_tag == 0) return false;
+                          const float* sorted_w, int T, uint16_t* out, hipStream_t stream) {
+    if (T <= 0 || T > kFusedCombineMaxT) return false;
     launch_kernel((gemm2_combine_kernel<2>), dim3(kH / kFusedCols), dim3(512), 0, stream, C,
-                       meta + kCWideFlag, w2, s2, tiles, num_tiles, inv, sorted_w, T, out, wide_tag);
+                  meta + kCWideFlag, w2, s2, tiles, num_tiles, inv, sorted_w, T, out);
     return true;
 }
 

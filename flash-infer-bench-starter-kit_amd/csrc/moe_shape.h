@@ -22,12 +22,11 @@ constexpr int kN1B = kN1 / kBlk;   // 32 GEMM1 output blocks
 // Words of the workspace's meta region after the 33 expert offsets [0 .. kEL]: the tile
 // count of the first list, of the second list, then two per-call flag words (cleared by
 // the route kernel): C of GEMM1 exceeds the fp16 range, an expert row of GEMM2 does.
-// Where no route kernel runs (GEMM1 variant 9 routes its tokens itself), the first word
-// is not cleared: that GEMM1 writes the call's tag (a value >= 2, different on every
-// call) there instead of 1, and its GEMM2 (variant 6) compares the word with the tag.
-// A word that holds the tag for another reason (garbage, or a HIP graph replaying one
-// call's tag after a replay whose C was wide) only sends GEMM2 down its rare path, which
-// reads C's group exponents, and GEMM1 writes every exponent on every call.
+// Where no route kernel runs (GEMM1 variant 9 routes its tokens itself), nothing clears
+// the first word: that GEMM1 sets it as the others do, and its GEMM2 (variant 6) takes
+// a zero word as C within the fp16 range and checks a nonzero one against C's group
+// exponents, which GEMM1 writes for every row on every call (a stale word only costs
+// the check; the GEMM2 clears a word the check finds stale).
 constexpr int kCWideFlag = kEL + 3;
 constexpr int kRowsWideFlag = kEL + 4;
 constexpr int kGroup16 = 16;       // columns per fp16-form exponent byte

@@ -130,8 +130,9 @@ typedef struct moe_mi355_args {
  *                                  with the routing computed inside it too (T <= 8, the
  *                                  default there; pairs with GEMM2 variant 6 only):
  *                                  bit-identical output and workspace routing, one launch
- *                                  fewer; it marks C beyond the fp16 range with a per-call
- *                                  tag instead of clearing the flag word.
+ *                                  fewer.  No kernel clears the C-range flag word (meta[35])
+ *                                  before it, so GEMM2 variant 6 checks a set word against
+ *                                  C's group exponents (and clears a stale one).
  *   MOE_MI355_FLAG_ROW_SCALES_ON / _OFF  GEMM1 reads the token scales gathered into row
  *                                  order / straight by token (default: gathered from
  *                                  T = 512, except under GEMM1 variants 7 and 8, which gather

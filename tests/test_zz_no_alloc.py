@@ -54,8 +54,8 @@ def test_noalloc_rejects_sizes_beyond_its_maximum():
 @pytest.mark.gpu
 def test_noalloc_matches_forward_on_consecutive_calls():
     """T = 256 (the maximum), then smaller calls on the same array (37 tokens with
-    another expert offset, then 5, then 3, where GEMM1 routes the tokens itself and marks
-    the array's flag word with its call tag): each output is bit-identical to
+    another expert offset, then 5, then 3, where GEMM1 routes the tokens itself and no
+    kernel clears the C-range flag word): each output is bit-identical to
     moe_mi355_forward's with a fresh workspace, and the call allocates no memory
     through torch."""
     from gpu_common import config_inputs, first_tokens, note
