@@ -110,6 +110,13 @@ constexpr int32_t kRowScalesMinT = 512;
 // T = 1400 .. 3500 the ranked order was 4-24 us faster on 17 of 21 (GEMM1 ~180-270 us)
 // and at most 6 us slower; at T = 4096 (skewed), 5000 and 8192 it was 4-19 us slower.
 constexpr int32_t kRankedMaxT = 3500;
+
+// GEMM2 computes the combine itself (variant 6, after GEMM1 variant 5) up to T =
+// kFusedCombinePlanMaxT, though it can up to kFusedCombineMaxT: measured against GEMM2
+// variant 1 and the combine launch (wall time per call, three runs each), it is 0.6-3.2 us
+// faster at T = 12 .. 20 and 0.3-0.9 us slower at T = 24 .. 32, where each of its 224
+// workgroups walks the more tiles of the call that variant 1 spreads over all CUs.
+constexpr int32_t kFusedCombinePlanMaxT = 22;
 constexpr int32_t kKnownFlags = MOE_MI355_FLAG_PROFILE | MOE_MI355_FLAG_FORCE_PLAN |
                                 MOE_MI355_FLAG_ROW_SCALES_ON | MOE_MI355_FLAG_ROW_SCALES_OFF |
                                 MOE_MI355_FLAG_LIST_ORDER | (0xff << 8);
@@ -124,7 +131,7 @@ inline int plan_for(int32_t T, int32_t flags, Plan* p) {
     // GEMM1 with the dispatch folded in reads the token scales by token: asking for the
     // gathered ones selects the separate dispatch there
     if (T <= kRouteInGemm1MaxT && !on) g1 = 9, g2 = 6;   // T <= 8
-    else if (T <= kFusedCombineMaxT && !on) g1 = 5, g2 = 6;
+    else if (T <= kFusedCombinePlanMaxT && !on) g1 = 5, g2 = 6;
     else if (T <= kDispatchInGemm1MaxT && !on) g1 = 5, g2 = 1;
     else if (T <= 88) g1 = 1, g2 = 1;
     else if (T <= 199) g1 = 2, g2 = 3;

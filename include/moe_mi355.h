@@ -125,7 +125,7 @@ typedef struct moe_mi355_args {
  *                                  with GEMM2 variants 1 and 6): bit-identical output,
  *                                  one launch fewer.  GEMM2 variant 6 is variant 1 with
  *                                  the combine computed inside it (T <= 32, the default
- *                                  there, after GEMM1 variant 5, 1 or 9): bit-identical
+ *                                  up to T = 22, after GEMM1 variant 5, 1 or 9): bit-identical
  *                                  output, one launch fewer.  GEMM1 variant 9 is variant 5
  *                                  with the routing computed inside it too (T <= 8, the
  *                                  default there; pairs with GEMM2 variant 6 only):

@@ -22,7 +22,7 @@ static int g_fail = 0;
         }                                                                      \
     } while (0)
 
-static const int32_t kTs[] = {INT32_MIN, -1, 0, 1, 2, 4, 5, 8, 9, 16, 32, 33, 63, 64, 65, 88, 89, 199, 200,
+static const int32_t kTs[] = {INT32_MIN, -1, 0, 1, 2, 4, 5, 8, 9, 16, 22, 23, 32, 33, 63, 64, 65, 88, 89, 199, 200,
                               299, 300, 511, 559, 560,
                               512, 960, 961, 1024, 1344, 1345, 3500, 3501, 8192,
                               (1 << 19) - 1, 1 << 19, (1 << 19) + 1, INT32_MAX};

@@ -239,8 +239,11 @@ def test_layout_reports_the_forced_plan():
     lib = k._build_extension()
     assert lib.moe_mi355_get_workspace_layout(65, k.plan_flags(5, 1), ctypes.byref(lay)) == -7
     assert lib.moe_mi355_get_workspace_layout(8, k.plan_flags(5, 3), ctypes.byref(lay)) == -7
-    # GEMM2 writes the output itself (variant 6) up to T = 32, after GEMM1 variant 5 or 1
-    assert [k.workspace_layout(t).combine_in_gemm2 for t in (1, 8, 32, 33, 64, 200)] == [1, 1, 1, 0, 0, 0]
+    # GEMM2 writes the output itself (variant 6) by default up to T = 22, when forced up to
+    # T = 32, after GEMM1 variant 9, 5 or 1
+    assert [k.workspace_layout(t).combine_in_gemm2 for t in (1, 8, 22, 23, 32, 33, 64, 200)] == \
+        [1, 1, 1, 0, 0, 0, 0, 0]
+    assert k.workspace_layout(32, k.plan_flags(5, 6)).combine_in_gemm2 == 1
     assert k.workspace_layout(8, k.plan_flags(5, 1)).combine_in_gemm2 == 0
     assert k.workspace_layout(8, k.plan_flags(1, 6)).combine_in_gemm2 == 1
     assert k.workspace_layout(8, k.plan_flags(1, 6)).dispatch_in_gemm1 == 0

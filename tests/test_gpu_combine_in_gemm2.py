@@ -1,4 +1,5 @@
-"""GEMM2 with the combine folded in (GEMM2 variant 6, the plan for T <= 32): a workgroup
+"""GEMM2 with the combine folded in (GEMM2 variant 6, for T <= 32; the default plan up to
+T = 22): a workgroup
 owns 32 output columns of every row tile, keeps the call's expert rows for them in LDS
 and writes the bf16 output itself.  Its output must be bit-identical to the streaming
 GEMM2 followed by the combine launch (variant 1), with the dispatch folded into GEMM1
@@ -40,8 +41,9 @@ def test_matches_separate_combine_bit_for_bit(T, offset):
     k = pkg("kernel")
     d = first_tokens(config_inputs(3), T)
     d["local_expert_offset"] = offset
-    lay = k.workspace_layout(T)
+    lay = k.workspace_layout(T, k.plan_flags(5, 6))
     assert lay.combine_in_gemm2 == 1 and lay.dispatch_in_gemm1 == 1
+    assert k.workspace_layout(T).combine_in_gemm2 == (1 if T <= 22 else 0)
     note(f"[gpu] combine in GEMM2 T={T} offset={offset}")
     fused = run_forward(d, flags=k.plan_flags(5, 6))
     separate = run_forward(d, flags=k.plan_flags(5, 1))

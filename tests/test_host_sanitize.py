@@ -62,8 +62,8 @@ def test_host_logic_default_plans(drivers):
         f = plans[T].split()
         return int(f[4]), int(f[6])
     assert g(1) == (9, 6) and g(4) == (9, 6) and g(5) == (9, 6) and g(8) == (9, 6)
-    assert g(9) == (5, 6) and g(32) == (5, 6)
-    assert g(33) == (5, 1) and g(64) == (5, 1)
+    assert g(9) == (5, 6) and g(22) == (5, 6)
+    assert g(23) == (5, 1) and g(32) == (5, 1) and g(33) == (5, 1) and g(64) == (5, 1)
     assert g(65) == (1, 1) and g(88) == (1, 1)
     assert g(89) == (2, 3) and g(199) == (2, 3)
     assert g(200) == (8, 7) and g(559) == (8, 7)
