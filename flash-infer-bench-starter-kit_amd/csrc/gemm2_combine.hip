@@ -59,6 +59,7 @@ __global__ __launch_bounds__(256 * NG, 1) void gemm2_combine_kernel(
     __shared__ float s_w[kFusedRows];
     __shared__ int4 s_tiles[64];
     __shared__ int s_beyond[NW];                     // a wave read a nonzero group exponent
+    __shared__ int s_flag;                           // flags[0] as this workgroup read it
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -89,8 +90,14 @@ __global__ __launch_bounds__(256 * NG, 1) void gemm2_combine_kernel(
         }
     }
     const int nt = __builtin_amdgcn_readfirstlane(*num_tiles);
-    const int c_flag = __builtin_amdgcn_readfirstlane(flags[0]);
-    __syncthreads();   // the tile list is in LDS
+    // flags[0] is read once for the workgroup: another workgroup may clear it (below)
+    // between two waves' reads, and the waves must all take the same branch (barriers)
+    if (wave == 0) {
+        const int f = __builtin_amdgcn_readfirstlane(flags[0]);
+        if (lane == 0) s_flag = f;
+    }
+    __syncthreads();   // the tile list and the flag word are in LDS
+    const int c_flag = __builtin_amdgcn_readfirstlane(s_flag);
 
     // A nonzero flag word is checked against C's group exponents of every row in the
     // tiles (GEMM1 writes each one on every call): wave (grp, ks) reads bytes 32 ks ..
