@@ -286,7 +286,8 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(WPE)))
 // and the dispatch's dependent load of the routing ids go away.  Nothing clears the
 // C-range flag word before this kernel: it sets the word when C goes beyond the fp16
 // range, and the GEMM2 after it (variant 6) checks a nonzero word against C's group
-// exponents (a stale word from earlier calls or other data sends it nowhere else).
+// exponents (a stale nonzero word left by earlier calls or other data only costs that check,
+// and the GEMM2 clears it).
 constexpr int kDG1MaxTiles = dispatch_max_tiles(kDispatchInGemm1MaxT, 16);   // 64
 
 template <int NRW>
